@@ -1,0 +1,130 @@
+/* espalier.h -- C ABI of the MI355X (gfx950) trellis kernel layer, libespalier_hip.so.
+ *
+ * One entry point per function of the reference's extension module `espalier_ext`
+ * (vllm_espalier/csrc/experts.cpp:234-248), with the same argument order and meaning, as plain pointers and sizes:
+ *   - tensors become device pointers plus the sizes the reference reads from them;
+ *   - the stream is the caller's hipStream_t (the reference launches on the current stream);
+ *   - every launch is asynchronous and nothing here allocates or synchronises, so calls are legal under graph
+ *     capture. The caller owns every buffer.
+ * Errors: a call returns ESP_OK (0) or an ESP_ERR_* code, and esp_last_error() holds a message. The reference
+ * raises these as TORCH_CHECK failures (RuntimeError in Python); the torch binding raises the same.
+ * dtype codes: ESP_F16 0, ESP_BF16 1, ESP_F32 2.
+ * Codebook ids are the kernels' (1 mcg, 3 E2M1, 6 int5, 7 int6), K2 = 2 * bits; the supported (cb, K2) pairs are
+ * mcg at K2 2..16 (even), E2M1 at 2, 4, 6, int5 at 4, 6, 8, int6 at 6, 8, 10 (experts_grouped.cuh:227-229).
+ */
+#ifndef ESPALIER_H
+#define ESPALIER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ESP_OK 0
+#define ESP_ERR_ARG 1          /* a shape, size, limit or layout check failed */
+#define ESP_ERR_UNSUPPORTED 2  /* no kernel for this codebook / width / tile setting */
+#define ESP_ERR_HIP 3          /* the HIP runtime reported an error */
+
+#define ESP_F16 0
+#define ESP_BF16 1
+#define ESP_F32 2
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* esp_last_error(void);
+
+/* ABI version (incremented on any signature change). */
+int esp_abi_version(void);
+
+/* Replaces `had` (experts.cpp:226-232, dense.cu:242-265, 342-351): y = fp16(H(x * pre) / sqrt(128) * post) along rows
+ * of 128. x, y fp16 [M][K] (y may alias x); pre / post fp16 [K] or NULL. K % 128 == 0. */
+int esp_had(const void* x, const void* pre, const void* post, void* y, int64_t M, int64_t K, void* stream);
+
+/* Replaces `dequant` (experts.cpp:68-77, experts_grouped.cuh:321-340, 379-387): out fp16 [K][N] = the decoded
+ * weight of a trellis int16 [K/16][N/16][8 * k2]. */
+int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2, int64_t cb, void* stream);
+
+/* Replaces `dense` (experts.cpp:193-211, dense.cu:273-340): for each of n_shards (1..4) matrices sharing x,
+ * y[:, col0[s] : col0[s] + n_cols[s]] = H(H(x * suh_s) @ W_s) * svh_s, M <= 32 rows.
+ * x [M][x_stride] (x_dtype), trellis[s] int16 [K/16][n_cols[s]/16][8*k2], suh[s] fp16 [K], svh[s] fp16 [n_cols[s]],
+ * y [M][y_stride] (y_dtype) with y_cols columns. Scratch: xh fp16 (xh_numel halves; n_shards*M*K used when the input
+ * rotation is not fused), Z fp32 (z_numel; SK*M*sum(n_cols) used when SK > 1), counters int32 (counters_numel;
+ * 2 * sum(n_cols)/128 used, zero on entry and left zero). SK K splits; W, PF tile hints; the input rotation is fused
+ * when M * (K / SK) * 2 <= rot_smem bytes. */
+int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+              const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
+              const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh, int64_t xh_numel,
+              float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK,
+              int64_t W, int64_t PF, int64_t rot_smem, void* stream);
+
+/* Replaces `route_group` (experts.cpp:214-223, route.cu:35-207): router logits x @ gate^T (+ the shared gate), top-k
+ * by the exactly rounded bf16 logits (lowest id on ties), weights renormalised over the picks, the shared slot's
+ * weight sigmoid(x . sgate), then the grouping of the picks. x [R][x_stride] and gate [E][H] in one dtype (bf16 or
+ * fp16); sgate [H] or NULL (needed when shared_id >= 0). logits fp32 scratch (logits_numel >= R * (E + has));
+ * counter int32 [1] zero on entry and left zero; pick_out int32 / wts_out fp32 [R * (k + has)]; uids int32 [maxu];
+ * ucount int32 [1]; members int32 [maxu][maxm]. Limits: E <= 256, k <= 16, H % 256 == 0, R * (k + has) <= 1056. */
+int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
+                    const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
+                    int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount,
+                    int32_t* members, int64_t maxm, void* stream);
+
+/* Replaces `group_shared` (experts.cpp:154-172, experts.cu:247-330, 518-539): pick/weight tables with the shared
+ * expert as slot slots_in (weight sigmoid(x . gate_w), fp32), then the grouping. pick_in int32 / wts_in fp32
+ * [R][slots_in]; x [R][x_stride] with H columns; gate_w [H] (x's dtype) or NULL; pick_out / wts_out [R * slots]. */
+int esp_group_shared(const int32_t* pick_in, const float* wts_in, const void* x, int x_dtype, int64_t x_stride,
+                     int64_t H, const void* gate_w, int64_t shared_id, int32_t* pick_out, float* wts_out,
+                     int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm, int64_t R,
+                     int64_t slots_in, int64_t E, void* stream);
+
+/* Replaces `group` (experts.cpp:79-90, experts.cu:23-76, 435-455): distinct picks in [0, E) in id order (uids,
+ * ucount) and their members row * 32 + slot in pick order, -1 padded to maxm. */
+int esp_group(const int32_t* pick, int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm,
+              int64_t R, int64_t slots, int64_t E, void* stream);
+
+/* Replaces `rot_in` (experts.cpp:92-104, experts.cu:97-115, 457-475): out0/out1 fp16 [rows*slots][K] =
+ * fp16(H(x[row] * suh0/1[pick]) / sqrt(128)) for every valid pick (0 <= pick < E); x bf16/fp16 [rows][x_stride];
+ * suh0/1 fp16 [E][K]. */
+int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const int32_t* pick, const void* suh0, const void* suh1,
+               void* out0, void* out1, int64_t rows, int64_t K, int64_t slots, int64_t E, void* stream);
+
+/* Replaces `grouped` (experts.cpp:44-66, experts_grouped.cuh:237-318, 360-377): Z fp32 [mats][SK][P][N] = the K-split
+ * partial sums of X_mat[row] @ W_mat[e] for every member row of every distinct expert u < ucount. X0/X1 fp16 [P][K];
+ * TP0/TP1 int64 [E] trellis device pointers; B0/B1 int32 [E] K2; C0/C1 int32 [E] codebook ids; uids [nexp_max];
+ * members [nexp_max][maxm]. nt, warps, pf are tile hints; lo/hi bound the K2 of the launch's experts. */
+int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
+                const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
+                const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int64_t mats,
+                int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t nt, int64_t warps, int64_t pf,
+                int64_t lo, int64_t hi, void* stream);
+
+/* Replaces `gateup_epilogue` (experts.cpp:106-118, experts.cu:120-162, 477-487): per valid pick p, the gate / up
+ * splits of Z [2][SK][P][N] summed in order, H, * svh, SwiGLU (act_mode 1: fp32; 0: bf16 roundings; clamped to
+ * limit), * suh_d, H -> xd fp16 [P][N]. svh_g/svh_u/suh_d fp16 [E][N]. */
+int esp_gateup_epilogue(const float* Z, const int32_t* pick, const void* svh_g, const void* svh_u, const void* suh_d,
+                        void* xd, int64_t rows, int64_t P, int64_t N, int64_t SK, int64_t slots, int64_t E,
+                        double limit, int64_t act_mode, void* stream);
+
+/* Replaces `down_epilogue` (experts.cpp:120-129, experts.cu:165-184): y fp32 [P][D] = H(sum of Z [SK][P][D]) *
+ * svh_d[pick] / sqrt(128) for every valid pick. */
+int esp_down_epilogue(const float* Z, const int32_t* pick, const void* svh_d, float* y, int64_t rows, int64_t P,
+                      int64_t D, int64_t SK, int64_t slots, int64_t E, void* stream);
+
+/* Replaces `combine` (experts.cpp:131-137, experts.cu:187-195): out fp32 [rows][D] = sum over slots in order of
+ * wts * y (fp32 fma chain from 0). */
+int esp_combine(const float* y, const float* wts, float* out, int64_t rows, int64_t D, int64_t slots, void* stream);
+
+/* Replaces `down_combine` (experts.cpp:139-151, experts.cu:198-241): down_epilogue then combine over all slots,
+ * fp32 out [rows][D]; an invalid pick reuses y's stored row. */
+int esp_down_combine(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts, float* out,
+                     int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E, void* stream);
+
+/* Replaces `down_combine2` (experts.cpp:175-190, experts.cu:340-393, 541-559): as down_combine, the routed sum over
+ * the first n_routed slots into out, and w * y of slot n_routed into out_shared (may be NULL), both in out_dtype. */
+int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts, void* out,
+                      int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots,
+                      int64_t E, int64_t n_routed, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,298 @@
+// espalier_ext: the torch extension module of the plugin, a thin layer over the C ABI in libespalier_hip.so.
+//
+// The 13 functions, their positional arguments and their checks are those of the reference module
+// (vllm_espalier/csrc/experts.cpp:39-248): tensors are checked here (device, dtype, contiguity, sizes) and passed to
+// the esp_* entry points as pointers and sizes, on the current stream of the tensor's device. A failing check or call
+// raises RuntimeError (c10::Error), as TORCH_CHECK does in the reference.
+#include <torch/extension.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <vector>
+
+#include "../../../include/espalier.h"
+
+namespace {
+
+void check(const at::Tensor& x, at::ScalarType t, const char* name) {
+    TORCH_CHECK(x.is_cuda() && x.scalar_type() == t && x.is_contiguous(), name,
+                ": expected a contiguous CUDA tensor of the right dtype");
+}
+
+void* cur_stream() { return (void*)c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
+
+int dtype_code(const at::Tensor& t) {
+    return t.scalar_type() == at::kFloat ? ESP_F32 : t.scalar_type() == at::kBFloat16 ? ESP_BF16 : ESP_F16;
+}
+
+void call(int rc) { TORCH_CHECK(rc == ESP_OK, esp_last_error()); }
+
+template <typename T>
+const T* cptr(const at::Tensor& t) { return reinterpret_cast<const T*>(t.data_ptr()); }
+template <typename T>
+T* mptr(const at::Tensor& t) { return reinterpret_cast<T*>(t.data_ptr()); }
+
+}  // namespace
+
+void grouped(const at::Tensor& X0, const at::Tensor& X1, const at::Tensor& TP0, const at::Tensor& TP1,
+             const at::Tensor& B0, const at::Tensor& B1, const at::Tensor& C0, const at::Tensor& C1,
+             const at::Tensor& uids, const at::Tensor& ucount, const at::Tensor& members, at::Tensor Z, int64_t mats,
+             int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t nt, int64_t warps, int64_t pf,
+             int64_t lo, int64_t hi) {
+    check(X0, at::kHalf, "X0");
+    check(X1, at::kHalf, "X1");
+    check(TP0, at::kLong, "TP0");
+    check(TP1, at::kLong, "TP1");
+    check(B0, at::kInt, "B0");
+    check(B1, at::kInt, "B1");
+    check(C0, at::kInt, "C0");
+    check(C1, at::kInt, "C1");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    check(Z, at::kFloat, "Z");
+    TORCH_CHECK(Z.numel() >= mats * SK * P * N, "Z too small");
+    TORCH_CHECK(X0.numel() >= P * K && X1.numel() >= P * K, "X too small");
+    TORCH_CHECK(members.dim() == 2 && members.size(0) >= uids.numel(), "members: [nexp_max, maxm]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(X0.device());
+    call(esp_grouped(X0.data_ptr(), X1.data_ptr(), cptr<int64_t>(TP0), cptr<int64_t>(TP1), cptr<int32_t>(B0),
+                     cptr<int32_t>(B1), cptr<int32_t>(C0), cptr<int32_t>(C1), cptr<int32_t>(uids), uids.numel(),
+                     cptr<int32_t>(ucount), cptr<int32_t>(members), members.size(1), mptr<float>(Z), Z.numel(), mats,
+                     K, N, P, SK, slots, nt, warps, pf, lo, hi, cur_stream()));
+}
+
+void dequant(const at::Tensor& T, at::Tensor out, int64_t k2, int64_t cb) {
+    TORCH_CHECK(T.is_cuda() && T.scalar_type() == at::kShort && T.is_contiguous() && T.dim() == 3,
+                "T: int16 [K/16, N/16, 8 * k2]");
+    TORCH_CHECK(T.size(2) == 8 * k2, "trellis last dim must be 8 * k2");
+    check(out, at::kHalf, "out");
+    const int64_t K = T.size(0) * 16, N = T.size(1) * 16;
+    TORCH_CHECK(out.numel() == K * N, "out must be [K, N]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(T.device());
+    call(esp_dequant(T.data_ptr(), out.data_ptr(), K, N, k2, cb, cur_stream()));
+}
+
+void group(const at::Tensor& pick, at::Tensor uids, at::Tensor ucount, at::Tensor members, int64_t R, int64_t slots,
+           int64_t E) {
+    check(pick, at::kInt, "pick");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    TORCH_CHECK(pick.numel() >= R * slots, "pick too small");
+    TORCH_CHECK(uids.numel() >= std::min<int64_t>(R * slots, E), "uids too small");
+    TORCH_CHECK(members.size(0) >= uids.numel() && members.size(1) >= 1, "members too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(pick.device());
+    call(esp_group(cptr<int32_t>(pick), mptr<int32_t>(uids), uids.numel(), mptr<int32_t>(ucount),
+                   mptr<int32_t>(members), members.size(1), R, slots, E, cur_stream()));
+}
+
+void rot_in(const at::Tensor& x, int64_t x_stride, const at::Tensor& pick, const at::Tensor& suh0,
+            const at::Tensor& suh1, at::Tensor out0, at::Tensor out1, int64_t rows, int64_t K, int64_t slots,
+            int64_t E) {
+    TORCH_CHECK(x.is_cuda() && (x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf),
+                "x: bf16/fp16 CUDA");
+    check(pick, at::kInt, "pick");
+    check(suh0, at::kHalf, "suh0");
+    check(suh1, at::kHalf, "suh1");
+    check(out0, at::kHalf, "out0");
+    check(out1, at::kHalf, "out1");
+    TORCH_CHECK(K % 128 == 0, "K must be a multiple of 128");
+    TORCH_CHECK(pick.numel() >= rows * slots, "pick too small");
+    TORCH_CHECK(out0.numel() >= rows * slots * K && out1.numel() >= rows * slots * K, "out too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_rot_in(x.data_ptr(), dtype_code(x), x_stride, cptr<int32_t>(pick), suh0.data_ptr(), suh1.data_ptr(),
+                    out0.data_ptr(), out1.data_ptr(), rows, K, slots, E, cur_stream()));
+}
+
+void gateup_epilogue(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_g, const at::Tensor& svh_u,
+                     const at::Tensor& suh_d, at::Tensor xd, int64_t rows, int64_t P, int64_t N, int64_t SK,
+                     int64_t slots, int64_t E, double limit, int64_t act_mode) {
+    check(Z, at::kFloat, "Z");
+    check(pick, at::kInt, "pick");
+    check(svh_g, at::kHalf, "svh_g");
+    check(svh_u, at::kHalf, "svh_u");
+    check(suh_d, at::kHalf, "suh_d");
+    check(xd, at::kHalf, "xd");
+    TORCH_CHECK(N % 128 == 0, "N must be a multiple of 128");
+    TORCH_CHECK(Z.numel() >= 2 * SK * P * N && xd.numel() >= rows * slots * N, "Z / xd too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(Z.device());
+    call(esp_gateup_epilogue(cptr<float>(Z), cptr<int32_t>(pick), svh_g.data_ptr(), svh_u.data_ptr(),
+                             suh_d.data_ptr(), xd.data_ptr(), rows, P, N, SK, slots, E, limit, act_mode,
+                             cur_stream()));
+}
+
+void down_epilogue(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_d, at::Tensor y, int64_t rows,
+                   int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E) {
+    check(Z, at::kFloat, "Z");
+    check(pick, at::kInt, "pick");
+    check(svh_d, at::kHalf, "svh_d");
+    check(y, at::kFloat, "y");
+    TORCH_CHECK(D % 128 == 0, "D must be a multiple of 128");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(Z.device());
+    call(esp_down_epilogue(cptr<float>(Z), cptr<int32_t>(pick), svh_d.data_ptr(), mptr<float>(y), rows, P, D, SK,
+                           slots, E, cur_stream()));
+}
+
+void combine(const at::Tensor& y, const at::Tensor& wts, at::Tensor out, int64_t rows, int64_t D, int64_t slots) {
+    check(y, at::kFloat, "y");
+    check(wts, at::kFloat, "wts");
+    check(out, at::kFloat, "out");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(y.device());
+    call(esp_combine(cptr<float>(y), cptr<float>(wts), mptr<float>(out), rows, D, slots, cur_stream()));
+}
+
+void down_combine(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_d, at::Tensor y,
+                  const at::Tensor& wts, at::Tensor out, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots,
+                  int64_t E) {
+    check(Z, at::kFloat, "Z");
+    check(pick, at::kInt, "pick");
+    check(svh_d, at::kHalf, "svh_d");
+    check(y, at::kFloat, "y");
+    check(wts, at::kFloat, "wts");
+    check(out, at::kFloat, "out");
+    TORCH_CHECK(D % 128 == 0, "D must be a multiple of 128");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(Z.device());
+    call(esp_down_combine(cptr<float>(Z), cptr<int32_t>(pick), svh_d.data_ptr(), mptr<float>(y), cptr<float>(wts),
+                          mptr<float>(out), rows, P, D, SK, slots, E, cur_stream()));
+}
+
+void group_shared(const at::Tensor& pick_in, const at::Tensor& wts_in, const at::Tensor& x, int64_t x_stride,
+                  const c10::optional<at::Tensor>& gate_w, int64_t shared_id, at::Tensor pick_out, at::Tensor wts_out,
+                  at::Tensor uids, at::Tensor ucount, at::Tensor members, int64_t R, int64_t slots_in, int64_t E) {
+    check(pick_in, at::kInt, "pick_in");
+    check(wts_in, at::kFloat, "wts_in");
+    check(pick_out, at::kInt, "pick_out");
+    check(wts_out, at::kFloat, "wts_out");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    TORCH_CHECK(x.is_cuda() && (x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf),
+                "x: bf16/fp16 CUDA");
+    if (gate_w.has_value())
+        TORCH_CHECK(gate_w->scalar_type() == x.scalar_type() && gate_w->is_contiguous() && gate_w->numel() == x.size(1),
+                    "gate_w: x's dtype, [H]");
+    TORCH_CHECK(shared_id < 0 || gate_w.has_value(), "a shared slot needs its gate weight");
+    TORCH_CHECK(members.dim() == 2, "members: [nexp_max, maxm]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_group_shared(cptr<int32_t>(pick_in), cptr<float>(wts_in), x.data_ptr(), dtype_code(x), x_stride,
+                          x.size(1), gate_w.has_value() ? gate_w->data_ptr() : nullptr, shared_id,
+                          mptr<int32_t>(pick_out), mptr<float>(wts_out), mptr<int32_t>(uids), uids.numel(),
+                          mptr<int32_t>(ucount), mptr<int32_t>(members), members.size(1), R, slots_in, E,
+                          cur_stream()));
+}
+
+void down_combine2(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_d, at::Tensor y,
+                   const at::Tensor& wts, at::Tensor out, const c10::optional<at::Tensor>& out_shared, int64_t rows,
+                   int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E, int64_t n_routed) {
+    check(Z, at::kFloat, "Z");
+    check(pick, at::kInt, "pick");
+    check(svh_d, at::kHalf, "svh_d");
+    check(y, at::kFloat, "y");
+    check(wts, at::kFloat, "wts");
+    TORCH_CHECK(out.is_cuda() && out.is_contiguous(), "out: contiguous CUDA");
+    TORCH_CHECK(out.scalar_type() == at::kBFloat16 || out.scalar_type() == at::kHalf ||
+                    out.scalar_type() == at::kFloat,
+                "out: bf16, fp16 or fp32");
+    if (out_shared.has_value())
+        TORCH_CHECK(out_shared->scalar_type() == out.scalar_type() && out_shared->is_contiguous(),
+                    "out_shared: out's dtype");
+    TORCH_CHECK(D % 128 == 0, "D must be a multiple of 128");
+    TORCH_CHECK(n_routed <= slots, "n_routed <= slots");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(Z.device());
+    call(esp_down_combine2(cptr<float>(Z), cptr<int32_t>(pick), svh_d.data_ptr(), mptr<float>(y), cptr<float>(wts),
+                           out.data_ptr(), dtype_code(out), out_shared.has_value() ? out_shared->data_ptr() : nullptr,
+                           rows, P, D, SK, slots, E, n_routed, cur_stream()));
+}
+
+void dense(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
+           const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y, at::Tensor xh,
+           at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+           int64_t rot_smem) {
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1, "x: CUDA [M, K], unit column stride");
+    TORCH_CHECK(y.is_cuda() && y.dim() == 2 && y.stride(1) == 1, "y: CUDA [M, N], unit column stride");
+    TORCH_CHECK(T.size() == suh.size() && T.size() == svh.size() && T.size() == col0.size(), "one entry a matrix");
+    TORCH_CHECK(T.size() >= 1 && T.size() <= 4, "1 to 4 matrices a launch");
+    const int64_t M = x.size(0), K = x.size(1);
+    std::vector<const void*> tp, sp, vp;
+    std::vector<int64_t> ncols;
+    for (size_t s = 0; s < T.size(); ++s) {
+        TORCH_CHECK(T[s].is_cuda() && T[s].scalar_type() == at::kShort && T[s].is_contiguous() && T[s].dim() == 3,
+                    "trellis: contiguous int16 [K/16, N/16, 16K]");
+        check(suh[s], at::kHalf, "suh");
+        check(svh[s], at::kHalf, "svh");
+        TORCH_CHECK(col0[s] + svh[s].numel() <= y.size(1), "matrix columns past y");
+        TORCH_CHECK(T[s].size(0) * 16 == K && T[s].size(1) * 16 == svh[s].numel() && T[s].size(2) == 8 * k2,
+                    "matrix shape");
+        TORCH_CHECK(suh[s].numel() == K, "suh must have K elements");
+        tp.push_back(T[s].data_ptr());
+        sp.push_back(suh[s].data_ptr());
+        vp.push_back(svh[s].data_ptr());
+        ncols.push_back(svh[s].numel());
+    }
+    check(Z, at::kFloat, "Z");
+    check(counters, at::kInt, "counters");
+    TORCH_CHECK(xh.scalar_type() == at::kHalf, "xh: fp16 scratch");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_dense(x.data_ptr(), dtype_code(x), x.stride(0), M, K, (int64_t)T.size(), tp.data(), sp.data(), vp.data(),
+                   ncols.data(), col0.data(), y.data_ptr(), dtype_code(y), y.stride(0), y.size(1), xh.data_ptr(),
+                   xh.numel(), mptr<float>(Z), Z.numel(), mptr<int32_t>(counters), counters.numel(), k2, cb, SK, W, PF,
+                   rot_smem, cur_stream()));
+}
+
+void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
+                 int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out, at::Tensor wts_out,
+                 at::Tensor uids, at::Tensor ucount, at::Tensor members) {
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1 && gate.is_contiguous(), "x / gate layout");
+    TORCH_CHECK(gate.scalar_type() == x.scalar_type(), "gate and x must share a dtype");
+    TORCH_CHECK(x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf, "x: bf16/fp16");
+    check(logits, at::kFloat, "logits");
+    check(counter, at::kInt, "counter");
+    check(pick_out, at::kInt, "pick_out");
+    check(wts_out, at::kFloat, "wts_out");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    TORCH_CHECK(members.dim() == 2, "members: [nexp_max, maxm]");
+    TORCH_CHECK(gate.dim() == 2 && gate.size(1) == x.size(1), "gate: [E, H]");
+    if (sgate.has_value())
+        TORCH_CHECK(sgate->scalar_type() == x.scalar_type() && sgate->is_contiguous() && sgate->numel() == x.size(1),
+                    "sgate: x's dtype, [H]");
+    const int64_t R = x.size(0), H = x.size(1), E = gate.size(0);
+    const int64_t slots = k + (shared_id >= 0);
+    TORCH_CHECK(pick_out.numel() >= R * slots && wts_out.numel() >= R * slots, "pick / wts too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_route_group(x.data_ptr(), dtype_code(x), x.stride(0), R, H, gate.data_ptr(), E,
+                         sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits),
+                         logits.numel(), mptr<int32_t>(counter), mptr<int32_t>(pick_out), mptr<float>(wts_out),
+                         mptr<int32_t>(uids), uids.numel(), mptr<int32_t>(ucount), mptr<int32_t>(members),
+                         members.size(1), cur_stream()));
+}
+
+void had(const at::Tensor& x, const c10::optional<at::Tensor>& pre, const c10::optional<at::Tensor>& post,
+         at::Tensor y) {
+    check(x, at::kHalf, "x");
+    check(y, at::kHalf, "y");
+    TORCH_CHECK(x.dim() == 2 && y.numel() == x.numel(), "had: x [M, K], y the same size");
+    const int64_t M = x.size(0), K = x.size(1);
+    if (pre.has_value()) check(*pre, at::kHalf, "pre");
+    if (post.has_value()) check(*post, at::kHalf, "post");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_had(x.data_ptr(), pre.has_value() ? pre->data_ptr() : nullptr,
+                 post.has_value() ? post->data_ptr() : nullptr, y.data_ptr(), M, K, cur_stream()));
+}
+
+PYBIND11_MODULE(espalier_ext, m) {
+    m.def("had", &had);
+    m.def("route_group", &route_group);
+    m.def("dense", &dense);
+    m.def("group_shared", &group_shared);
+    m.def("down_combine2", &down_combine2);
+    m.def("grouped", &grouped);
+    m.def("dequant", &dequant);
+    m.def("group", &group);
+    m.def("rot_in", &rot_in);
+    m.def("gateup_epilogue", &gateup_epilogue);
+    m.def("down_epilogue", &down_epilogue);
+    m.def("combine", &combine);
+    m.def("down_combine", &down_combine);
+}

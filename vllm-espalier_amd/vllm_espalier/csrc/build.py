@@ -1,0 +1,102 @@
+"""Build the gfx950 kernel layer in-tree with hipcc (no hipify, no JIT cache):
+
+  libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, moe.hip, abi.cpp)
+  espalier_ext*.so     the torch extension module (binding.cpp, host code only), linked to libespalier_hip.so
+
+Both land in the vllm_espalier package directory. Usage: python build.py [--jobs N] [--only lib|ext]
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PKG = CSRC.parent
+REPO = PKG.parent.parent
+BUILD = CSRC / "_build"
+ARCH = os.environ.get("ESPALIER_OFFLOAD_ARCH", "gfx950")
+LIB = PKG / "libespalier_hip.so"
+
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and Path(c).exists():
+            return c
+    raise RuntimeError("hipcc not found: the gfx950 kernels need ROCm's hipcc")
+
+
+def run(cmd: list[str]) -> None:
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    # the host pass does not know the packed-fp32 feature; that warning is expected
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in (p.stderr or "").splitlines() if noise not in l)
+    if p.returncode != 0:
+        raise RuntimeError(f"command failed ({p.returncode}): {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def ext_suffix() -> str:
+    return sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+
+
+def build_lib(jobs: int) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    cc = hipcc()
+    srcs = [CSRC / "dense.hip", CSRC / "moe.hip", CSRC / "abi.cpp"]
+    objs = [BUILD / (s.stem + ".o") for s in srcs]
+
+    def compile_one(pair):
+        s, o = pair
+        lang = ["-x", "hip"] if s.suffix == ".hip" else []
+        run([cc, *HIP_FLAGS, *lang, "-c", str(s), "-o", str(o)])
+
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(compile_one, zip(srcs, objs)))
+    tmp = LIB.with_suffix(".so.tmp")
+    run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_ext() -> Path:
+    import torch.utils.cpp_extension as ce
+    import torch
+    cc = hipcc()
+    out = PKG / ("espalier_ext" + ext_suffix())
+    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    libdirs = [f"-L{p}" for p in ce.library_paths()]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [cc, "-O2", "-std=c++17", "-fPIC", "-shared", str(CSRC / "binding.cpp"), *inc,
+           "-DTORCH_EXTENSION_NAME=espalier_ext", "-DTORCH_API_INCLUDE_EXTENSION_H", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-Wno-unused-result", "-Wno-deprecated-declarations",
+           *libdirs, f"-L{PKG}", "-lespalier_hip", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-ltorch_python", "-Wl,-rpath,$ORIGIN", "-o", str(out) + ".tmp"]
+    run(cmd)
+    os.replace(str(out) + ".tmp", out)
+    return out
+
+
+def build(jobs: int = 4, only: str | None = None) -> None:
+    if only in (None, "lib"):
+        build_lib(jobs)
+    if only in (None, "ext"):
+        build_ext()
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--only", choices=["lib", "ext"])
+    a = ap.parse_args()
+    build(a.jobs, a.only)

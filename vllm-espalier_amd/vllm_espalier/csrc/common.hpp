@@ -1,0 +1,131 @@
+// Shared device helpers of the gfx950 kernel layer: fp16/bf16 conversions, wave64 lane exchanges, the 128-point
+// Walsh-Hadamard transform, and the C-ABI error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace esp {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 1 / sqrt(128), the reference's constant (dense.cu:23, experts.cu:17)
+constexpr float HAD_SCALE = 0.08838834764831845f;
+
+enum DType : int { F16 = 0, BF16 = 1, F32 = 2 };
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }   // RNE
+__device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {                                                      // RNE
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// one element of a 16-bit (f16 / bf16) or f32 array as f32
+__device__ __forceinline__ float load_elem(const void* p, int dtype, size_t i) {
+    if (dtype == F32) return static_cast<const float*>(p)[i];
+    const uint16_t h = static_cast<const uint16_t*>(p)[i];
+    return dtype == BF16 ? bf2f(h) : h2f(h);
+}
+
+// four consecutive elements starting at i (i a multiple of 4)
+__device__ __forceinline__ void load4(const void* p, int dtype, size_t i, float (&v)[4]) {
+    if (dtype == F32) {
+        const float4 u = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        const uint16_t h[4] = {(uint16_t)(u.x & 0xFFFFu), (uint16_t)(u.x >> 16), (uint16_t)(u.y & 0xFFFFu),
+                               (uint16_t)(u.y >> 16)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = dtype == BF16 ? bf2f(h[j]) : h2f(h[j]);
+    }
+}
+
+__device__ __forceinline__ void store4(void* p, int dtype, size_t i, const float (&v)[4]) {
+    if (dtype == F32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = dtype == BF16 ? f2bf(v[j]) : f2h(v[j]);
+        uint2 u;
+        u.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        u.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = u;
+    }
+}
+
+// lane ^ M inside each 32-lane half of the wave: quad DPP for 1 and 2, ds_swizzle's bitmask mode above
+template <int M>
+__device__ __forceinline__ float xor_lane32(float v) {
+    int i = __builtin_bit_cast(int, v);
+    if constexpr (M == 1)
+        i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);     // quad_perm [1,0,3,2]
+    else if constexpr (M == 2)
+        i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);     // quad_perm [2,3,0,1]
+    else
+        i = __builtin_amdgcn_ds_swizzle(i, (M << 10) | 0x1F);             // and 0x1F, or 0, xor M
+    return __builtin_bit_cast(float, i);
+}
+
+template <int M>
+__device__ __forceinline__ void fwht_stage(float (&v)[4], int lane32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float o = xor_lane32<M>(v[j]);
+        v[j] = (lane32 & M) ? o - v[j] : v[j] + o;
+    }
+}
+
+// Walsh-Hadamard transform of 128 fp32 values held 4 a lane by 32 lanes (lane l: elements 4l..4l+3). Strides 1 and 2
+// in registers, then 4..64 across lanes; the lower element of each pair takes a + b, the upper a - b. The stage order
+// is the reference's (experts.cu:79-90), so the fp32 results are the same bits.
+__device__ __forceinline__ void fwht128(float (&v)[4], int lane32) {
+    const float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];
+    v[0] = a + c; v[1] = b + d; v[2] = a - c; v[3] = b - d;
+    fwht_stage<1>(v, lane32);
+    fwht_stage<2>(v, lane32);
+    fwht_stage<4>(v, lane32);
+    fwht_stage<8>(v, lane32);
+    fwht_stage<16>(v, lane32);
+}
+
+// fp16 H(x * suh) / sqrt(128) of the 128 values of x starting at xi (dtype), 4 a lane of a 32-lane half; the multiply
+// is never contracted into the butterfly (dense.cu:92-108)
+__device__ __forceinline__ uint2 rot128(const void* x, int x_dtype, size_t xi, const uint16_t* suh, int lane32) {
+    float v[4];
+    load4(x, x_dtype, xi + 4 * lane32, v);
+    const uint2 su = *reinterpret_cast<const uint2*>(suh + 4 * lane32);
+    v[0] = __fmul_rn(v[0], h2f((uint16_t)(su.x & 0xFFFFu)));
+    v[1] = __fmul_rn(v[1], h2f((uint16_t)(su.x >> 16)));
+    v[2] = __fmul_rn(v[2], h2f((uint16_t)(su.y & 0xFFFFu)));
+    v[3] = __fmul_rn(v[3], h2f((uint16_t)(su.y >> 16)));
+    fwht128(v, lane32);
+    uint2 u;
+    u.x = (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
+    u.y = (uint32_t)f2h(v[2] * HAD_SCALE) | ((uint32_t)f2h(v[3] * HAD_SCALE) << 16);
+    return u;
+}
+
+}  // namespace esp
+
+// ---- C-ABI error plumbing (host) ----
+namespace esp_host {
+const char* last_error();
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int ok();
+int launch_check(const char* what);
+}  // namespace esp_host
+
+#define ESP_REQUIRE(cond, ...)                                                                  \
+    do {                                                                                        \
+        if (!(cond)) return esp_host::fail(ESP_ERR_ARG, __VA_ARGS__);                           \
+    } while (0)

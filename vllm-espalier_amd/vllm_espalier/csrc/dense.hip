@@ -1,0 +1,435 @@
+// Dense trellis layers for decode (1-32 rows) on gfx950, plus the trellis dequantisation and the standalone Hadamard.
+//
+// esp_dense: every matrix of one layer (<= 4 sharing the input and the codebook) in one launch, y_s = H(H(x * suh_s)
+// @ W_s) * svh_s written into each matrix's columns of y (dense.cu:1-9, 273-340 define the contract).
+//
+// Work split. A workgroup is 4 waves on one 128-column block (the output Hadamard's width) and one K range (K / SK);
+// wave w owns the block's n tiles 2w, 2w+1 over the whole K range, so no partial sums are exchanged between waves.
+// Per 32-k step a wave decodes 2 B operands (trellis -> fp16 in registers, trellis.hpp) and issues one
+// v_mfma_f32_16x16x32_f16 per B operand and 16-row group (rows 0-15, 16-31): weights stream from HBM once for all
+// rows. Split K (SK > 1) goes through Z, and the last workgroup of a column block to arrive (atomic counter) adds the
+// splits in order and finishes; counters are left zero.
+//
+// Row invariance: a row's sums depend only on that row (MFMA keeps rows apart), the K split and per-wave ranges
+// depend on the shape alone, and splits are added in a fixed order.
+#include "common.hpp"
+#include "trellis.hpp"
+#include "../../../include/espalier.h"
+
+namespace esp {
+
+constexpr int MAX_SHARDS = 4;
+
+struct Shard {
+    const uint32_t* T;       // trellis words [K/16][N/16][4*K2]
+    const uint16_t* suh;     // [K]
+    const uint16_t* svh;     // [N]
+    int nb0, nb, col0;       // first 128-column block in the launch, blocks, first output column
+    float scale;             // grid step c when the int5 / int6 index is decoded, else 1
+};
+
+struct DenseArgs {
+    Shard s[MAX_SHARDS];
+    int n;
+    const void* x;
+    int x_dtype, x_stride;
+    const uint16_t* xh;      // unfused input rotation: fp16 [n][M][K]
+    void* y;
+    int y_dtype, y_stride;
+    float* Z;
+    int* counters;
+    int M, K, SK, NBT, fused, xs_stride;
+};
+
+// ------------------------------------------------------------------------------------------------------------------
+// dequant: out fp16 [K][N]. A wave decodes one 32k x 16n block (two k tiles of one n tile) with the MFMA lane decode
+// (the same code the GEMMs run) and scatters its 8 values a lane.
+// ------------------------------------------------------------------------------------------------------------------
+template <int CB, int K2>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ T, uint16_t* __restrict__ out,
+                                                      int K, int N) {
+    constexpr int TW = 4 * K2;
+    const int lane = threadIdx.x & 63;
+    const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);   // (k pair, n tile)
+    const int NT = N >> 4, KP = (K >> 5);
+    const int kp = blk / NT, nt = blk % NT;
+    if (kp >= KP) return;
+    const int c = lane & 15, G = lane >> 4;
+    const int kt = 2 * kp + (G >> 1);
+    const LanePlan<K2> lp(lane);
+    uint32_t w[6];
+    load_words<K2>(T + ((size_t)kt * NT + nt) * TW, lp, w);
+    const u32x4 b = decode_words<CB, K2>(w, lp);
+    const int col = nt * 16 + c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int row = kt * 16 + slot_k(G, i);
+        out[(size_t)row * N + col] = slot_bits(b, i);
+    }
+}
+
+// K a multiple of 16 but not of 32: the last k tile pairs with nothing, handled by this single-tile variant
+template <int CB, int K2>
+__global__ __launch_bounds__(256) void dequant_tail_kernel(const uint32_t* __restrict__ T, uint16_t* __restrict__ out,
+                                                           int K, int N) {
+    constexpr int TW = 4 * K2;
+    const int lane = threadIdx.x & 63;
+    const int nt = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int NT = N >> 4;
+    if (nt >= NT) return;
+    const int c = lane & 15, G = lane >> 4;
+    if (G >= 2) return;                                      // only the lanes of the first k tile
+    const int kt = (K >> 4) - 1;
+    const LanePlan<K2> lp(lane);
+    uint32_t w[6];
+    load_words<K2>(T + ((size_t)kt * NT + nt) * TW, lp, w);
+    const u32x4 b = decode_words<CB, K2>(w, lp);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[(size_t)(kt * 16 + slot_k(G, i)) * N + nt * 16 + c] = slot_bits(b, i);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// had: y = fp16(H(x * pre) / sqrt(128) * post) (dense.cu:242-265). A wave takes two 128-blocks, one per 32-lane half.
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void had_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre,
+                                                  const uint16_t* __restrict__ post, uint16_t* __restrict__ y, int M,
+                                                  int K) {
+    const int l32 = threadIdx.x & 31;
+    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int nb = K >> 7;
+    if (unit >= (long)M * nb) return;
+    const int row = (int)(unit / nb), blk = (int)(unit % nb);
+    const size_t i = (size_t)row * K + blk * 128 + 4 * l32;
+    float v[4];
+    load4(x, F16, i, v);
+    if (pre) {
+        float s[4];
+        load4(pre, F16, blk * 128 + 4 * l32, s);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(v[j], s[j]);
+    }
+    fwht128(v, l32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] *= HAD_SCALE;
+    if (post) {
+        float s[4];
+        load4(post, F16, blk * 128 + 4 * l32, s);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] *= s[j];
+    }
+    store4(y, F16, i, v);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// dense: unfused input rotation xh[s][row][k] = fp16(H(x * suh_s) / sqrt(128)) (dense.cu:110-117)
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dense_rot_kernel(DenseArgs a, uint16_t* __restrict__ xh) {
+    const int l32 = threadIdx.x & 31;
+    const int nb = a.K >> 7;
+    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);   // (shard, row, block)
+    if (unit >= (long)a.n * a.M * nb) return;
+    const int blk = (int)(unit % nb);
+    const int row = (int)((unit / nb) % a.M);
+    const int s = (int)(unit / ((long)nb * a.M));
+    const uint2 u = rot128(a.x, a.x_dtype, (size_t)row * a.x_stride + blk * 128, a.s[s].suh + blk * 128, l32);
+    *reinterpret_cast<uint2*>(xh + ((size_t)s * a.M + row) * a.K + blk * 128 + 4 * l32) = u;
+}
+
+// the finished outputs of one row's 128 columns from their fp32 sums, 4 a lane: H / sqrt(128), * c, * svh
+// (dense.cu:120-128)
+__device__ __forceinline__ void finish(float (&v)[4], int l32, const uint16_t* svh, float scale) {
+    fwht128(v, l32);
+    const uint2 sv = *reinterpret_cast<const uint2*>(svh + 4 * l32);
+    const float s[4] = {h2f((uint16_t)(sv.x & 0xFFFFu)), h2f((uint16_t)(sv.x >> 16)), h2f((uint16_t)(sv.y & 0xFFFFu)),
+                        h2f((uint16_t)(sv.y >> 16))};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] *= scale;
+        v[j] *= HAD_SCALE * s[j];
+    }
+}
+
+template <int CB, int K2, int MG>
+__global__ __launch_bounds__(256) void dense_kernel(DenseArgs a) {
+    constexpr int TW = 4 * K2;
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int last;
+    const int nbg = blockIdx.x, split = blockIdx.y;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_SHARDS; ++i)
+        if (i < a.n && nbg >= a.s[i].nb0) si = i;
+    const Shard S = a.s[si];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int c = lane & 15, G = lane >> 4;
+    const int NTILES = S.nb * 8;
+    const int cb_local = nbg - S.nb0;                       // column block inside the matrix
+    const int kr = a.K / a.SK, k0 = split * kr;
+    const int M = a.M;
+
+    // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    const uint16_t* X;
+    int xstride, xk0;
+    if (a.fused) {
+        const int chunks = kr >> 7;
+        for (int idx = wave * 2 + half; idx < M * chunks; idx += 8) {
+            const int r = idx / chunks, ch = idx % chunks;
+            const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + k0 + ch * 128, S.suh + k0 + ch * 128, l32);
+            *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) = u;
+        }
+        __syncthreads();
+        X = xs;
+        xstride = a.xs_stride;
+        xk0 = k0;
+    } else {
+        X = a.xh + (size_t)si * M * a.K;
+        xstride = a.K;
+        xk0 = 0;
+    }
+
+    // 2. the K loop: 2 B operands (n tiles) a step, words of the next step in flight
+    const LanePlan<K2> lp(lane);
+    const int nt_w = cb_local * 8 + 2 * wave;
+    const uint32_t* Tw = S.T + (size_t)nt_w * TW;
+    const size_t kstride = (size_t)NTILES * TW;              // words between consecutive k tiles
+    const int kt_base = (k0 >> 4) + (G >> 1);
+    const int steps = kr >> 5;
+
+    f32x4 acc[2][MG];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // A operand rows of this lane: c and 16 + c
+    bool rok[MG];
+    const uint16_t* xr[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+        const int row = g * 16 + c;
+        rok[g] = row < M;
+        xr[g] = X + (size_t)(rok[g] ? row : 0) * xstride + 16 * (G >> 1) + 4 * (G & 1) - xk0;
+    }
+
+    uint32_t wc[2][6], wn[2][6];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_words<K2>(Tw + (size_t)kt_base * kstride + j * TW, lp, wc[j]);
+
+    for (int st = 0; st < steps; ++st) {
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                load_words<K2>(Tw + (size_t)(kt_base + 2 * (st + 1)) * kstride + j * TW, lp, wn[j]);
+        }
+        const int k = k0 + 32 * st;
+        f16x8 av[MG];
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
+            if (rok[g]) {
+                lo = *reinterpret_cast<const uint2*>(xr[g] + k);
+                hi = *reinterpret_cast<const uint2*>(xr[g] + k + 8);
+            }
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 t = {lo.x, lo.y, hi.x, hi.y};
+            av[g] = __builtin_bit_cast(f16x8, t);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f16x8 b = decode_b<CB, K2>(wc[j], lp);
+#pragma unroll
+            for (int g = 0; g < MG; ++g) acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
+        }
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 6; ++i) wc[j][i] = wn[j][i];
+        }
+    }
+
+    // 3. the block's [M][128] sums in shared memory (the rotated rows are no longer read)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = g * 16 + 4 * G + i;
+                if (row < M) red[row * 128 + 32 * wave + 16 * j + c] = acc[j][g][i];
+            }
+    __syncthreads();
+
+    const uint16_t* svh = S.svh + cb_local * 128;
+    const int ycol = S.col0 + cb_local * 128 + 4 * l32;
+    if (a.SK == 1) {
+        for (int r = wave * 2 + half; r < M; r += 8) {
+            float v[4] = {red[r * 128 + 4 * l32], red[r * 128 + 4 * l32 + 1], red[r * 128 + 4 * l32 + 2],
+                          red[r * 128 + 4 * l32 + 3]};
+            finish(v, l32, svh, S.scale);
+            store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
+        }
+        return;
+    }
+    const size_t zrow = (size_t)a.NBT * 128;
+    for (int r = wave * 2 + half; r < M; r += 8) {
+        const float4 v = make_float4(red[r * 128 + 4 * l32], red[r * 128 + 4 * l32 + 1], red[r * 128 + 4 * l32 + 2],
+                                     red[r * 128 + 4 * l32 + 3]);
+        *reinterpret_cast<float4*>(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32) = v;
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.counters + nbg, 1) == a.SK - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int r = wave * 2 + half; r < M; r += 8) {
+        const size_t at = (size_t)r * zrow + nbg * 128 + 4 * l32;
+        float4 s = *reinterpret_cast<const float4*>(a.Z + at);
+        for (int q = 1; q < a.SK; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(a.Z + (size_t)q * M * zrow + at);
+            s.x += u.x; s.y += u.y; s.z += u.z; s.w += u.w;
+        }
+        float v[4] = {s.x, s.y, s.z, s.w};
+        finish(v, l32, svh, S.scale);
+        store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
+    }
+    if (threadIdx.x == 0) a.counters[nbg] = 0;             // every split of the block arrived
+}
+
+template <int KCB, int K2, int MG>
+static int launch_dense(const DenseArgs& a, dim3 grid, size_t smem, hipStream_t st) {
+    auto kern = dense_kernel<KCB, K2, MG>;
+    if (smem > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "dense: cannot raise the shared memory limit to %zu bytes", smem);
+    kern<<<grid, 256, smem, st>>>(a);
+    return ESP_OK;
+}
+
+}  // namespace esp
+
+// ======================================================================================================================
+// C ABI
+// ======================================================================================================================
+using namespace esp;
+
+extern "C" int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2, int64_t cb,
+                           void* stream) {
+    ESP_REQUIRE(trellis && out, "dequant: null pointer");
+    ESP_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 16 == 0, "dequant: K and N must be positive multiples of 16");
+    if (!supported((int)cb, (int)k2))
+        return esp_host::fail(ESP_ERR_UNSUPPORTED, "no instance for codebook %lld K2 %lld", (long long)cb,
+                              (long long)k2);
+    hipStream_t s = (hipStream_t)stream;
+    const long blocks = (K / 32) * (N / 16);
+    const unsigned grid = (unsigned)((blocks + 3) / 4);
+    const bool tail = (K % 32) != 0;
+    const unsigned tgrid = (unsigned)((N / 16 + 3) / 4);
+    auto T = static_cast<const uint32_t*>(trellis);
+    auto o = static_cast<uint16_t*>(out);
+    switch (cb * 32 + k2) {
+#define ESP_DQ(CB_, K2_)                                                                                   \
+    case CB_ * 32 + K2_:                                                                                   \
+        if (grid) dequant_kernel<CB_, K2_><<<grid, 256, 0, s>>>(T, o, (int)K, (int)N);                     \
+        if (tail) dequant_tail_kernel<CB_, K2_><<<tgrid, 256, 0, s>>>(T, o, (int)K, (int)N);               \
+        break;
+        ESP_CASES(ESP_DQ)
+#undef ESP_DQ
+    }
+    return esp_host::launch_check("dequant");
+}
+
+extern "C" int esp_had(const void* x, const void* pre, const void* post, void* y, int64_t M, int64_t K,
+                       void* stream) {
+    ESP_REQUIRE(x && y, "had: null pointer");
+    ESP_REQUIRE(K % 128 == 0, "had: K must be a multiple of 128");
+    if (M <= 0 || K <= 0) return esp_host::ok();
+    const long units = M * (K / 128);
+    had_kernel<<<(unsigned)((units + 7) / 8), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(pre), static_cast<const uint16_t*>(post),
+        static_cast<uint16_t*>(y), (int)M, (int)K);
+    return esp_host::launch_check("had");
+}
+
+extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                         const void* const* trellis, const void* const* suh, const void* const* svh,
+                         const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                         int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters,
+                         int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+                         int64_t rot_smem, void* stream) {
+    (void)W;
+    (void)PF;
+    ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "1 to 4 matrices a launch");
+    ESP_REQUIRE(M >= 1 && M <= 32, "1 to 32 rows");
+    ESP_REQUIRE(SK >= 1 && K > 0 && K % (128 * SK) == 0 && (K / SK) % 32 == 0,
+                "K must split evenly over SK in 128s");
+    ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "x / y dtype");
+    ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "x / y row stride");
+    if (!supported((int)cb, (int)k2))
+        return esp_host::fail(ESP_ERR_UNSUPPORTED, "unsupported codebook/width: cb=%lld k2=%lld", (long long)cb,
+                              (long long)k2);
+    DenseArgs a{};
+    int nbt = 0;
+    const float c = (cb == 6 || cb == 7) ? grid_c((int)cb) : 1.0f;
+    for (int s = 0; s < n_shards; ++s) {
+        const int64_t N = n_cols[s];
+        ESP_REQUIRE(N > 0 && N % 128 == 0, "matrix shape");
+        ESP_REQUIRE(col0[s] >= 0 && col0[s] + N <= y_cols, "matrix columns past y");
+        ESP_REQUIRE(trellis[s] && suh[s] && svh[s], "dense: null matrix pointer");
+        a.s[s] = Shard{static_cast<const uint32_t*>(trellis[s]), static_cast<const uint16_t*>(suh[s]),
+                       static_cast<const uint16_t*>(svh[s]), nbt, (int)(N / 128), (int)col0[s], c};
+        nbt += (int)(N / 128);
+    }
+    a.n = (int)n_shards;
+    ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= nbt),
+                "scratch too small");
+    const int64_t kr = K / SK;
+    const int xs_stride = (int)kr + 8;                        // pad rows across the LDS banks
+    const bool fused = M * kr * 2 <= rot_smem;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.x_stride = (int)x_stride;
+    a.xh = static_cast<const uint16_t*>(xh);
+    a.y = y;
+    a.y_dtype = y_dtype;
+    a.y_stride = (int)y_stride;
+    a.Z = Z;
+    a.counters = counters;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.SK = (int)SK;
+    a.NBT = nbt;
+    a.fused = fused;
+    a.xs_stride = xs_stride;
+    hipStream_t st = (hipStream_t)stream;
+    if (!fused) {
+        ESP_REQUIRE(xh && xh_numel >= n_shards * M * K, "xh too small");
+        const long units = n_shards * M * (K / 128);
+        dense_rot_kernel<<<(unsigned)((units + 7) / 8), 256, 0, st>>>(a, static_cast<uint16_t*>(xh));
+        int rc = esp_host::launch_check("dense rotation");
+        if (rc) return rc;
+    }
+    const size_t smem_x = fused ? (size_t)M * xs_stride * 2 : 0;
+    const size_t smem_red = (size_t)M * 128 * 4;
+    const size_t smem = smem_x > smem_red ? smem_x : smem_red;
+    ESP_REQUIRE(smem <= 160 * 1024, "dense: shared memory for the fused rotation exceeds 160 KiB");
+    dim3 grid((unsigned)nbt, (unsigned)SK);
+    const int mg = M > 16 ? 2 : 1;
+    int rc = ESP_OK;
+    switch (cb * 32 + k2) {
+#define ESP_DENSE_CASE(CB_, K2_)                                                                           \
+    case CB_ * 32 + K2_: {                                                                                 \
+        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                       \
+        rc = mg == 1 ? launch_dense<KCB, K2_, 1>(a, grid, smem, st) : launch_dense<KCB, K2_, 2>(a, grid, smem, st); \
+        break;                                                                                             \
+    }
+        ESP_CASES(ESP_DENSE_CASE)
+#undef ESP_DENSE_CASE
+    }
+    if (rc) return rc;
+    return esp_host::launch_check("dense");
+}

@@ -1,0 +1,849 @@
+// Routed + shared expert pipeline on gfx950: fused routing (router GEMV + top-k + grouping), grouping, input rotation,
+// the grouped trellis GEMM over the distinct experts, and the epilogues (experts.cu, route.cu, experts_grouped.cuh
+// define the contract).
+//
+// Grouping: distinct picks in id order, each with its member rows (code row * 32 + slot) in pick order, -1 padded.
+// When every expert appears at most once a row (top-k picks are distinct) and R <= 32, a row bitmask per expert gives
+// each member's rank as a popcount; otherwise each expert scans the picks in order.
+#include "common.hpp"
+#include "trellis.hpp"
+#include "../../../include/espalier.h"
+
+namespace esp {
+
+constexpr int GT = 256;                 // threads of the grouping / routing tail blocks
+constexpr int MAX_PICKS = 32 * 33;      // R * slots limit of the routing window (route.cu:191)
+constexpr int MAX_GROUP_IDS = 4096;     // ids the grouping covers (experts.cu:437)
+
+// ------------------------------------------------------------------------------------------------------------------
+// block-level grouping of sh_pick[0..n) (shared memory) over ids [0, nid)
+// ------------------------------------------------------------------------------------------------------------------
+struct GroupSmem {
+    int cnt[MAX_GROUP_IDS];
+    unsigned mask[MAX_GROUP_IDS];
+    int place[MAX_GROUP_IDS];
+    int wave_tot[GT / 64];
+    int dup;
+};
+
+__device__ void group_block(const int* sh_pick, int n, int R, int slots, int nid, int maxm, int* __restrict__ uids,
+                            int* __restrict__ ucount, int* __restrict__ members, GroupSmem& g) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < nid; e += GT) {
+        g.cnt[e] = 0;
+        g.mask[e] = 0u;
+    }
+    if (tid == 0) g.dup = R > 32;
+    __syncthreads();
+    for (int i = tid; i < n; i += GT) {
+        const int e = sh_pick[i];
+        if (e >= 0 && e < nid) {
+            atomicAdd(&g.cnt[e], 1);
+            if (R <= 32) atomicOr(&g.mask[e], 1u << (i / slots));
+        }
+    }
+    __syncthreads();
+    // exclusive scan of used[e] in id order: each thread a contiguous id range
+    const int per = (nid + GT - 1) / GT;
+    const int e0 = tid * per;
+    int used = 0;
+    for (int e = e0; e < e0 + per && e < nid; ++e) {
+        used += g.cnt[e] > 0;
+        if (R <= 32 && g.cnt[e] != __builtin_popcount(g.mask[e])) g.dup = 1;   // an id twice in a row
+    }
+    int inc = used;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+    }
+    if (lane == 63) g.wave_tot[wave] = inc;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += g.wave_tot[w];
+    int place = base + inc - used;
+    for (int e = e0; e < e0 + per && e < nid; ++e) {
+        if (g.cnt[e] > 0) {
+            g.place[e] = place;
+            uids[place] = e;
+            ++place;
+        } else {
+            g.place[e] = -1;
+        }
+    }
+    if (tid == GT - 1) *ucount = place;
+    __syncthreads();
+    if (!g.dup) {
+        // at most once a row: a member's rank is the number of earlier rows holding the same id
+        for (int i = tid; i < n; i += GT) {
+            const int e = sh_pick[i];
+            if (e < 0 || e >= nid) continue;
+            const int r = i / slots;
+            const int rank = __builtin_popcount(g.mask[e] & ((1u << r) - 1u));
+            if (rank < maxm) members[g.place[e] * maxm + rank] = r * 32 + (i % slots);
+        }
+        for (int e = tid; e < nid; e += GT) {
+            if (g.place[e] < 0) continue;
+            for (int m = g.cnt[e]; m < maxm; ++m) members[g.place[e] * maxm + m] = -1;
+        }
+    } else {
+        for (int e = tid; e < nid; e += GT) {
+            if (g.place[e] < 0) continue;
+            int j = 0;
+            for (int i = 0; i < n && j < maxm; ++i)
+                if (sh_pick[i] == e) members[g.place[e] * maxm + j++] = (i / slots) * 32 + (i % slots);
+            for (; j < maxm; ++j) members[g.place[e] * maxm + j] = -1;
+        }
+    }
+}
+
+__global__ __launch_bounds__(GT) void group_kernel(const int* __restrict__ pick, int* __restrict__ uids,
+                                                   int* __restrict__ ucount, int* __restrict__ members, int R,
+                                                   int slots, int E, int maxm) {
+    __shared__ int sh_pick[MAX_PICKS];
+    __shared__ GroupSmem g;
+    const int n = R * slots;
+    for (int i = threadIdx.x; i < n; i += GT) sh_pick[i] = pick[i];
+    __syncthreads();
+    group_block(sh_pick, n, R, slots, E, maxm, uids, ucount, members, g);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// fp64 dot products of bf16 / fp16 rows: a bf16 x bf16 product is exact in fp64 and the accumulation order is fixed
+// (lane-strided chunks of 4, then a fixed butterfly), so a row's value never depends on the other rows.
+// ------------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ void load4_16(const uint16_t* p, int bf16, double (&v)[4]) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    const uint16_t h[4] = {(uint16_t)(u.x & 0xFFFFu), (uint16_t)(u.x >> 16), (uint16_t)(u.y & 0xFFFFu),
+                           (uint16_t)(u.y >> 16)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (double)(bf16 ? bf2f(h[j]) : h2f(h[j]));
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// bf16 bits of a double, one rounding (to nearest, ties to even)
+__device__ __forceinline__ uint16_t f64_to_bf16(double d) {
+    const uint64_t x = __builtin_bit_cast(uint64_t, d);
+    const uint32_t sign = (uint32_t)(x >> 48) & 0x8000u;
+    const uint64_t ax = x & 0x7FFFFFFFFFFFFFFFull;
+    if (ax > 0x7FF0000000000000ull) return (uint16_t)(sign | 0x7FC0u);
+    const int e = (int)(ax >> 52);
+    if (e == 0) return (uint16_t)sign;
+    int E = e - 1023 + 127;
+    if (E >= 255) return (uint16_t)(sign | 0x7F80u);
+    const uint64_t m = (ax & ((1ull << 52) - 1)) | (1ull << 52);
+    const int shift = E >= 1 ? 45 : 45 + (1 - E);
+    if (shift > 54) return (uint16_t)sign;
+    uint64_t q = m >> shift;
+    const uint64_t rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q += 1;
+    uint32_t bits;
+    if (E >= 1) {
+        if (q == 256) {
+            q = 128;
+            E += 1;
+            if (E >= 255) return (uint16_t)(sign | 0x7F80u);
+        }
+        bits = ((uint32_t)E << 7) | (uint32_t)(q & 0x7Fu);
+    } else {
+        bits = (uint32_t)q;
+    }
+    return (uint16_t)(sign | bits);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// route_group (route.cu:35-181): every wave computes router logits (4 rows x 4 columns a wave tile, fp64), the last
+// block to arrive does top-k / weights / shared gate per row (one wave a row) and the grouping.
+// ------------------------------------------------------------------------------------------------------------------
+struct RouteArgs {
+    const uint16_t* x;
+    const uint16_t* gate;
+    const uint16_t* sgate;
+    float* logits;
+    int* counter;
+    int* pick_out;
+    float* wts_out;
+    int* uids;
+    int* ucount;
+    int* members;
+    int x_stride, bf16, R, H, E, k, shared_id, maxm;
+};
+
+constexpr int RT_ROWS = 4, RT_COLS = 4;
+
+__global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
+    __shared__ int last;
+    __shared__ int sh_pick[MAX_PICKS];
+    __shared__ GroupSmem g;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int has = a.shared_id >= 0, C = a.E + has, slots = a.k + has;
+    const int rtiles = (a.R + RT_ROWS - 1) / RT_ROWS, ctiles = (C + RT_COLS - 1) / RT_COLS;
+
+    // 1. logits
+    for (int t = blockIdx.x * (GT / 64) + wave; t < rtiles * ctiles; t += gridDim.x * (GT / 64)) {
+        const int r0 = (t / ctiles) * RT_ROWS, c0 = (t % ctiles) * RT_COLS;
+        double acc[RT_ROWS][RT_COLS];
+#pragma unroll
+        for (int i = 0; i < RT_ROWS; ++i)
+#pragma unroll
+            for (int j = 0; j < RT_COLS; ++j) acc[i][j] = 0.0;
+        for (int h = 4 * lane; h < a.H; h += 256) {
+            double xv[RT_ROWS][4], wv[RT_COLS][4];
+#pragma unroll
+            for (int i = 0; i < RT_ROWS; ++i) {
+                const int r = r0 + i < a.R ? r0 + i : a.R - 1;
+                load4_16(a.x + (size_t)r * a.x_stride + h, a.bf16, xv[i]);
+            }
+#pragma unroll
+            for (int j = 0; j < RT_COLS; ++j) {
+                const int cc = c0 + j < C ? c0 + j : C - 1;
+                const uint16_t* w = cc < a.E ? a.gate + (size_t)cc * a.H : a.sgate;
+                load4_16(w + h, a.bf16, wv[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < RT_ROWS; ++i)
+#pragma unroll
+                for (int j = 0; j < RT_COLS; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[i][j] = __builtin_fma(xv[i][q], wv[j][q], acc[i][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < RT_ROWS; ++i)
+#pragma unroll
+            for (int j = 0; j < RT_COLS; ++j) {
+                const double s = wave_sum_f64(acc[i][j]);
+                const int r = r0 + i, cc = c0 + j;
+                if (lane == 0 && r < a.R && cc < C)
+                    a.logits[(size_t)r * C + cc] = cc < a.E ? bf2f(f64_to_bf16(s)) : (float)s;
+            }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+
+    // 2. per row: top-k by logit (lowest id on ties), softmax weights over the picks, the shared gate's sigmoid
+    for (int r = wave; r < a.R; r += GT / 64) {
+        const float* lr = a.logits + (size_t)r * C;
+        float l[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = lane + 64 * q;
+            l[q] = e < a.E ? __builtin_nontemporal_load(lr + e) : -INFINITY;
+        }
+        float mx = 0.f, psum = 0.f;
+        for (int t = 0; t < a.k; ++t) {
+            float bv = -INFINITY;
+            int be = 1 << 30;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = lane + 64 * q;
+                if (e < a.E && (l[q] > bv || (l[q] == bv && e < be))) {
+                    bv = l[q];
+                    be = e;
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oe = __shfl_xor(be, o, 64);
+                if (ov > bv || (ov == bv && oe < be)) {
+                    bv = ov;
+                    be = oe;
+                }
+            }
+            if (t == 0) mx = bv;
+            const float p = expf(bv - mx);
+            psum += p;
+            if (lane == 0) {
+                a.pick_out[r * slots + t] = be;
+                a.wts_out[r * slots + t] = p;                      // normalised below
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (lane + 64 * q == be) l[q] = -INFINITY;
+        }
+        if (lane == 0) {
+            for (int t = 0; t < a.k; ++t) a.wts_out[r * slots + t] = a.wts_out[r * slots + t] / psum;
+            if (has) {
+                a.pick_out[r * slots + a.k] = a.shared_id;
+                a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-__builtin_nontemporal_load(lr + a.E)));
+            }
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+
+    // 3. grouping of the picks (ids < E + has)
+    const int n = a.R * slots;
+    for (int i = tid; i < n; i += GT) sh_pick[i] = a.pick_out[i];
+    __syncthreads();
+    group_block(sh_pick, n, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    if (tid == 0) *a.counter = 0;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// group_shared (experts.cu:247-330): extended pick / weight tables with the shared slot, then the grouping
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(GT) void group_shared_kernel(const int* __restrict__ pick_in, const float* __restrict__ wts_in,
+                                                          const uint16_t* __restrict__ x, int x_stride, int bf16,
+                                                          const uint16_t* __restrict__ gate_w, int H, int shared_id,
+                                                          int* __restrict__ pick_out, float* __restrict__ wts_out,
+                                                          int* __restrict__ uids, int* __restrict__ ucount,
+                                                          int* __restrict__ members, int R, int slots_in, int E,
+                                                          int maxm) {
+    __shared__ int sh_pick[MAX_PICKS];
+    __shared__ GroupSmem g;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int has = shared_id >= 0, slots = slots_in + has, n = R * slots;
+    for (int i = tid; i < n; i += GT) {
+        const int r = i / slots, k = i % slots;
+        const int e = k < slots_in ? pick_in[r * slots_in + k] : shared_id;
+        sh_pick[i] = e;
+        pick_out[i] = e;
+        if (k < slots_in) wts_out[i] = wts_in[r * slots_in + k];
+    }
+    if (has) {
+        for (int r = wave; r < R; r += GT / 64) {
+            double acc = 0.0;
+            for (int h = 4 * lane; h < H; h += 256) {
+                double xv[4], wv[4];
+                load4_16(x + (size_t)r * x_stride + h, bf16, xv);
+                load4_16(gate_w + h, bf16, wv);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc = __builtin_fma(xv[q], wv[q], acc);
+            }
+            const double s = wave_sum_f64(acc);
+            if (lane == 0) wts_out[r * slots + slots_in] = 1.f / (1.f + expf(-(float)s));
+        }
+    }
+    __syncthreads();
+    group_block(sh_pick, n, R, slots, E, maxm, uids, ucount, members, g);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// rot_in (experts.cu:97-115): one wave per (slot row, 128-block); lanes 0-31 the gate input, 32-63 the up input
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rot_in_kernel(const uint16_t* __restrict__ x, int x_dtype, int x_stride,
+                                                     const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
+                                                     const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
+                                                     uint16_t* __restrict__ out1, int P, int K, int slots, int E) {
+    const int l32 = threadIdx.x & 31, mat = (threadIdx.x >> 5) & 1;
+    const long unit = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = K >> 7;
+    if (unit >= (long)P * nb) return;
+    const int p = (int)(unit / nb), blk = (int)(unit % nb);
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    const int row = p / slots;
+    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K + blk * 128;
+    const uint2 u = rot128(x, x_dtype, (size_t)row * x_stride + blk * 128, suh, l32);
+    *reinterpret_cast<uint2*>((mat ? out1 : out0) + (size_t)p * K + blk * 128 + 4 * l32) = u;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// grouped (experts_grouped.cuh:237-318): program (distinct expert u, 128-column block, split * mats). 4 waves, wave w
+// owns n tiles 2w, 2w+1 of the block over the split's K range; up to 32 member rows in two 16-row MFMA groups, so an
+// expert's weights stream once whatever its member count. The int5 / int6 grids are decoded as their index q and the
+// sums scaled by c before they are stored.
+// ------------------------------------------------------------------------------------------------------------------
+struct GroupedArgs {
+    const uint16_t* X0;
+    const uint16_t* X1;
+    const int64_t* TP0;
+    const int64_t* TP1;
+    const int* B0;
+    const int* B1;
+    const int* C0;
+    const int* C1;
+    const int* uids;
+    const int* ucount;
+    const int* members;
+    float* Z;
+    int K, N, P, SK, maxm, slots;
+};
+
+template <int CB, int K2, int MG>
+__device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_t* __restrict__ T,
+                                             const uint16_t* __restrict__ X, const int* rows_sh, int mat, int split,
+                                             float scale) {
+    constexpr int TW = 4 * K2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, G = lane >> 4;
+    const int NTILES = a.N >> 4;
+    const int nt_w = blockIdx.y * 8 + 2 * wave;
+    const int kr = a.K / a.SK, k0 = split * kr, steps = kr >> 5;
+    const LanePlan<K2> lp(lane);
+    const uint32_t* Tw = T + (size_t)nt_w * TW;
+    const size_t kstride = (size_t)NTILES * TW;
+    const int kt_base = (k0 >> 4) + (G >> 1);
+
+    bool rok[MG];
+    const uint16_t* xr[MG];
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+        const int p = rows_sh[g * 16 + c];
+        rok[g] = p >= 0;
+        xr[g] = X + (size_t)(p >= 0 ? p : 0) * a.K + 16 * (G >> 1) + 4 * (G & 1);
+    }
+    f32x4 acc[2][MG];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t wc[2][6], wn[2][6];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_words<K2>(Tw + (size_t)kt_base * kstride + j * TW, lp, wc[j]);
+    for (int st = 0; st < steps; ++st) {
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                load_words<K2>(Tw + (size_t)(kt_base + 2 * (st + 1)) * kstride + j * TW, lp, wn[j]);
+        }
+        const int k = k0 + 32 * st;
+        f16x8 av[MG];
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
+            if (rok[g]) {
+                lo = *reinterpret_cast<const uint2*>(xr[g] + k);
+                hi = *reinterpret_cast<const uint2*>(xr[g] + k + 8);
+            }
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 t = {lo.x, lo.y, hi.x, hi.y};
+            av[g] = __builtin_bit_cast(f16x8, t);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const f16x8 b = decode_b<CB, K2>(wc[j], lp);
+#pragma unroll
+            for (int g = 0; g < MG; ++g)
+                acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
+        }
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 6; ++i) wc[j][i] = wn[j][i];
+        }
+    }
+    float* Zm = a.Z + ((size_t)mat * a.SK + split) * a.P * a.N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = rows_sh[g * 16 + 4 * G + i];
+                if (p >= 0) Zm[(size_t)p * a.N + nt_w * 16 + 16 * j + c] = acc[j][g][i] * scale;
+            }
+}
+
+__global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
+    const int u = blockIdx.x;
+    if (u >= a.ucount[0]) return;
+    const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
+    const int e = a.uids[u];
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? a.TP1[e] : a.TP0[e]);
+    const int k2 = mat ? a.B1[e] : a.B0[e];
+    const int cb = mat ? a.C1[e] : a.C0[e];
+    const uint16_t* X = mat ? a.X1 : a.X0;
+    __shared__ int rows_sh[32];
+    __shared__ int nrows;
+    if (threadIdx.x < 32) {
+        const int m = threadIdx.x;
+        const int code = m < a.maxm ? a.members[(size_t)u * a.maxm + m] : -1;
+        rows_sh[m] = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int n = 0;
+        while (n < 32 && rows_sh[n] >= 0) ++n;
+        nrows = n;
+    }
+    __syncthreads();
+    if (nrows == 0) return;                                 // members come first: no rows
+    const bool two = nrows > 16;
+    switch (cb * 32 + k2) {
+#define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
+    case CB_ * 32 + K2_: {                                                                                    \
+        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                          \
+        const float scale = (CB_ == 6 || CB_ == 7) ? grid_c(CB_) : 1.0f;                                      \
+        if (two)                                                                                              \
+            grouped_body<KCB, K2_, 2>(a, T, X, rows_sh, mat, split, scale);                                   \
+        else                                                                                                  \
+            grouped_body<KCB, K2_, 1>(a, T, X, rows_sh, mat, split, scale);                                   \
+        break;                                                                                                \
+    }
+        ESP_CASES(ESP_GROUPED_CASE)
+#undef ESP_GROUPED_CASE
+        default:
+            break;                                          // no kernel: Z is left untouched (the host checks tables)
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// epilogues (experts.cu:117-241, 332-393); one 32-lane half per (row, 128-block) unit
+// ------------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
+
+__global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                              const uint16_t* __restrict__ svh_g,
+                                                              const uint16_t* __restrict__ svh_u,
+                                                              const uint16_t* __restrict__ suh_d,
+                                                              uint16_t* __restrict__ xd, int P, int N, int SK, int E,
+                                                              float limit, int act_mode) {
+    const int l32 = threadIdx.x & 31;
+    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int nb = N >> 7;
+    if (unit >= (long)P * nb) return;
+    const int p = (int)(unit / nb), blk = (int)(unit % nb);
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    const int n = blk * 128 + 4 * l32;
+    float gv[4], uv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float sg = 0.f, su = 0.f;
+        for (int s = 0; s < SK; ++s) {
+            sg += Z[((size_t)(0 * SK + s) * P + p) * N + n + j];
+            su += Z[((size_t)(1 * SK + s) * P + p) * N + n + j];
+        }
+        gv[j] = sg;
+        uv[j] = su;
+    }
+    fwht128(gv, l32);
+    fwht128(uv, l32);
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const size_t at = (size_t)e * N + n + j;
+        float act;
+        if (act_mode == 0) {
+            const float gg = fminf(bf16r(gv[j] * HAD_SCALE * h2f(svh_g[at])), limit);
+            const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * h2f(svh_u[at])), -limit), limit);
+            act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+        } else {
+            const float gg = fminf(gv[j] * HAD_SCALE * h2f(svh_g[at]), limit);
+            const float uu = fminf(fmaxf(uv[j] * HAD_SCALE * h2f(svh_u[at]), -limit), limit);
+            act = gg / (1.f + expf(-gg)) * uu;
+        }
+        v[j] = __fmul_rn(act, h2f(suh_d[at]));
+    }
+    fwht128(v, l32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] *= HAD_SCALE;
+    store4(xd, F16, (size_t)p * N + n, v);
+}
+
+__global__ __launch_bounds__(256) void down_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                            const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+                                                            int P, int D, int SK, int E) {
+    const int l32 = threadIdx.x & 31;
+    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int nb = D >> 7;
+    if (unit >= (long)P * nb) return;
+    const int p = (int)(unit / nb), blk = (int)(unit % nb);
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    const int n = blk * 128 + 4 * l32;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.f;
+        for (int q = 0; q < SK; ++q) s += Z[((size_t)q * P + p) * D + n + j];
+        v[j] = s;
+    }
+    fwht128(v, l32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[(size_t)p * D + n + j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const float* __restrict__ wts,
+                                                      float* __restrict__ out, int rows, int D, int slots) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)rows * D) return;
+    const int r = (int)(i / D), d = (int)(i % D);
+    float acc = 0.f;
+    for (int k = 0; k < slots; ++k) acc = fmaf(wts[r * slots + k], y[((size_t)r * slots + k) * D + d], acc);
+    out[(size_t)r * D + d] = acc;
+}
+
+// down epilogue of every slot of one (row, 128-block) into shared memory, then the routed fma chain in slot order and
+// the shared slot's gated output. n_routed == slots and out_shared == nullptr give down_combine.
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(256) void down_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                           const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+                                                           const float* __restrict__ wts, void* __restrict__ out,
+                                                           void* __restrict__ out_shared, int P, int D, int SK, int E,
+                                                           int slots, int n_routed) {
+    __shared__ float part[32][128];
+    const int r = blockIdx.x, blk = blockIdx.y;
+    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    const int n0 = blk * 128;
+    for (int k = hw; k < slots; k += 8) {
+        const int p = r * slots + k;
+        const int e = pick[p];
+        const int n = n0 + 4 * l32;
+        float o[4];
+        if (e >= 0 && e < E) {
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float s = 0.f;
+                for (int q = 0; q < SK; ++q) s += Z[((size_t)q * P + p) * D + n + j];
+                v[j] = s;
+            }
+            fwht128(v, l32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                o[j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
+                y[(size_t)p * D + n + j] = o[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = y[(size_t)p * D + n + j];   // an invalid pick reuses y's row
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[k][4 * l32 + j] = o[j];
+    }
+    __syncthreads();
+    const int col = threadIdx.x & 127;
+    const size_t at = (size_t)r * D + n0 + col;
+    if (threadIdx.x < 128) {
+        float acc = 0.f;
+        for (int q = 0; q < n_routed; ++q) acc = fmaf(wts[r * slots + q], part[q][col], acc);
+        if constexpr (OUT_DTYPE == F32) static_cast<float*>(out)[at] = acc;
+        else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out)[at] = f2bf(acc);
+        else static_cast<uint16_t*>(out)[at] = f2h(acc);
+    } else if (out_shared != nullptr && n_routed < slots) {
+        const float v = wts[r * slots + n_routed] * part[n_routed][col];
+        if constexpr (OUT_DTYPE == F32) static_cast<float*>(out_shared)[at] = v;
+        else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out_shared)[at] = f2bf(v);
+        else static_cast<uint16_t*>(out_shared)[at] = f2h(v);
+    }
+}
+
+}  // namespace esp
+
+// ======================================================================================================================
+// C ABI
+// ======================================================================================================================
+using namespace esp;
+
+static unsigned units_grid(long units, int per_block) { return (unsigned)((units + per_block - 1) / per_block); }
+
+extern "C" int esp_group(const int32_t* pick, int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members,
+                         int64_t maxm, int64_t R, int64_t slots, int64_t E, void* stream) {
+    ESP_REQUIRE(pick && uids && ucount && members, "group: null pointer");
+    ESP_REQUIRE(E >= 1 && E <= MAX_GROUP_IDS, "too many experts for the grouping kernel");
+    ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
+    ESP_REQUIRE(R >= 1 && R * slots <= MAX_PICKS, "grouping window too large");
+    ESP_REQUIRE(maxu >= (R * slots < E ? R * slots : E), "uids too small");
+    ESP_REQUIRE(maxm >= 1, "members too small");
+    group_kernel<<<1, GT, 0, (hipStream_t)stream>>>(pick, uids, ucount, members, (int)R, (int)slots, (int)E,
+                                                     (int)maxm);
+    return esp_host::launch_check("group");
+}
+
+extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
+                               int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
+                               int64_t logits_numel, int32_t* counter, int32_t* pick_out, float* wts_out,
+                               int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm,
+                               void* stream) {
+    const int has = shared_id >= 0;
+    ESP_REQUIRE(x && gate && logits && counter && pick_out && wts_out && uids && ucount && members,
+                "route_group: null pointer");
+    ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
+    ESP_REQUIRE(E >= 1 && E <= 256 && k >= 1 && k <= 16 && k <= E && H % 256 == 0 && H > 0,
+                "route_group: shape limits");
+    ESP_REQUIRE(R >= 1 && R * (k + has) <= MAX_PICKS && k + has <= 32, "route_group: window too large");
+    ESP_REQUIRE(!has || sgate, "the shared gate weight is needed with a shared slot");
+    ESP_REQUIRE(logits_numel >= R * (E + has), "logits scratch too small");
+    ESP_REQUIRE(x_stride >= H && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE(maxu >= (R * (k + has) < E + has ? R * (k + has) : E + has), "uids too small");
+    ESP_REQUIRE(maxm >= 1, "members too small");
+    RouteArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.gate = static_cast<const uint16_t*>(gate);
+    a.sgate = static_cast<const uint16_t*>(sgate);
+    a.logits = logits;
+    a.counter = counter;
+    a.pick_out = pick_out;
+    a.wts_out = wts_out;
+    a.uids = uids;
+    a.ucount = ucount;
+    a.members = members;
+    a.x_stride = (int)x_stride;
+    a.bf16 = x_dtype == ESP_BF16;
+    a.R = (int)R;
+    a.H = (int)H;
+    a.E = (int)E;
+    a.k = (int)k;
+    a.shared_id = (int)shared_id;
+    a.maxm = (int)maxm;
+    const long tiles = ((R + RT_ROWS - 1) / RT_ROWS) * ((E + has + RT_COLS - 1) / RT_COLS);
+    route_group_kernel<<<units_grid(tiles, GT / 64), GT, 0, (hipStream_t)stream>>>(a);
+    return esp_host::launch_check("route_group");
+}
+
+extern "C" int esp_group_shared(const int32_t* pick_in, const float* wts_in, const void* x, int x_dtype,
+                                int64_t x_stride, int64_t H, const void* gate_w, int64_t shared_id, int32_t* pick_out,
+                                float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members,
+                                int64_t maxm, int64_t R, int64_t slots_in, int64_t E, void* stream) {
+    const int has = shared_id >= 0;
+    const int64_t slots = slots_in + has;
+    ESP_REQUIRE(pick_in && wts_in && pick_out && wts_out && uids && ucount && members, "group_shared: null pointer");
+    ESP_REQUIRE(E >= 1 && E <= MAX_GROUP_IDS, "too many experts for the grouping kernel");
+    ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
+    ESP_REQUIRE(R >= 1 && R * slots <= MAX_PICKS, "grouping window too large");
+    ESP_REQUIRE(!has || (gate_w && x), "a shared slot needs its gate weight");
+    ESP_REQUIRE(!has || (x_dtype == ESP_BF16 || x_dtype == ESP_F16), "x: bf16/fp16");
+    ESP_REQUIRE(!has || (H % 256 == 0 && x_stride % 4 == 0), "group_shared: H must be a multiple of 256");
+    ESP_REQUIRE(maxu >= (R * slots < E ? R * slots : E), "uids too small");
+    ESP_REQUIRE(maxm >= 1, "members too small");
+    group_shared_kernel<<<1, GT, 0, (hipStream_t)stream>>>(
+        pick_in, wts_in, static_cast<const uint16_t*>(x), (int)x_stride, x_dtype == ESP_BF16,
+        static_cast<const uint16_t*>(gate_w), (int)H, (int)shared_id, pick_out, wts_out, uids, ucount, members,
+        (int)R, (int)slots_in, (int)E, (int)maxm);
+    return esp_host::launch_check("group_shared");
+}
+
+extern "C" int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const int32_t* pick, const void* suh0,
+                          const void* suh1, void* out0, void* out1, int64_t rows, int64_t K, int64_t slots, int64_t E,
+                          void* stream) {
+    ESP_REQUIRE(x && pick && suh0 && suh1 && out0 && out1, "rot_in: null pointer");
+    ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
+    ESP_REQUIRE(K % 128 == 0 && K > 0, "K must be a multiple of 128");
+    ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
+    const long units = rows * slots * (K / 128);
+    if (units <= 0) return esp_host::ok();
+    rot_in_kernel<<<units_grid(units, 4), 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint16_t*>(x), x_dtype, (int)x_stride, pick, static_cast<const uint16_t*>(suh0),
+        static_cast<const uint16_t*>(suh1), static_cast<uint16_t*>(out0), static_cast<uint16_t*>(out1),
+        (int)(rows * slots), (int)K, (int)slots, (int)E);
+    return esp_host::launch_check("rot_in");
+}
+
+extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
+                           const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids,
+                           int64_t nexp_max, const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z,
+                           int64_t z_numel, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
+                           int64_t nt, int64_t warps, int64_t pf, int64_t lo, int64_t hi, void* stream) {
+    (void)nt;
+    (void)warps;
+    (void)pf;
+    ESP_REQUIRE(X0 && X1 && TP0 && TP1 && B0 && B1 && C0 && C1 && uids && ucount && members && Z,
+                "grouped: null pointer");
+    ESP_REQUIRE(mats == 1 || mats == 2, "mats must be 1 or 2");
+    ESP_REQUIRE(SK >= 1 && K > 0 && N > 0 && K % (32 * SK) == 0 && N % 128 == 0, "K and N must split evenly");
+    ESP_REQUIRE(z_numel >= mats * SK * P * N, "Z too small");
+    ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
+    ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
+    ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
+    if (nexp_max <= 0) return esp_host::ok();
+    GroupedArgs a{};
+    a.X0 = static_cast<const uint16_t*>(X0);
+    a.X1 = static_cast<const uint16_t*>(X1);
+    a.TP0 = TP0;
+    a.TP1 = TP1;
+    a.B0 = B0;
+    a.B1 = B1;
+    a.C0 = C0;
+    a.C1 = C1;
+    a.uids = uids;
+    a.ucount = ucount;
+    a.members = members;
+    a.Z = Z;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)P;
+    a.SK = (int)SK;
+    a.maxm = (int)maxm;
+    a.slots = (int)slots;
+    dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK));
+    grouped_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    return esp_host::launch_check("grouped");
+}
+
+extern "C" int esp_gateup_epilogue(const float* Z, const int32_t* pick, const void* svh_g, const void* svh_u,
+                                   const void* suh_d, void* xd, int64_t rows, int64_t P, int64_t N, int64_t SK,
+                                   int64_t slots, int64_t E, double limit, int64_t act_mode, void* stream) {
+    ESP_REQUIRE(Z && pick && svh_g && svh_u && suh_d && xd, "gateup_epilogue: null pointer");
+    ESP_REQUIRE(N % 128 == 0 && N > 0, "N must be a multiple of 128");
+    ESP_REQUIRE(SK >= 1, "SK must be positive");
+    ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
+    const long units = rows * slots * (N / 128);
+    if (units <= 0) return esp_host::ok();
+    gateup_epilogue_kernel<<<units_grid(units, 8), 256, 0, (hipStream_t)stream>>>(
+        Z, pick, static_cast<const uint16_t*>(svh_g), static_cast<const uint16_t*>(svh_u),
+        static_cast<const uint16_t*>(suh_d), static_cast<uint16_t*>(xd), (int)P, (int)N, (int)SK, (int)E,
+        (float)limit, (int)act_mode);
+    return esp_host::launch_check("gateup_epilogue");
+}
+
+extern "C" int esp_down_epilogue(const float* Z, const int32_t* pick, const void* svh_d, float* y, int64_t rows,
+                                 int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E, void* stream) {
+    ESP_REQUIRE(Z && pick && svh_d && y, "down_epilogue: null pointer");
+    ESP_REQUIRE(D % 128 == 0 && D > 0, "D must be a multiple of 128");
+    ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
+    const long units = rows * slots * (D / 128);
+    if (units <= 0) return esp_host::ok();
+    down_epilogue_kernel<<<units_grid(units, 8), 256, 0, (hipStream_t)stream>>>(
+        Z, pick, static_cast<const uint16_t*>(svh_d), y, (int)P, (int)D, (int)SK, (int)E);
+    return esp_host::launch_check("down_epilogue");
+}
+
+extern "C" int esp_combine(const float* y, const float* wts, float* out, int64_t rows, int64_t D, int64_t slots,
+                           void* stream) {
+    ESP_REQUIRE(y && wts && out, "combine: null pointer");
+    const long n = rows * D;
+    if (n <= 0) return esp_host::ok();
+    combine_kernel<<<units_grid(n, 256), 256, 0, (hipStream_t)stream>>>(y, wts, out, (int)rows, (int)D, (int)slots);
+    return esp_host::launch_check("combine");
+}
+
+static int down_combine_any(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts,
+                            void* out, int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK,
+                            int64_t slots, int64_t E, int64_t n_routed, void* stream) {
+    ESP_REQUIRE(Z && pick && svh_d && y && wts && out, "down_combine: null pointer");
+    ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
+    ESP_REQUIRE(D % 128 == 0 && D > 0, "D must be a multiple of 128");
+    ESP_REQUIRE(n_routed >= 0 && n_routed <= slots, "n_routed <= slots");
+    ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
+    if (rows <= 0) return esp_host::ok();
+    dim3 grid((unsigned)rows, (unsigned)(D / 128));
+    hipStream_t s = (hipStream_t)stream;
+    auto svh = static_cast<const uint16_t*>(svh_d);
+    if (out_dtype == ESP_BF16)
+        down_combine_kernel<BF16><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+                                                      (int)E, (int)slots, (int)n_routed);
+    else if (out_dtype == ESP_F16)
+        down_combine_kernel<F16><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+                                                     (int)E, (int)slots, (int)n_routed);
+    else
+        down_combine_kernel<F32><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+                                                     (int)E, (int)slots, (int)n_routed);
+    return esp_host::launch_check("down_combine");
+}
+
+extern "C" int esp_down_combine(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts,
+                                float* out, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E,
+                                void* stream) {
+    return down_combine_any(Z, pick, svh_d, y, wts, out, ESP_F32, nullptr, rows, P, D, SK, slots, E, slots, stream);
+}
+
+extern "C" int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts,
+                                 void* out, int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D,
+                                 int64_t SK, int64_t slots, int64_t E, int64_t n_routed, void* stream) {
+    return down_combine_any(Z, pick, svh_d, y, wts, out, out_dtype, out_shared, rows, P, D, SK, slots, E, n_routed,
+                            stream);
+}

@@ -1,0 +1,184 @@
+// EXL3 16-bit-state trellis decode for gfx950, laid out for the 16x16x32 f16 MFMA B operand.
+//
+// Format (experts_grouped.cuh:83-154): a 16x16 tile of a b-bit matrix is TW = 8b uint32 words, read as one circular
+// big-endian bit stream of L = 256b bits (stream bit j = bit 31 - j%32 of word j/32). State p (0..255) is the 16
+// stream bits ending at (p + 1) * b, earliest bit most significant; it holds W[2t + 8(q&1) + (j&1)][g + 8(q>>1)] for
+// lane = p/8, j = p%8, q = j/2, t = lane%4, g = lane/4 (dequant_kernel's placement, :330-338).
+//
+// MFMA mapping. v_mfma_f32_16x16x32_f16 takes, from lane l, 8 k values of B column l%16 in k group G = l/16. One
+// B operand here covers two k tiles (32 k) of one n tile: lane (c = l%16, G) decodes column c of k tile G/2, the
+// 8 states with t in {2(G&1), 2(G&1)+1}: two runs of 4 consecutive states,
+//   run A: p = 32(c&7) + 4(c>>3) + 16(G&1) + {0,1,2,3}   (k = 4(G&1) + {0, 1, 8, 9})
+//   run B: run A + 8                                       (k = 4(G&1) + {2, 3, 10, 11}).
+// The B slots are put in natural k order, [4(G&1) + 0..3, 8 + 4(G&1) + 0..3] of the lane's k tile, so the A operand
+// (lane l: row l%16, same k group) reads x at those k: two 8-byte loads, no permutation.
+//
+// Each run's 4 windows lie inside 3b + 16 <= 40 stream bits: three words are loaded, a funnel shift by the lane's
+// bit offset lines the run up at bit 63 of (R0:R1), and window j is 16 bits at offset j*b of that 64-bit value.
+#pragma once
+
+#include "common.hpp"
+
+namespace esp {
+
+constexpr uint32_t MCG_MUL = 0xCBAC1FEDu;   // experts_grouped.cuh:67
+constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;  // :73
+constexpr uint32_t MCG_XOR = 0x3B603B60u;
+
+// int5 / int6 grids: k reproduces rintf(v / c) (experts_grouped.cuh:40-42)
+constexpr float GRID_K5 = 0x1.e62c10p+1f;
+constexpr float GRID_K6 = 0x1.f660bap+2f;
+__host__ __device__ constexpr float grid_c(int cb) { return cb == 6 ? 3.94921875f / 15.0f : 3.94921875f / 31.0f; }
+
+// Per-lane constants of the MFMA B-operand decode for b = K2/2 bits: word indices (mod TW) and funnel shifts of the
+// two runs. The same for every tile of a matrix.
+template <int K2>
+struct LanePlan {
+    static constexpr int B = K2 / 2, TW = 4 * K2;
+    int wa, wb;      // first word of run A / B
+    int sha, shb;    // funnel shifts (32 - bit offset of the run in its first word)
+    __device__ __forceinline__ explicit LanePlan(int lane) {
+        const int c = lane & 15, G = lane >> 4;
+        const int pa = 32 * (c & 7) + 4 * (c >> 3) + 16 * (G & 1);
+        const int sa = (pa + 1) * B - 16, sb = (pa + 9) * B - 16;   // first stream bit of each run's first window
+        const int qa = (sa - 1) >> 5, qb = (sb - 1) >> 5;          // floor division (sa may be negative)
+        sha = 32 - (sa - 32 * qa);
+        shb = 32 - (sb - 32 * qb);
+        wa = (qa + TW) % TW;
+        wb = (qb + TW) % TW;
+    }
+};
+
+// The 6 words of one tile a lane needs: w[0..2] for run A, w[3..5] for run B.
+template <int K2>
+__device__ __forceinline__ void load_words(const uint32_t* __restrict__ tile, const LanePlan<K2>& lp, uint32_t (&w)[6]) {
+    constexpr int TW = 4 * K2;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        int ia = lp.wa + i, ib = lp.wb + i;
+        ia = ia >= TW ? ia - TW : ia;
+        ib = ib >= TW ? ib - TW : ib;
+        w[i] = __builtin_nontemporal_load(tile + ia);
+        w[3 + i] = __builtin_nontemporal_load(tile + ib);
+    }
+}
+
+// window j (0..3) of a run lined up in (r0:r1)
+template <int B, int J>
+__device__ __forceinline__ uint32_t window(uint32_t r0, uint32_t r1) {
+    constexpr int off = J * B;
+    if constexpr (off <= 16)
+        return __builtin_amdgcn_ubfe(r0, 16 - off, 16);
+    else
+        return __builtin_amdgcn_alignbit(r0, r1, 48 - off) & 0xFFFFu;
+}
+
+// the 4 states of a run starting in words (w0, w1, w2) at funnel shift sh
+template <int B>
+__device__ __forceinline__ void run_states(uint32_t w0, uint32_t w1, uint32_t w2, int sh, uint32_t (&s)[4]) {
+    const uint32_t r0 = __builtin_amdgcn_alignbit(w0, w1, sh);
+    const uint32_t r1 = __builtin_amdgcn_alignbit(w1, w2, sh);
+    s[0] = window<B, 0>(r0, r1);
+    s[1] = window<B, 1>(r0, r1);
+    s[2] = window<B, 2>(r0, r1);
+    s[3] = window<B, 3>(r0, r1);
+}
+
+__device__ __forceinline__ uint32_t mcg_hash(uint32_t s) { return (s * MCG_MUL & MCG_MASK) ^ MCG_XOR; }
+
+// mcg values of two states as packed fp16 (lo = s0): the two halves of each hash added in one RNE fp16 add
+// (experts_grouped.cuh:64-79)
+__device__ __forceinline__ uint32_t mcg_pair(uint32_t s0, uint32_t s1) {
+    const uint32_t x0 = mcg_hash(s0), x1 = mcg_hash(s1);
+    const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+    const f16x2 r = __builtin_bit_cast(f16x2, lo) + __builtin_bit_cast(f16x2, hi);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Codebook value pair. CB: 1 mcg; 3 E2M1 snap; 6 / 7 fp16(q * c) on the int5 / int6 grid; 22 / 23 the grid index q
+// itself (fp16, exact), whose sums the caller scales by c.
+template <int CB>
+__device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
+    const uint32_t m = mcg_pair(s0, s1);
+    if constexpr (CB == 1) {
+        return m;
+    } else if constexpr (CB == 3) {
+        // E2M1 (experts_grouped.cuh:25-38): |v| against 0.75 * {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5}, summing the grid
+        // steps, then v's sign. Each step is clamp((|v| - t) * 2^14, 0, 1): |v| > t by at least one fp16 ulp of t gives
+        // >= 2, so the step is exactly 0 or 1, and every partial sum is exact in fp16.
+        const f16x2 a = __builtin_bit_cast(f16x2, m & 0x7FFF7FFFu);
+        const f16x2 big = {(_Float16)16384.0f, (_Float16)16384.0f};
+        const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f}, one = {(_Float16)1.0f, (_Float16)1.0f};
+        constexpr float T[7] = {0.1875f, 0.5625f, 0.9375f, 1.3125f, 1.875f, 2.625f, 3.75f};
+        constexpr float S[7] = {0.375f, 0.375f, 0.375f, 0.375f, 0.75f, 0.75f, 1.5f};
+        f16x2 acc = zero;
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            const f16x2 nt = {(_Float16)(-T[i] * 16384.0f), (_Float16)(-T[i] * 16384.0f)};
+            f16x2 st = __builtin_elementwise_fma(a, big, nt);
+            st = __builtin_elementwise_min(__builtin_elementwise_max(st, zero), one);
+            const f16x2 w = {(_Float16)S[i], (_Float16)S[i]};
+            acc = __builtin_elementwise_fma(st, w, acc);
+        }
+        return __builtin_bit_cast(uint32_t, acc) | (m & 0x80008000u);
+    } else {
+        static_assert(CB == 6 || CB == 7 || CB == 22 || CB == 23, "codebook");
+        constexpr float k = (CB == 6 || CB == 22) ? GRID_K5 : GRID_K6;
+        const f16x2 v = __builtin_bit_cast(f16x2, m);
+        const float q0 = __builtin_rintf((float)v[0] * k), q1 = __builtin_rintf((float)v[1] * k);
+        if constexpr (CB == 22 || CB == 23) {
+            const f16x2 r = {(_Float16)q0, (_Float16)q1};           // |q| <= 31: exact
+            return __builtin_bit_cast(uint32_t, r);
+        } else {
+            constexpr float c = grid_c(CB);
+            const f16x2 r = {(_Float16)(q0 * c), (_Float16)(q1 * c)};   // one RNE rounding each
+            return __builtin_bit_cast(uint32_t, r);
+        }
+    }
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// A lane's MFMA B operand for one tile from its 6 words, as 4 packed fp16 pairs: slots in natural k order,
+// [A0 A1 | B0 B1 | A2 A3 | B2 B3] (k = 4(G&1) + {0,1 | 2,3 | 8,9 | 10,11}).
+template <int CB, int K2>
+__device__ __forceinline__ u32x4 decode_words(const uint32_t (&w)[6], const LanePlan<K2>& lp) {
+    constexpr int B = K2 / 2;
+    uint32_t sa[4], sb[4];
+    run_states<B>(w[0], w[1], w[2], lp.sha, sa);
+    run_states<B>(w[3], w[4], w[5], lp.shb, sb);
+    uint32_t r[4];
+    r[0] = decode_pair<CB>(sa[0], sa[1]);
+    r[1] = decode_pair<CB>(sb[0], sb[1]);
+    r[2] = decode_pair<CB>(sa[2], sa[3]);
+    r[3] = decode_pair<CB>(sb[2], sb[3]);
+    const u32x4 v = {r[0], r[1], r[2], r[3]};
+    return v;
+}
+
+template <int CB, int K2>
+__device__ __forceinline__ f16x8 decode_b(const uint32_t (&w)[6], const LanePlan<K2>& lp) {
+    return __builtin_bit_cast(f16x8, decode_words<CB, K2>(w, lp));
+}
+
+// fp16 bits of B slot i (0..7) of a decoded operand
+__device__ __forceinline__ uint16_t slot_bits(const u32x4& v, int i) {
+    const uint32_t word = v[i >> 1];
+    return (uint16_t)((i & 1) ? (word >> 16) : (word & 0xFFFFu));
+}
+
+// k offset (inside its 16-k tile) of B slot i for k group G
+__host__ __device__ constexpr int slot_k(int G, int i) { return 4 * (G & 1) + (i & 3) + 8 * (i >> 2); }
+
+// The (codebook, K2) pairs with kernels (experts_grouped.cuh:227-229).
+#define ESP_CASES(X) \
+    X(1, 2) X(1, 4) X(1, 6) X(1, 8) X(1, 10) X(1, 12) X(1, 14) X(1, 16) \
+    X(3, 2) X(3, 4) X(3, 6) X(6, 4) X(6, 6) X(6, 8) X(7, 6) X(7, 8) X(7, 10)
+
+__host__ __device__ constexpr bool supported(int cb, int k2) {
+    return (cb == 1 && k2 >= 2 && k2 <= 16 && k2 % 2 == 0) || (cb == 3 && (k2 == 2 || k2 == 4 || k2 == 6)) ||
+           (cb == 6 && (k2 == 4 || k2 == 6 || k2 == 8)) || (cb == 7 && (k2 == 6 || k2 == 8 || k2 == 10));
+}
+
+}  // namespace esp
