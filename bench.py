@@ -1,0 +1,351 @@
+#!/usr/bin/env python3
+"""Benchmark of the trellis kernel layer on one MI355X ("us/layer & compressed-weight HBM GB/s (% of
+peak) at batch 1/8/32; decode tok/s").
+
+Headline (`value`): BASELINE config 2, the dense attention-block layer (qkv 2048->5120 int6, o 4096->2048 int6,
+shared-expert gate/up 2048->2x512 int5 and down 512->2048 int5, all 4-bit trellis; four launches a layer, one per vLLM
+layer) at batch 1, as compressed-weight GB/s: algorithmic bytes (trellis + suh + svh of the four launches) over the
+time per layer. Weights are cold: a HIP graph replays the layer over enough distinct weight copies (>= 1 GiB) that
+the 256 MB MALL cannot serve them. A step is one replay of that graph; inputs are resident in HBM.
+
+Also reported: us/layer at batch 8 and 32; BASELINE config 1 (one 2048x2048 int6 matrix); config 3 (route_group);
+config 4 (a 256-expert MoE layer, fused routing + six launches, T = 1, 4, 32); `roofline` of the dominant kernel (the
+qkv dense launch: average launch time from a graph of cold launches, with HIP events on the launch stream); and
+`cpu_baseline`: the reference's CPU path on this host (this repo's C restatement of the dequantisation, multithreaded,
+then fp32 Hadamards and torch.matmul), on a bounded sample of the same layer.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-moe]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
+
+PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
+COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def graph_of(fn):
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, reps: int, warmup: int = 2) -> float:
+    """ms per replay, from HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(reps):
+        g.replay()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) / reps
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------------------------------------------
+def dense_block(gen, dev):
+    """BASELINE config 2's four launches: [qkv], [o], [shared gate, up], [shared down]."""
+    from vllm_espalier import dense as D, workloads as WL
+    q = [WL.matrix(2048, 4096, 4, "int6", gen, dev), WL.matrix(2048, 512, 4, "int6", gen, dev),
+         WL.matrix(2048, 512, 4, "int6", gen, dev)]
+    o = [WL.matrix(4096, 2048, 4, "int6", gen, dev)]
+    gu = [WL.matrix(2048, 512, 4, "int5", gen, dev), WL.matrix(2048, 512, 4, "int5", gen, dev)]
+    dn = [WL.matrix(512, 2048, 4, "int5", gen, dev)]
+    return [D.Dense(q), D.Dense(o), D.Dense(gu), D.Dense(dn)]
+
+
+def block_bytes(block) -> int:
+    from vllm_espalier import workloads as WL
+    return sum(WL.nbytes(d.mats) for d in block)
+
+
+def dense_stack(copies: int, seed: int, dev):
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    return [dense_block(gen, dev) for _ in range(copies)]
+
+
+def run_dense(stack, M: int, dev, which=None):
+    """A graph over every copy of the block at M rows (which: the launch indices to include)."""
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(1000 + M)
+    xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for K in (512, 2048, 4096)}
+    outs = [[torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev) for d in block] for block in stack]
+    idx = range(4) if which is None else which
+
+    def fn():
+        for block, ob in zip(stack, outs):
+            for i in idx:
+                block[i].forward(xs[block[i].K], out=ob[i])
+    return graph_of(fn)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# MoE (config 4)
+# ---------------------------------------------------------------------------------------------------------------
+def moe_layer(gen, dev, E=256, D=2048, I=512):
+    import torch
+    from vllm_espalier import experts as G, workloads as WL
+    widths = torch.randint(1, 4, (E,), generator=gen, device=dev).tolist()
+    grid = {1: "e2m1", 2: "e2m1", 3: "int5"}
+    experts = [tuple(WL.matrix(k, n, b, grid[b], gen, dev) for k, n in ((D, I), (D, I), (I, D))) for b in widths]
+    shared = tuple(WL.matrix(k, n, 4, "int5", gen, dev) for k, n in ((D, I), (D, I), (I, D)))
+    gate_w = (torch.randn((D,), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+    router = (torch.randn((E, D), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    L = G.prepare(experts, shared, gate_w)
+    return L, experts, shared, router
+
+
+def bench_moe(dev, steps: int, layers: int, rows=(1, 4, 32)):
+    import torch
+    from vllm_espalier import experts as G, workloads as WL
+    gen = torch.Generator(device=dev).manual_seed(4)
+    stack = [moe_layer(gen, dev) for _ in range(layers)]
+    res = {}
+    for T in rows:
+        xg = torch.Generator(device=dev).manual_seed(40 + T)
+        xs = [torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16) for _ in stack]
+        s = G.scratch(stack[0][0], 32, 9, dev)
+        outs = [(torch.empty((T, 2048), dtype=torch.bfloat16, device=dev),
+                 torch.empty((T, 2048), dtype=torch.bfloat16, device=dev)) for _ in stack]
+        # the experts each layer picks, for its algorithmic bytes
+        nbytes = 0
+        for (L, experts, shared, router), x in zip(stack, xs):
+            G.route(x, router, 8, L, s)
+            torch.cuda.synchronize()
+            cnt = int(s.count.item())
+            ids = s.ids[:cnt].tolist()
+            nbytes += sum(WL.nbytes(experts[e]) if e < 256 else WL.nbytes(shared) for e in ids)
+
+        def fn():
+            for (L, experts, shared, router), x, (o, sh) in zip(stack, xs, outs):
+                G.route(x, router, 8, L, s)
+                G.routed2(x, None, None, L, s, out=o, out_shared=sh, k=8)
+        g = graph_of(fn)
+        ms = time_graph(g, steps)
+        us = ms * 1000 / len(stack)
+        gbs = nbytes / len(stack) / (us * 1e-6) / 1e9
+        res[str(T)] = {"us_per_layer": round(us, 2), "bytes_per_layer": nbytes // len(stack), "GBps": round(gbs, 1),
+                       "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+        log(f"moe T={T}: {us:.2f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak)")
+    # the router alone (config 3)
+    rt = {}
+    for T in (1, 32):
+        xg = torch.Generator(device=dev).manual_seed(70 + T)
+        xs = [torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16) for _ in stack]
+        s = G.scratch(stack[0][0], 32, 9, dev)
+
+        def fr():
+            for (L, experts, shared, router), x in zip(stack, xs):
+                G.route(x, router, 8, L, s)
+        ms = time_graph(graph_of(fr), steps)
+        rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2)}
+        log(f"route_group T={T}: {ms * 1000 / len(stack):.2f} us")
+    del stack
+    torch.cuda.empty_cache()
+    return res, rt
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# CPU baseline: the reference's CPU path (dequantisation + torch matmul) on this host
+# ---------------------------------------------------------------------------------------------------------------
+def cpu_baseline(block, reps: int):
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as O            # the C restatement of the reference dequantisation (cpu_baseline leg only)
+    from vllm_espalier import experts as G
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    H = torch.from_numpy(O.sylvester() / np.sqrt(128.0)).float()
+    mats = [[(m.trellis.cpu().numpy(), 2 * m.K, G.KERNEL_CB[m.cb], m.suh.float().cpu(), m.svh.float().cpu())
+             for m in d.mats] for d in block]
+    x = {K: torch.randn((1, K)) for K in (512, 2048, 4096)}
+
+    def had(v):
+        return (v.view(*v.shape[:-1], -1, 128) @ H).view(v.shape)
+
+    def layer():
+        for launch in mats:
+            for t, k2, cb, suh, svh in launch:
+                W = torch.from_numpy(O.dequant_f32(t, k2, cb, cores))
+                xv = x[W.shape[0]]
+                _ = had(had(xv * suh) @ W) * svh
+    layer()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return med, cores
+
+
+# ---------------------------------------------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=20)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU (the reference path is single-GPU, TP=1); --gpus {a.gpus} is "
+              "not supported", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    from vllm_espalier import experts as G
+    G.ext()                                   # the HIP extension must be there: no fallback
+    name = torch.cuda.get_device_name(dev)
+    log(f"device {name}")
+
+    # ---- config 2 dense block, cold stack
+    probe = dense_stack(1, 1, dev)
+    bpl = block_bytes(probe[0])
+    copies = max(2, -(-COLD_BYTES // bpl))
+    del probe
+    stack = dense_stack(copies, 2, dev)
+    log(f"dense block: {bpl} algorithmic bytes a layer, {copies} cold copies ({copies * bpl / 2**30:.2f} GiB)")
+    per_m = {}
+    g1 = None
+    for M in (1, 8, 32):
+        g = run_dense(stack, M, dev)
+        ms = time_graph(g, a.steps if M == 1 else max(5, a.steps // 2), a.warmup)
+        us = ms * 1000 / copies
+        gbs = bpl / (us * 1e-6) / 1e9
+        per_m[str(M)] = {"us_per_layer": round(us, 3), "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+        log(f"dense block M={M}: {us:.3f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak)")
+        if M == 1:
+            g1 = g
+        else:
+            del g
+    # the timed steps of the headline: a step = one replay over the cold stack at batch 1
+    for _ in range(a.warmup):
+        g1.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(a.steps):
+        g1.replay()
+    en.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = st.elapsed_time(en) / a.steps
+    value = copies * bpl / (ms_step * 1e-3) / 1e9
+    log(f"headline: {ms_step:.3f} ms a step ({copies} layers), {value:.0f} GB/s; wall {wall:.3f} s")
+    del g1
+
+    # ---- roofline of the dominant kernel: the qkv launch (5.27 MB), a graph of cold launches at batch 1
+    gq = run_dense(stack, 1, dev, which=[0])
+    ms = time_graph(gq, a.steps, a.warmup)
+    from vllm_espalier import dense as D, workloads as WL
+    qkv_bytes = WL.nbytes(stack[0][0].mats)
+    q_us = ms * 1000 / copies
+    achieved = qkv_bytes / (q_us * 1e-6) / 1e9
+    log(f"qkv launch: {q_us:.3f} us, {achieved:.0f} GB/s")
+    del gq
+    per_launch = {}
+    for i, nm in enumerate(("qkv", "o", "shared_gate_up", "shared_down")):
+        if i == 0:
+            per_launch[nm] = round(q_us, 3)
+            continue
+        gi = run_dense(stack, 1, dev, which=[i])
+        per_launch[nm] = round(time_graph(gi, a.steps, a.warmup) * 1000 / copies, 3)
+        del gi
+
+    # ---- config 1: one 2048x2048 4-bit int6 matrix, cold
+    gen = torch.Generator(device=dev).manual_seed(11)
+    m1 = [D.Dense([WL.matrix(2048, 2048, 4, "int6", gen, dev)]) for _ in range(max(2, COLD_BYTES // 2105344))]
+    x1 = torch.randn((1, 2048), device=dev).to(torch.bfloat16)
+    o1 = torch.empty((1, 2048), dtype=torch.bfloat16, device=dev)
+    g = graph_of(lambda: [d.forward(x1, out=o1) for d in m1])
+    c1_us = time_graph(g, a.steps, a.warmup) * 1000 / len(m1)
+    c1_gbs = WL.nbytes(m1[0].mats) / (c1_us * 1e-6) / 1e9
+    log(f"config 1: {c1_us:.3f} us, {c1_gbs:.0f} GB/s")
+    del g, m1
+
+    cpu_block = stack[0]
+    del stack
+    torch.cuda.empty_cache()
+
+    moe = route = None
+    if not a.no_moe:
+        moe, route = bench_moe(dev, max(5, a.steps // 2), 6)
+
+    cpu = None
+    if not a.no_cpu:
+        med, cores = cpu_baseline(cpu_block, a.cpu_reps)
+        cpu = {"value": round(bpl / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+               "us_per_layer": round(med * 1e6, 1),
+               "sample": f"median of {a.cpu_reps} forwards of one config-2 block at batch 1: C dequantisation "
+                         f"(oracle/, {cores} threads) + fp32 Hadamards + torch.matmul"}
+        log(f"cpu baseline: {med * 1e3:.1f} ms/layer on {cores} cores")
+
+    out = {
+        "metric": "compressed-weight HBM GB/s, config-2 dense block at batch 1 (us/layer at batch 1/8/32 and the MoE "
+                  "layer alongside)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random trellis codes, N(0,1) bf16 activations)",
+        "config": {"workload": f"BASELINE config 2 dense block (qkv/o int6, shared gate/up/down int5, 4-bit), batch 1, "
+                               f"{copies} cold copies a step",
+                   "bytes_per_layer": bpl, "layers_per_step": copies, "device": name},
+        "dense_block": per_m,
+        "dense_launch_us_batch1": per_launch,
+        "config1_us": round(c1_us, 3),
+        "config1_GBps": round(c1_gbs, 1),
+        "moe_layer": moe,
+        "route_group": route,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "dense_kernel (qkv launch, 5,269,504 B a launch)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

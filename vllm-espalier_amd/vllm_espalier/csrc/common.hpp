@@ -115,6 +115,42 @@ __device__ __forceinline__ uint2 rot128(const void* x, int x_dtype, size_t xi, c
     return u;
 }
 
+// ---- hand-off of partial results between workgroups ----
+// MI355X's eight XCDs each have their own L2, so an agent-scope release fence writes back the whole L2 (buffer_wbl2):
+// ~100 ns a fence, serialised per XCD, which at thousands of waves a launch costs more than the GEMM. Partials
+// instead travel with device-scope (sc1) stores and loads, which are coherent across XCDs by themselves: a workgroup
+// stores its partials with store_dev, arrive_last drains its stores (s_waitcnt) before one relaxed device-scope count,
+// and the last workgroup to arrive reads every partial back with load_dev.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev4(float* p, const float4& v) {
+    store_dev(p, v.x);
+    store_dev(p + 1, v.y);
+    store_dev(p + 2, v.z);
+    store_dev(p + 3, v.w);
+}
+__device__ __forceinline__ float4 load_dev4(const float* p) {
+    return make_float4(load_dev(p), load_dev(p + 1), load_dev(p + 2), load_dev(p + 3));
+}
+
+// True in every thread of the last of `total` workgroups to call it on `counter` (the count is left at total; the
+// last workgroup resets it with store_dev once it has read the partials). Every thread of the workgroup calls it.
+__device__ __forceinline__ bool arrive_last(int* counter, int total, int* sh_flag) {
+    __builtin_amdgcn_s_waitcnt(0);          // this wave's device-scope stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *sh_flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    __syncthreads();
+    return *sh_flag != 0;
+}
+
 }  // namespace esp
 
 // ---- C-ABI error plumbing (host) ----

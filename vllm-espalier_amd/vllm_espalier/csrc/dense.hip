@@ -14,6 +14,7 @@
 // depend on the shape alone, and splits are added in a fixed order.
 #include "common.hpp"
 #include "trellis.hpp"
+#include "gemm.hpp"
 #include "../../../include/espalier.h"
 
 namespace esp {
@@ -38,7 +39,7 @@ struct DenseArgs {
     int y_dtype, y_stride;
     float* Z;
     int* counters;
-    int M, K, SK, NBT, fused, xs_stride;
+    int M, K, SK, NBT, fused, xs_stride, stage_bytes;
 };
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -150,8 +151,7 @@ __device__ __forceinline__ void finish(float (&v)[4], int l32, const uint16_t* s
 }
 
 template <int CB, int K2, int MG>
-__global__ __launch_bounds__(256) void dense_kernel(DenseArgs a) {
-    constexpr int TW = 4 * K2;
+__global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int last;
     const int nbg = blockIdx.x, split = blockIdx.y;
@@ -166,147 +166,108 @@ __global__ __launch_bounds__(256) void dense_kernel(DenseArgs a) {
     const int cb_local = nbg - S.nb0;                       // column block inside the matrix
     const int kr = a.K / a.SK, k0 = split * kr;
     const int M = a.M;
+    const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
+    uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
+
+    // 0. the first stage of trellis copies, in flight while the input rows are rotated
+    {
+        const int steps = kr >> 5;
+        const int sst = steps < StagePlan<K2>::MAX_STEPS ? steps : StagePlan<K2>::MAX_STEPS;
+        issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
+    }
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    const uint16_t* X;
-    int xstride, xk0;
+    RowsA<MG> al;
     if (a.fused) {
+        uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const int chunks = kr >> 7;
-        for (int idx = wave * 2 + half; idx < M * chunks; idx += 8) {
+        for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
             const int r = idx / chunks, ch = idx % chunks;
             const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + k0 + ch * 128, S.suh + k0 + ch * 128, l32);
             *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) = u;
         }
-        __syncthreads();
-        X = xs;
-        xstride = a.xs_stride;
-        xk0 = k0;
-    } else {
-        X = a.xh + (size_t)si * M * a.K;
-        xstride = a.K;
-        xk0 = 0;
-    }
-
-    // 2. the K loop: 2 B operands (n tiles) a step, words of the next step in flight
-    const LanePlan<K2> lp(lane);
-    const int nt_w = cb_local * 8 + 2 * wave;
-    const uint32_t* Tw = S.T + (size_t)nt_w * TW;
-    const size_t kstride = (size_t)NTILES * TW;              // words between consecutive k tiles
-    const int kt_base = (k0 >> 4) + (G >> 1);
-    const int steps = kr >> 5;
-
-    f32x4 acc[2][MG];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // A operand rows of this lane: c and 16 + c
-    bool rok[MG];
-    const uint16_t* xr[MG];
-#pragma unroll
-    for (int g = 0; g < MG; ++g) {
-        const int row = g * 16 + c;
-        rok[g] = row < M;
-        xr[g] = X + (size_t)(rok[g] ? row : 0) * xstride + 16 * (G >> 1) + 4 * (G & 1) - xk0;
-    }
-
-    uint32_t wc[2][6], wn[2][6];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) load_words<K2>(Tw + (size_t)kt_base * kstride + j * TW, lp, wc[j]);
-
-    for (int st = 0; st < steps; ++st) {
-        if (st + 1 < steps) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                load_words<K2>(Tw + (size_t)(kt_base + 2 * (st + 1)) * kstride + j * TW, lp, wn[j]);
-        }
-        const int k = k0 + 32 * st;
-        f16x8 av[MG];
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
-            uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
-            if (rok[g]) {
-                lo = *reinterpret_cast<const uint2*>(xr[g] + k);
-                hi = *reinterpret_cast<const uint2*>(xr[g] + k + 8);
-            }
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-            const u32x4 t = {lo.x, lo.y, hi.x, hi.y};
-            av[g] = __builtin_bit_cast(f16x8, t);
+            const int row = g * 16 + c;
+            al.row[g] = row < M ? xs + (size_t)row * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
         }
+        al.kbase = k0;
+    } else {
+        const uint16_t* X = a.xh + (size_t)si * M * a.K;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const f16x8 b = decode_b<CB, K2>(wc[j], lp);
-#pragma unroll
-            for (int g = 0; g < MG; ++g) acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
+        for (int g = 0; g < MG; ++g) {
+            const int row = g * 16 + c;
+            al.row[g] = row < M ? X + (size_t)row * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
         }
-        if (st + 1 < steps) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 6; ++i) wc[j][i] = wn[j][i];
-        }
+        al.kbase = 0;
     }
 
-    // 3. the block's [M][128] sums in shared memory (the rotated rows are no longer read)
+    // 2. the K loop (its first wait is a workgroup barrier, after which the rotated rows are visible)
+    f32x4 acc[2][MG];
+    block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, al, acc, true);
+
+    // 3. the block's [M][128] sums: every wave's partials in shared memory (the stages are no longer read), the KW
+    // k slots added in order
     __syncthreads();
     float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int g = 0; g < MG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = g * 16 + 4 * G + i;
-                if (row < M) red[row * 128 + 32 * wave + 16 * j + c] = acc[j][g][i];
-            }
+    store_partials<MG>(red, M, acc);
     __syncthreads();
+    auto row_sum = [&](int r) {
+        float4 s4 = *reinterpret_cast<const float4*>(red + (size_t)r * 128 + 4 * l32);
+        for (int q = 1; q < KW; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(red + ((size_t)q * M + r) * 128 + 4 * l32);
+            s4.x += u.x; s4.y += u.y; s4.z += u.z; s4.w += u.w;
+        }
+        return s4;
+    };
 
     const uint16_t* svh = S.svh + cb_local * 128;
     const int ycol = S.col0 + cb_local * 128 + 4 * l32;
     if (a.SK == 1) {
-        for (int r = wave * 2 + half; r < M; r += 8) {
-            float v[4] = {red[r * 128 + 4 * l32], red[r * 128 + 4 * l32 + 1], red[r * 128 + 4 * l32 + 2],
-                          red[r * 128 + 4 * l32 + 3]};
+        for (int r = wave * 2 + half; r < M; r += 2 * NW) {
+            const float4 s4 = row_sum(r);
+            float v[4] = {s4.x, s4.y, s4.z, s4.w};
             finish(v, l32, svh, S.scale);
             store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
         }
         return;
     }
+    // 4. K splits: partials to Z, the last split of the block to arrive adds them in split order and finishes
     const size_t zrow = (size_t)a.NBT * 128;
-    for (int r = wave * 2 + half; r < M; r += 8) {
-        const float4 v = make_float4(red[r * 128 + 4 * l32], red[r * 128 + 4 * l32 + 1], red[r * 128 + 4 * l32 + 2],
-                                     red[r * 128 + 4 * l32 + 3]);
-        *reinterpret_cast<float4*>(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32) = v;
-    }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(a.counters + nbg, 1) == a.SK - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int r = wave * 2 + half; r < M; r += 8) {
-        const size_t at = (size_t)r * zrow + nbg * 128 + 4 * l32;
-        float4 s = *reinterpret_cast<const float4*>(a.Z + at);
-        for (int q = 1; q < a.SK; ++q) {
-            const float4 u = *reinterpret_cast<const float4*>(a.Z + (size_t)q * M * zrow + at);
+    for (int r = wave * 2 + half; r < M; r += 2 * NW)
+        store_dev4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
+    if (!arrive_last(a.counters + nbg, a.SK, &last)) return;
+    const size_t zsplit = (size_t)M * zrow;
+    for (int r = wave * 2 + half; r < M; r += 2 * NW) {
+        const float* zp = a.Z + (size_t)r * zrow + nbg * 128 + 4 * l32;
+        float4 s = load_dev4(zp);
+        int q = 1;
+        for (; q + 4 <= a.SK; q += 4) {                  // four splits' loads in flight at once
+            const float4 u0 = load_dev4(zp + q * zsplit), u1 = load_dev4(zp + (q + 1) * zsplit);
+            const float4 u2 = load_dev4(zp + (q + 2) * zsplit), u3 = load_dev4(zp + (q + 3) * zsplit);
+            s.x += u0.x; s.y += u0.y; s.z += u0.z; s.w += u0.w;
+            s.x += u1.x; s.y += u1.y; s.z += u1.z; s.w += u1.w;
+            s.x += u2.x; s.y += u2.y; s.z += u2.z; s.w += u2.w;
+            s.x += u3.x; s.y += u3.y; s.z += u3.z; s.w += u3.w;
+        }
+        for (; q < a.SK; ++q) {
+            const float4 u = load_dev4(zp + q * zsplit);
             s.x += u.x; s.y += u.y; s.z += u.z; s.w += u.w;
         }
         float v[4] = {s.x, s.y, s.z, s.w};
         finish(v, l32, svh, S.scale);
         store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
     }
-    if (threadIdx.x == 0) a.counters[nbg] = 0;             // every split of the block arrived
+    if (threadIdx.x == 0) store_dev(a.counters + nbg, 0);  // every split of the block arrived
 }
 
 template <int KCB, int K2, int MG>
-static int launch_dense(const DenseArgs& a, dim3 grid, size_t smem, hipStream_t st) {
+static int launch_dense(const DenseArgs& a, dim3 grid, int W, size_t smem, hipStream_t st) {
     auto kern = dense_kernel<KCB, K2, MG>;
     if (smem > 64 * 1024 &&
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "dense: cannot raise the shared memory limit to %zu bytes", smem);
-    kern<<<grid, 256, smem, st>>>(a);
+    kern<<<grid, 64 * W, smem, st>>>(a);
     return ESP_OK;
 }
 
@@ -361,13 +322,13 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
                          int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters,
                          int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
                          int64_t rot_smem, void* stream) {
-    (void)W;
     (void)PF;
     ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "1 to 4 matrices a launch");
     ESP_REQUIRE(M >= 1 && M <= 32, "1 to 32 rows");
     ESP_REQUIRE(SK >= 1 && K > 0 && K % (128 * SK) == 0 && (K / SK) % 32 == 0,
                 "K must split evenly over SK in 128s");
     ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "x / y dtype");
+    ESP_REQUIRE(W == 4 || W == 8 || W == 16, "W (waves a workgroup) must be 4, 8 or 16");
     ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "x / y row stride");
     if (!supported((int)cb, (int)k2))
         return esp_host::fail(ESP_ERR_UNSUPPORTED, "unsupported codebook/width: cb=%lld k2=%lld", (long long)cb,
@@ -413,8 +374,10 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
         int rc = esp_host::launch_check("dense rotation");
         if (rc) return rc;
     }
-    const size_t smem_x = fused ? (size_t)M * xs_stride * 2 : 0;
-    const size_t smem_red = (size_t)M * 128 * 4;
+    const size_t stage_bytes = (size_t)host_stage_words((int)k2, (int)kr) * 4;
+    a.stage_bytes = (int)stage_bytes;
+    const size_t smem_x = stage_bytes + (fused ? (size_t)M * xs_stride * 2 : 0);
+    const size_t smem_red = (size_t)(W / 4) * M * 128 * 4;
     const size_t smem = smem_x > smem_red ? smem_x : smem_red;
     ESP_REQUIRE(smem <= 160 * 1024, "dense: shared memory for the fused rotation exceeds 160 KiB");
     dim3 grid((unsigned)nbt, (unsigned)SK);
@@ -424,7 +387,8 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
 #define ESP_DENSE_CASE(CB_, K2_)                                                                           \
     case CB_ * 32 + K2_: {                                                                                 \
         constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                       \
-        rc = mg == 1 ? launch_dense<KCB, K2_, 1>(a, grid, smem, st) : launch_dense<KCB, K2_, 2>(a, grid, smem, st); \
+        rc = mg == 1 ? launch_dense<KCB, K2_, 1>(a, grid, (int)W, smem, st)                                 \
+                     : launch_dense<KCB, K2_, 2>(a, grid, (int)W, smem, st);                                \
         break;                                                                                             \
     }
         ESP_CASES(ESP_DENSE_CASE)

@@ -7,6 +7,7 @@
 // each member's rank as a popcount; otherwise each expert scans the picks in order.
 #include "common.hpp"
 #include "trellis.hpp"
+#include "gemm.hpp"
 #include "../../../include/espalier.h"
 
 namespace esp {
@@ -219,15 +220,10 @@ __global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
                 const double s = wave_sum_f64(acc[i][j]);
                 const int r = r0 + i, cc = c0 + j;
                 if (lane == 0 && r < a.R && cc < C)
-                    a.logits[(size_t)r * C + cc] = cc < a.E ? bf2f(f64_to_bf16(s)) : (float)s;
+                    store_dev(a.logits + (size_t)r * C + cc, cc < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
             }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (!arrive_last(a.counter, (int)gridDim.x, &last)) return;
 
     // 2. per row: top-k by logit (lowest id on ties), softmax weights over the picks, the shared gate's sigmoid
     for (int r = wave; r < a.R; r += GT / 64) {
@@ -236,7 +232,7 @@ __global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = lane + 64 * q;
-            l[q] = e < a.E ? __builtin_nontemporal_load(lr + e) : -INFINITY;
+            l[q] = e < a.E ? load_dev(lr + e) : -INFINITY;
         }
         float mx = 0.f, psum = 0.f;
         for (int t = 0; t < a.k; ++t) {
@@ -274,7 +270,7 @@ __global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
             for (int t = 0; t < a.k; ++t) a.wts_out[r * slots + t] = a.wts_out[r * slots + t] / psum;
             if (has) {
                 a.pick_out[r * slots + a.k] = a.shared_id;
-                a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-__builtin_nontemporal_load(lr + a.E)));
+                a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
             }
         }
     }
@@ -286,7 +282,7 @@ __global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
     for (int i = tid; i < n; i += GT) sh_pick[i] = a.pick_out[i];
     __syncthreads();
     group_block(sh_pick, n, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
-    if (tid == 0) *a.counter = 0;
+    if (tid == 0) store_dev(a.counter, 0);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -372,82 +368,43 @@ struct GroupedArgs {
 
 template <int CB, int K2, int MG>
 __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_t* __restrict__ T,
-                                             const uint16_t* __restrict__ X, const int* rows_sh, int mat, int split,
-                                             float scale) {
-    constexpr int TW = 4 * K2;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                                             const uint16_t* __restrict__ X, const int* rows_sh, int nrows, int mat,
+                                             int split, float scale, uint32_t* stage) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int c = lane & 15, G = lane >> 4;
+    const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
     const int NTILES = a.N >> 4;
-    const int nt_w = blockIdx.y * 8 + 2 * wave;
-    const int kr = a.K / a.SK, k0 = split * kr, steps = kr >> 5;
-    const LanePlan<K2> lp(lane);
-    const uint32_t* Tw = T + (size_t)nt_w * TW;
-    const size_t kstride = (size_t)NTILES * TW;
-    const int kt_base = (k0 >> 4) + (G >> 1);
-
-    bool rok[MG];
-    const uint16_t* xr[MG];
+    const int nt0 = blockIdx.y * 8;
+    const int kr = a.K / a.SK, k0 = split * kr;
+    RowsA<MG> al;
 #pragma unroll
     for (int g = 0; g < MG; ++g) {
         const int p = rows_sh[g * 16 + c];
-        rok[g] = p >= 0;
-        xr[g] = X + (size_t)(p >= 0 ? p : 0) * a.K + 16 * (G >> 1) + 4 * (G & 1);
+        al.row[g] = p >= 0 ? X + (size_t)p * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
     }
+    al.kbase = 0;
     f32x4 acc[2][MG];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    uint32_t wc[2][6], wn[2][6];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) load_words<K2>(Tw + (size_t)kt_base * kstride + j * TW, lp, wc[j]);
-    for (int st = 0; st < steps; ++st) {
-        if (st + 1 < steps) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                load_words<K2>(Tw + (size_t)(kt_base + 2 * (st + 1)) * kstride + j * TW, lp, wn[j]);
-        }
-        const int k = k0 + 32 * st;
-        f16x8 av[MG];
-#pragma unroll
-        for (int g = 0; g < MG; ++g) {
-            uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
-            if (rok[g]) {
-                lo = *reinterpret_cast<const uint2*>(xr[g] + k);
-                hi = *reinterpret_cast<const uint2*>(xr[g] + k + 8);
-            }
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-            const u32x4 t = {lo.x, lo.y, hi.x, hi.y};
-            av[g] = __builtin_bit_cast(f16x8, t);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const f16x8 b = decode_b<CB, K2>(wc[j], lp);
-#pragma unroll
-            for (int g = 0; g < MG; ++g)
-                acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
-        }
-        if (st + 1 < steps) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 6; ++i) wc[j][i] = wn[j][i];
-        }
-    }
+    block_gemm<CB, K2, MG>(T, NTILES, nt0, k0, kr, KW, stage, al, acc, false);
+    // the k slots' partials added in order, then one member row a 32-lane half
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(stage);
+    store_partials<MG>(red, nrows, acc);
+    __syncthreads();
     float* Zm = a.Z + ((size_t)mat * a.SK + split) * a.P * a.N;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int g = 0; g < MG; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = rows_sh[g * 16 + 4 * G + i];
-                if (p >= 0) Zm[(size_t)p * a.N + nt_w * 16 + 16 * j + c] = acc[j][g][i] * scale;
-            }
+    for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+        float4 s4 = *reinterpret_cast<const float4*>(red + (size_t)m * 128 + 4 * l32);
+        for (int q = 1; q < KW; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(red + ((size_t)q * nrows + m) * 128 + 4 * l32);
+            s4.x += u.x; s4.y += u.y; s4.z += u.z; s4.w += u.w;
+        }
+        s4.x *= scale; s4.y *= scale; s4.z *= scale; s4.w *= scale;
+        *reinterpret_cast<float4*>(Zm + (size_t)rows_sh[m] * a.N + nt0 * 16 + 4 * l32) = s4;
+    }
 }
 
-__global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
+__global__ __launch_bounds__(1024) void grouped_kernel(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
     const int u = blockIdx.x;
     if (u >= a.ucount[0]) return;
     const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
@@ -478,9 +435,9 @@ __global__ __launch_bounds__(256) void grouped_kernel(GroupedArgs a) {
         constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                          \
         const float scale = (CB_ == 6 || CB_ == 7) ? grid_c(CB_) : 1.0f;                                      \
         if (two)                                                                                              \
-            grouped_body<KCB, K2_, 2>(a, T, X, rows_sh, mat, split, scale);                                   \
+            grouped_body<KCB, K2_, 2>(a, T, X, rows_sh, nrows, mat, split, scale, stage);                                   \
         else                                                                                                  \
-            grouped_body<KCB, K2_, 1>(a, T, X, rows_sh, mat, split, scale);                                   \
+            grouped_body<KCB, K2_, 1>(a, T, X, rows_sh, nrows, mat, split, scale, stage);                                   \
         break;                                                                                                \
     }
         ESP_CASES(ESP_GROUPED_CASE)
@@ -739,7 +696,6 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
                            int64_t z_numel, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
                            int64_t nt, int64_t warps, int64_t pf, int64_t lo, int64_t hi, void* stream) {
     (void)nt;
-    (void)warps;
     (void)pf;
     ESP_REQUIRE(X0 && X1 && TP0 && TP1 && B0 && B1 && C0 && C1 && uids && ucount && members && Z,
                 "grouped: null pointer");
@@ -749,6 +705,7 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
     ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
+    ESP_REQUIRE(warps == 4 || warps == 8 || warps == 16, "warps (waves a workgroup) must be 4, 8 or 16");
     if (nexp_max <= 0) return esp_host::ok();
     GroupedArgs a{};
     a.X0 = static_cast<const uint16_t*>(X0);
@@ -770,7 +727,14 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.maxm = (int)maxm;
     a.slots = (int)slots;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK));
-    grouped_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    const size_t stage = (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;     // the widest expert's stages
+    const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
+    const size_t smem = stage > red ? stage : red;
+    if (smem > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+            hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "grouped: cannot raise the shared memory limit to %zu bytes", smem);
+    grouped_kernel<<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("grouped");
 }
 

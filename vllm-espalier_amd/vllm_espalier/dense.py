@@ -21,18 +21,25 @@ _scratch: dict = {}
 
 
 def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
-    """(K splits, waves, tiles in flight) for a K -> N layer of 128-column blocks, from its shape alone. A gfx950
-    workgroup is 4 waves on one 128-column block; K splits of at least 256 are added until there are about two
-    workgroups a CU (the reference's sm89 heuristic is dense.py:22-39). ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
+    """(K splits across workgroups SK, waves a workgroup W, tiles in flight) for a K -> N layer of 128-column
+    blocks, from its shape alone so a row's bits never depend on the batch. A gfx950 workgroup is 4 * KW waves on one
+    block, KW of them on every 32-k step column; the K range is split (KW * SK ways in all) until there are about 16
+    waves a CU or a wave would get fewer than 2 steps (the reference's sm89 heuristic is dense.py:22-39).
+    ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
     forced = env("ESPALIER_DENSE_TILE_PLAN")
     if forced:
         sk, w, pf = (int(v) for v in forced.split(","))
         return sk, w, pf
     nb = N // 128
-    sk = 1
-    while nb * sk < 2 * sms and K % (128 * sk * 2) == 0 and K // (sk * 2) >= 256:
-        sk *= 2
-    return sk, 4, 2
+    steps = K // 32
+    splits = 1
+    while nb * 4 * splits < 16 * sms and steps // (2 * splits) >= 2:
+        kw = min(4, 2 * splits)
+        if K % (128 * (2 * splits // kw)):
+            break
+        splits *= 2
+    kw = min(4, splits)
+    return splits // kw, 4 * kw, 2
 
 
 def scratch(device, z_floats: int, xh_halves: int):

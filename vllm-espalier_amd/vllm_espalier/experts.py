@@ -73,17 +73,18 @@ def ext():
 
 
 def tile_config(K: int, N: int, gateup: bool) -> tuple[int, int, int, int]:
-    """(n tiles a block, waves, K splits, tiles in flight) for a K -> N projection, from the shape alone so a row's
-    bits never depend on the batch. The gfx950 kernel gives each 4-wave workgroup 128 columns over K / SK; K splits
-    of 256 keep a few workgroups a CU at one token. The reference's sm89 choices are experts.py:59-68."""
-    if N % 128:
+    """(n tiles a block, waves a workgroup, K splits across workgroups, tiles in flight) for a K -> N projection, from
+    the shape alone so a row's bits never depend on the batch. A gfx950 workgroup is 4 * KW waves on 128 columns; the
+    K range is split KW * SK ways (up to 16, at least 2 32-k steps a wave) so that the handful of experts one token
+    picks still keeps every CU busy. The reference's sm89 choices are experts.py:59-68."""
+    if N % 128 or K % 32:
         raise ValueError(f"no tile setting divides K={K}, N={N}")
-    sk = 1
-    while sk < 8 and K % (32 * sk * 2) == 0 and K // (sk * 2) >= 256:
-        sk *= 2
-    if K % (32 * sk):
-        raise ValueError(f"no tile setting divides K={K}, N={N}")
-    return 8, 4, sk, 2
+    steps = K // 32
+    splits = 1
+    while splits < 16 and steps // (2 * splits) >= 2 and K % (32 * (2 * splits // min(4, 2 * splits))) == 0:
+        splits *= 2
+    kw = min(4, splits)
+    return 8, 4 * kw, splits // kw, 2
 
 
 @dataclass

@@ -17,18 +17,21 @@ GRID = {"mcg": 0, "e2m1": 1, "int5": 3, "int6": 4}
 
 
 def matrix_tensors(K: int, N: int, bits: int, grid: str, gen: torch.Generator) -> dict[str, torch.Tensor]:
+    """The tensors on gen's device (a CPU generator gives device-independent bytes; a device generator is fast for
+    the benchmarks' gigabyte weight stacks)."""
     if K % 16 or N % 16:
         raise ValueError("K and N must be multiples of 16")
-    t = torch.randint(-32768, 32768, (K // 16, N // 16, 16 * bits), dtype=torch.int32, generator=gen)
+    dev = gen.device
+    t = torch.randint(-32768, 32768, (K // 16, N // 16, 16 * bits), dtype=torch.int32, generator=gen, device=dev)
     trellis = t.to(torch.int16)
-    suh = (torch.randint(0, 2, (K,), generator=gen) * 2 - 1).to(torch.float16)
-    sign = (torch.randint(0, 2, (N,), generator=gen) * 2 - 1).to(torch.float32)
-    scale = torch.exp(torch.randn((N,), generator=gen) * 0.25)
+    suh = (torch.randint(0, 2, (K,), generator=gen, device=dev) * 2 - 1).to(torch.float16)
+    sign = (torch.randint(0, 2, (N,), generator=gen, device=dev) * 2 - 1).to(torch.float32)
+    scale = torch.exp(torch.randn((N,), generator=gen, device=dev) * 0.25)
     svh = (sign * scale).to(torch.float16)
-    d = {"esp_trellis": trellis, "suh": suh, "svh": svh, "mcg": torch.zeros(1, dtype=torch.int32)}
+    d = {"esp_trellis": trellis, "suh": suh, "svh": svh, "mcg": torch.zeros(1, dtype=torch.int32, device=dev)}
     code = GRID[grid]
     if code:
-        d["esp_grid"] = torch.tensor([code], dtype=torch.int32)
+        d["esp_grid"] = torch.tensor([code], dtype=torch.int32, device=dev)
     return d
 
 
