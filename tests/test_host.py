@@ -1,0 +1,104 @@
+"""Host-side logic of the package on the CPU: launch plans, tile settings, launch grouping, checkpoint parsing and
+the expert tables. Nothing here calls a kernel."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from vllm_espalier import dense as D
+from vllm_espalier import experts as X
+from vllm_espalier import workloads as WL
+from vllm_espalier.matrix import EspMatrix
+
+# BASELINE shapes (K, N): config 1, the config-2 launches, the config-5 head
+SHAPES = [(2048, 2048), (2048, 5120), (4096, 2048), (2048, 1024), (512, 2048), (2048, 151936)]
+
+
+def test_tables_match_the_oracle():
+    assert X.KERNEL_CB == O.KERNEL_CB
+    assert X.COMPILED == O.COMPILED
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_dense_plan_is_valid(K, N):
+    sk, w, pf = D.plan(K, N, 256)
+    assert w in (4, 8, 16) and sk >= 1
+    assert K % (128 * sk) == 0                            # the fused rotation works in 128-wide chunks
+    assert (K // sk) // 32 >= 2 * (w // 4) or (sk == 1 and w == 4)   # every wave has at least two 32-k steps
+    assert (N // 128) * sk * w <= 16 * 256 * 2            # about 16 waves a CU, at most one doubling past it
+
+
+def test_dense_plan_depends_on_shape_only(monkeypatch):
+    assert D.plan(2048, 5120, 256) == D.plan(2048, 5120, 256)
+    monkeypatch.setenv("ESPALIER_DENSE_TILE_PLAN", "2,8,1")
+    assert D.plan(2048, 5120, 256) == (2, 8, 1)
+
+
+@pytest.mark.parametrize("K,N", [(2048, 512), (512, 2048), (2048, 1024), (4096, 4096)])
+def test_tile_config_is_valid(K, N):
+    nt, w, sk, pf = X.tile_config(K, N, True)
+    assert nt == 8 and w in (4, 8, 16) and sk >= 1
+    assert K % (32 * sk) == 0 and (K // sk) // 32 >= (w // 4)
+
+
+def test_tile_config_rejects_ragged():
+    with pytest.raises(ValueError):
+        X.tile_config(2048, 500, True)
+
+
+def _mat(K, N, bits, grid, seed=0):
+    return WL.matrix(K, N, bits, grid, torch.Generator().manual_seed(seed), "cpu")
+
+
+def test_dense_groups_launches_by_codebook_and_width():
+    mats = [_mat(256, 128, 4, "int6"), _mat(256, 256, 4, "int6"), _mat(256, 128, 4, "int5"),
+            _mat(256, 128, 3, "int5"), _mat(256, 128, 3, "int5")]
+    d = D.Dense(mats)
+    assert [(g[0], g[1], g[2]) for g in d.groups] == [([0, 1], 8, 7), ([2], 8, 6), ([3, 4], 6, 6)]
+    assert d.col0 == [0, 128, 384, 512, 640] and d.N == 768
+    six = D.Dense([_mat(256, 128, 4, "int6", s) for s in range(6)])
+    assert [len(g[0]) for g in six.groups] == [4, 2]      # at most 4 matrices a launch
+    with pytest.raises(ValueError):
+        D.Dense([_mat(256, 128, 4, "int6"), _mat(512, 128, 4, "int6")])
+
+
+def test_espmatrix_codebook_markers():
+    t = WL.matrix_tensors(32, 32, 2, "mcg", torch.Generator().manual_seed(1))
+    assert EspMatrix(t).cb == 0
+    assert EspMatrix({**t, "mul1": torch.zeros(1)}).cb == 1
+    assert EspMatrix({**t, "esp_grid": torch.tensor([4], dtype=torch.int32)}).cb == 4
+    with pytest.raises(ValueError):
+        EspMatrix({k: v for k, v in t.items() if k != "mcg"})
+    with pytest.raises(ValueError):
+        EspMatrix({**t, "esp_grid": torch.tensor([7], dtype=torch.int32)})
+    bad = dict(t)
+    bad["esp_trellis"] = t["esp_trellis"][:1]
+    with pytest.raises(ValueError):
+        EspMatrix(bad)
+
+
+def test_workload_bytes_and_determinism():
+    a = WL.matrix_tensors(2048, 2048, 4, "int6", torch.Generator().manual_seed(3))
+    b = WL.matrix_tensors(2048, 2048, 4, "int6", torch.Generator().manual_seed(3))
+    assert all(torch.equal(a[k], b[k]) for k in a)
+    m = EspMatrix(a)
+    assert WL.nbytes([m]) == 2105344                      # config 1's algorithmic bytes
+    s = a["suh"].float()
+    assert torch.all(s.abs() == 1)
+
+
+def test_prepare_tables():
+    E, Dm, I = 3, 256, 128
+    exps = [tuple(_mat(k, n, b, g, 10 * e + j) for j, (k, n) in enumerate([(Dm, I), (Dm, I), (I, Dm)]))
+            for e, (b, g) in enumerate([(1, "e2m1"), (2, "e2m1"), (3, "int5")])]
+    shared = tuple(_mat(k, n, 4, "int6", 99 + j) for j, (k, n) in enumerate([(Dm, I), (Dm, I), (I, Dm)]))
+    L = X.prepare(exps, shared, gate_w=torch.zeros(Dm, dtype=torch.bfloat16))
+    assert L.E == 4 and L.shared_id == 3 and (L.D, L.I) == (Dm, I)
+    assert L.k2[0].tolist() == [2, 4, 6, 8] and L.cb[0].tolist() == [3, 3, 6, 7]
+    assert L.k2_gu == (2, 8)
+    assert L.ptr[2][1].item() == exps[1][2].trellis.data_ptr()
+    # suh/svh rebound as rows of the stacks
+    assert exps[2][0].suh.data_ptr() == L.suh_g[2].data_ptr()
+    bad = [tuple(_mat(k, n, 4, "e2m1", j) for j, (k, n) in enumerate([(Dm, I), (Dm, I), (I, Dm)]))]
+    with pytest.raises(NotImplementedError):
+        X.prepare(bad)                                    # E2M1 has no 4-bit instance
