@@ -137,10 +137,9 @@ __global__ __launch_bounds__(256) void dense_rot_kernel(DenseArgs a, uint16_t* _
 }
 
 // the finished outputs of one row's 128 columns from their fp32 sums, 4 a lane: H / sqrt(128), * c, * svh
-// (dense.cu:120-128)
-__device__ __forceinline__ void finish(float (&v)[4], int l32, const uint16_t* svh, float scale) {
+// (dense.cu:120-128); sv holds the lane's 4 svh values (fp16 bits), loaded when the workgroup starts
+__device__ __forceinline__ void finish(float (&v)[4], int l32, uint2 sv, float scale) {
     fwht128(v, l32);
-    const uint2 sv = *reinterpret_cast<const uint2*>(svh + 4 * l32);
     const float s[4] = {h2f((uint16_t)(sv.x & 0xFFFFu)), h2f((uint16_t)(sv.x >> 16)), h2f((uint16_t)(sv.y & 0xFFFFu)),
                         h2f((uint16_t)(sv.y >> 16))};
 #pragma unroll
@@ -169,7 +168,8 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
 
-    // 0. the first stage of trellis copies, in flight while the input rows are rotated
+    // 0. the first stage of trellis copies, in flight while the input rows are rotated; the block's output scales
+    const uint2 sv = *reinterpret_cast<const uint2*>(S.svh + cb_local * 128 + 4 * l32);
     {
         const int steps = kr >> 5;
         const int sst = steps < StagePlan<K2>::MAX_STEPS ? steps : StagePlan<K2>::MAX_STEPS;
@@ -221,13 +221,12 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         return s4;
     };
 
-    const uint16_t* svh = S.svh + cb_local * 128;
     const int ycol = S.col0 + cb_local * 128 + 4 * l32;
     if (a.SK == 1) {
         for (int r = wave * 2 + half; r < M; r += 2 * NW) {
             const float4 s4 = row_sum(r);
             float v[4] = {s4.x, s4.y, s4.z, s4.w};
-            finish(v, l32, svh, S.scale);
+            finish(v, l32, sv, S.scale);
             store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
         }
         return;
@@ -240,22 +239,23 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const size_t zsplit = (size_t)M * zrow;
     for (int r = wave * 2 + half; r < M; r += 2 * NW) {
         const float* zp = a.Z + (size_t)r * zrow + nbg * 128 + 4 * l32;
-        float4 s = load_dev4(zp);
-        int q = 1;
-        for (; q + 4 <= a.SK; q += 4) {                  // four splits' loads in flight at once
-            const float4 u0 = load_dev4(zp + q * zsplit), u1 = load_dev4(zp + (q + 1) * zsplit);
-            const float4 u2 = load_dev4(zp + (q + 2) * zsplit), u3 = load_dev4(zp + (q + 3) * zsplit);
-            s.x += u0.x; s.y += u0.y; s.z += u0.z; s.w += u0.w;
-            s.x += u1.x; s.y += u1.y; s.z += u1.z; s.w += u1.w;
-            s.x += u2.x; s.y += u2.y; s.z += u2.z; s.w += u2.w;
-            s.x += u3.x; s.y += u3.y; s.z += u3.z; s.w += u3.w;
-        }
-        for (; q < a.SK; ++q) {
-            const float4 u = load_dev4(zp + q * zsplit);
-            s.x += u.x; s.y += u.y; s.z += u.z; s.w += u.w;
+        float4 s;
+        for (int q0 = 0; q0 < a.SK; q0 += 8) {             // up to eight splits' loads in flight at once
+            float4 u[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (q0 + i < a.SK) u[i] = load_dev4(zp + (q0 + i) * zsplit);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (q0 + i == 0) {
+                    s = u[0];                                  // split 0 starts the sum (dense.cu:223-233)
+                } else if (q0 + i < a.SK) {
+                    s.x += u[i].x; s.y += u[i].y; s.z += u[i].z; s.w += u[i].w;
+                }
+            }
         }
         float v[4] = {s.x, s.y, s.z, s.w};
-        finish(v, l32, svh, S.scale);
+        finish(v, l32, sv, S.scale);
         store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
     }
     if (threadIdx.x == 0) store_dev(a.counters + nbg, 0);  // every split of the block arrived

@@ -96,14 +96,29 @@ __device__ __forceinline__ uint32_t mcg_pair(uint32_t s0, uint32_t s1) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// mcg value of one state: the two halves of its hash added in one RNE fp16 add (a v_add_f16 reading the high half
+// through SDWA), in the low half of the register
+__device__ __forceinline__ _Float16 mcg_one(uint32_t s) {
+    const f16x2 h = __builtin_bit_cast(f16x2, mcg_hash(s));
+    return h[0] + h[1];
+}
+
+// f32(v) * k with one rounding, v read as fp16 by v_fma_mix_f32 (no separate conversion); the +0 addend leaves every
+// product unchanged (v is never -0: the sum of two opposite halves is +0)
+__device__ __forceinline__ float mul_mix(_Float16 v, float k) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(v), "v"(k));
+    return r;
+}
+
 // Codebook value pair. CB: 1 mcg; 3 E2M1 snap; 6 / 7 fp16(q * c) on the int5 / int6 grid; 22 / 23 the grid index q
 // itself (fp16, exact), whose sums the caller scales by c.
 template <int CB>
 __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
-    const uint32_t m = mcg_pair(s0, s1);
     if constexpr (CB == 1) {
-        return m;
+        return mcg_pair(s0, s1);
     } else if constexpr (CB == 3) {
+        const uint32_t m = mcg_pair(s0, s1);
         // E2M1 (experts_grouped.cuh:25-38): |v| against 0.75 * {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5}, summing the grid
         // steps, then v's sign. Each step is clamp((|v| - t) * 2^14, 0, 1): |v| > t by at least one fp16 ulp of t gives
         // >= 2, so the step is exactly 0 or 1, and every partial sum is exact in fp16.
@@ -125,8 +140,7 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
     } else {
         static_assert(CB == 6 || CB == 7 || CB == 22 || CB == 23, "codebook");
         constexpr float k = (CB == 6 || CB == 22) ? GRID_K5 : GRID_K6;
-        const f16x2 v = __builtin_bit_cast(f16x2, m);
-        const float q0 = __builtin_rintf((float)v[0] * k), q1 = __builtin_rintf((float)v[1] * k);
+        const float q0 = __builtin_rintf(mul_mix(mcg_one(s0), k)), q1 = __builtin_rintf(mul_mix(mcg_one(s1), k));
         if constexpr (CB == 22 || CB == 23) {
             const f16x2 r = {(_Float16)q0, (_Float16)q1};           // |q| <= 31: exact
             return __builtin_bit_cast(uint32_t, r);
