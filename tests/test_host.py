@@ -25,7 +25,7 @@ def test_dense_plan_is_valid(K, N):
     assert w in (4, 8, 16) and sk >= 1
     assert K % (128 * sk) == 0                            # the fused rotation works in 128-wide chunks
     assert (K // sk) // 32 >= 2 * (w // 4) or (sk == 1 and w == 4)   # every wave has at least two 32-k steps
-    assert (N // 128) * sk * w <= 16 * 256 * 2            # about 16 waves a CU, at most one doubling past it
+    assert (N // 128) * sk <= max(N // 128, 256)          # the splits keep to a workgroup a CU
 
 
 def test_dense_plan_depends_on_shape_only(monkeypatch):

@@ -99,20 +99,49 @@ __device__ __forceinline__ void fwht128(float (&v)[4], int lane32) {
 }
 
 // fp16 H(x * suh) / sqrt(128) of the 128 values of x starting at xi (dtype), 4 a lane of a 32-lane half; the multiply
-// is never contracted into the butterfly (dense.cu:92-108)
-__device__ __forceinline__ uint2 rot128(const void* x, int x_dtype, size_t xi, const uint16_t* suh, int lane32) {
+// is never contracted into the butterfly (dense.cu:92-108). Split into the loads (RotIn) and the arithmetic, so a
+// caller can put the loads in flight before other memory work.
+struct RotIn {
+    uint4 raw;       // the 4 elements' bits: 4 floats, or 4 halves in raw.x, raw.y
+    uint2 su;
+};
+
+__device__ __forceinline__ RotIn rot128_load(const void* x, int x_dtype, size_t xi, const uint16_t* suh, int lane32) {
+    RotIn r;
+    if (x_dtype == F32) {
+        r.raw = *reinterpret_cast<const uint4*>(static_cast<const float*>(x) + xi + 4 * lane32);
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(x) + xi + 4 * lane32);
+        r.raw = make_uint4(u.x, u.y, 0u, 0u);
+    }
+    r.su = *reinterpret_cast<const uint2*>(suh + 4 * lane32);
+    return r;
+}
+
+__device__ __forceinline__ uint2 rot128_apply(RotIn r, int x_dtype, int lane32) {
     float v[4];
-    load4(x, x_dtype, xi + 4 * lane32, v);
-    const uint2 su = *reinterpret_cast<const uint2*>(suh + 4 * lane32);
-    v[0] = __fmul_rn(v[0], h2f((uint16_t)(su.x & 0xFFFFu)));
-    v[1] = __fmul_rn(v[1], h2f((uint16_t)(su.x >> 16)));
-    v[2] = __fmul_rn(v[2], h2f((uint16_t)(su.y & 0xFFFFu)));
-    v[3] = __fmul_rn(v[3], h2f((uint16_t)(su.y >> 16)));
+    if (x_dtype == F32) {
+        v[0] = __builtin_bit_cast(float, r.raw.x); v[1] = __builtin_bit_cast(float, r.raw.y);
+        v[2] = __builtin_bit_cast(float, r.raw.z); v[3] = __builtin_bit_cast(float, r.raw.w);
+    } else {
+        const uint16_t h[4] = {(uint16_t)(r.raw.x & 0xFFFFu), (uint16_t)(r.raw.x >> 16), (uint16_t)(r.raw.y & 0xFFFFu),
+                               (uint16_t)(r.raw.y >> 16)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = x_dtype == BF16 ? bf2f(h[j]) : h2f(h[j]);
+    }
+    v[0] = __fmul_rn(v[0], h2f((uint16_t)(r.su.x & 0xFFFFu)));
+    v[1] = __fmul_rn(v[1], h2f((uint16_t)(r.su.x >> 16)));
+    v[2] = __fmul_rn(v[2], h2f((uint16_t)(r.su.y & 0xFFFFu)));
+    v[3] = __fmul_rn(v[3], h2f((uint16_t)(r.su.y >> 16)));
     fwht128(v, lane32);
     uint2 u;
     u.x = (uint32_t)f2h(v[0] * HAD_SCALE) | ((uint32_t)f2h(v[1] * HAD_SCALE) << 16);
     u.y = (uint32_t)f2h(v[2] * HAD_SCALE) | ((uint32_t)f2h(v[3] * HAD_SCALE) << 16);
     return u;
+}
+
+__device__ __forceinline__ uint2 rot128(const void* x, int x_dtype, size_t xi, const uint16_t* suh, int lane32) {
+    return rot128_apply(rot128_load(x, x_dtype, xi, suh, lane32), x_dtype, lane32);
 }
 
 // ---- hand-off of partial results between workgroups ----

@@ -20,6 +20,8 @@
 namespace esp {
 
 constexpr int MAX_SHARDS = 4;
+constexpr int CNT_STRIDE = 32;   // ints between two column blocks' arrival counters: one 128-byte line each, so the
+                                 // splits of different blocks never queue on one line's atomics
 
 struct Shard {
     const uint32_t* T;       // trellis words [K/16][N/16][4*K2]
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const size_t zrow = (size_t)a.NBT * 128;
     for (int r = wave * 2 + half; r < M; r += 2 * NW)
         store_dev4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
-    if (!arrive_last(a.counters + nbg, a.SK, &last)) return;
+    if (!arrive_last(a.counters + (size_t)nbg * CNT_STRIDE, a.SK, &last)) return;
     const size_t zsplit = (size_t)M * zrow;
     for (int r = wave * 2 + half; r < M; r += 2 * NW) {
         const float* zp = a.Z + (size_t)r * zrow + nbg * 128 + 4 * l32;
@@ -258,7 +260,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         finish(v, l32, sv, S.scale);
         store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
     }
-    if (threadIdx.x == 0) store_dev(a.counters + nbg, 0);  // every split of the block arrived
+    if (threadIdx.x == 0) store_dev(a.counters + (size_t)nbg * CNT_STRIDE, 0);  // every split of the block arrived
 }
 
 template <int KCB, int K2, int MG>
@@ -346,8 +348,8 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
         nbt += (int)(N / 128);
     }
     a.n = (int)n_shards;
-    ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= nbt),
-                "scratch too small");
+    ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= (int64_t)nbt * CNT_STRIDE),
+                "scratch too small: Z needs SK*M*N floats, counters 32 per 128 columns");
     const int64_t kr = K / SK;
     const int xs_stride = (int)kr + 8;                        // pad rows across the LDS banks
     const bool fused = M * kr * 2 <= rot_smem;

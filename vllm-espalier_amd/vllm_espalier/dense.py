@@ -16,30 +16,29 @@ from .experts import KERNEL_CB, ext
 from ._env import env
 
 MAX_ROWS = 32
+COUNTER_STRIDE = 32          # ints between two 128-column blocks' arrival counters (one 128-byte line each)
 ROT_SMEM = int(os.environ.get("ESPALIER_DENSE_ROTATION_SMEM", 64 * 1024))   # fuse the input rotation up to this much LDS
 _scratch: dict = {}
 
 
 def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
-    """(K splits across workgroups SK, waves a workgroup W, tiles in flight) for a K -> N layer of 128-column
-    blocks, from its shape alone so a row's bits never depend on the batch. A gfx950 workgroup is 4 * KW waves on one
-    block, KW of them on every 32-k step column; the K range is split (KW * SK ways in all) until there are about 16
-    waves a CU or a wave would get fewer than 2 steps (the reference's sm89 heuristic is dense.py:22-39).
+    """(K splits SK, waves a workgroup W, tiles in flight) for a K -> N layer of 128-column blocks, from its shape
+    alone so a row's bits never depend on the batch (the reference's sm89 heuristic is dense.py:22-39). A gfx950
+    workgroup is 4 * KW waves on one block, KW of them on every 32-k step column. From cold sweeps on MI355X at one
+    row (the decode case): the most splits that keep a workgroup a CU at most, then 16 waves when a workgroup has 8
+    steps or more, 8 from 4, else 4.
     ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
     forced = env("ESPALIER_DENSE_TILE_PLAN")
     if forced:
         sk, w, pf = (int(v) for v in forced.split(","))
         return sk, w, pf
     nb = N // 128
-    steps = K // 32
-    splits = 1
-    while nb * 4 * splits < 16 * sms and steps // (2 * splits) >= 2:
-        kw = min(4, 2 * splits)
-        if K % (128 * (2 * splits // kw)):
-            break
-        splits *= 2
-    kw = min(4, splits)
-    return splits // kw, 4 * kw, 2
+    sk = 1
+    while nb * sk * 2 <= sms and K % (128 * sk * 2) == 0:
+        sk *= 2
+    steps = K // (32 * sk)
+    w = 16 if steps >= 8 else 8 if steps >= 4 else 4
+    return sk, w, 2
 
 
 def scratch(device, z_floats: int, xh_halves: int):
@@ -91,7 +90,7 @@ class Dense:
             self.plans.append(p)
             nbt_max = max(nbt_max, n // 128)
             z = max(z, p[0] * MAX_ROWS * n)
-        self.counters = torch.zeros(2 * nbt_max, dtype=torch.int32, device=dev)
+        self.counters = torch.zeros(COUNTER_STRIDE * nbt_max, dtype=torch.int32, device=dev)
         scratch(dev, z, 4 * MAX_ROWS * self.K)
 
     def forward(self, x, trellis=None, suh=None, svh=None, out=None):
