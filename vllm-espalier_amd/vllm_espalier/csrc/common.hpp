@@ -98,6 +98,46 @@ __device__ __forceinline__ void fwht128(float (&v)[4], int lane32) {
     fwht_stage<16>(v, lane32);
 }
 
+// ---- wave64 reductions through DPP (no LDS round trips) ----
+// The total lands in lane 63: pairs and quads (quad_perm), 8-lane halves (row_half_mirror), 16-lane rows
+// (row_mirror), then rows 1 and 3 take row 0 and 2's totals (row_bcast:15) and row 3 takes rows 0-1's
+// (row_bcast:31). Lanes outside a step's row mask add the identity (the `old` operand).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t identity) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)u, 0u), hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(u >> 32), 0u);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);    // +0.0 where the row mask excludes the lane
+}
+
+// the wave's sum, in every lane (fp64: exact whenever the partial sums are, whatever the order)
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+    v += dpp_f64<0xB1>(v);            // quad_perm [1,0,3,2]
+    v += dpp_f64<0x4E>(v);            // quad_perm [2,3,0,1]
+    v += dpp_f64<0x141>(v);           // row_half_mirror
+    v += dpp_f64<0x140>(v);           // row_mirror
+    v += dpp_f64<0x142, 0xA>(v);      // row_bcast:15 into rows 1, 3
+    v += dpp_f64<0x143, 0xC>(v);      // row_bcast:31 into rows 2, 3
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, 63), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// the wave's maximum (unsigned), in every lane
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    uint32_t o;
+    o = dpp_u32<0xB1>(v, 0u);       v = v > o ? v : o;
+    o = dpp_u32<0x4E>(v, 0u);       v = v > o ? v : o;
+    o = dpp_u32<0x141>(v, 0u);      v = v > o ? v : o;
+    o = dpp_u32<0x140>(v, 0u);      v = v > o ? v : o;
+    o = dpp_u32<0x142, 0xA>(v, 0u); v = v > o ? v : o;
+    o = dpp_u32<0x143, 0xC>(v, 0u); v = v > o ? v : o;
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // fp16 H(x * suh) / sqrt(128) of the 128 values of x starting at xi (dtype), 4 a lane of a 32-lane half; the multiply
 // is never contracted into the butterfly (dense.cu:92-108). Split into the loads (RotIn) and the arithmetic, so a
 // caller can put the loads in flight before other memory work.

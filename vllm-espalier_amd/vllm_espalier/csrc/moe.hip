@@ -19,17 +19,21 @@ constexpr int MAX_GROUP_IDS = 4096;     // ids the grouping covers (experts.cu:4
 // ------------------------------------------------------------------------------------------------------------------
 // block-level grouping of sh_pick[0..n) (shared memory) over ids [0, nid)
 // ------------------------------------------------------------------------------------------------------------------
-struct GroupSmem {
-    int cnt[MAX_GROUP_IDS];
-    unsigned mask[MAX_GROUP_IDS];
-    int place[MAX_GROUP_IDS];
-    int wave_tot[GT / 64];
+template <int NID>
+struct GroupSmemT {
+    int cnt[NID];
+    unsigned mask[NID];
+    int place[NID];
+    int wave_tot[16];
     int dup;
 };
+typedef GroupSmemT<MAX_GROUP_IDS> GroupSmem;
 
+template <typename GS>
 __device__ void group_block(const int* sh_pick, int n, int R, int slots, int nid, int maxm, int* __restrict__ uids,
-                            int* __restrict__ ucount, int* __restrict__ members, GroupSmem& g) {
+                            int* __restrict__ ucount, int* __restrict__ members, GS& g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int GT = (int)blockDim.x;                     // the workgroup's threads (up to 1024)
     for (int e = tid; e < nid; e += GT) {
         g.cnt[e] = 0;
         g.mask[e] = 0u;
@@ -121,11 +125,6 @@ __device__ __forceinline__ void load4_16(const uint16_t* p, int bf16, double (&v
     for (int j = 0; j < 4; ++j) v[j] = (double)(bf16 ? bf2f(h[j]) : h2f(h[j]));
 }
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // bf16 bits of a double, one rounding (to nearest, ties to even)
 __device__ __forceinline__ uint16_t f64_to_bf16(double d) {
@@ -158,8 +157,13 @@ __device__ __forceinline__ uint16_t f64_to_bf16(double d) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// route_group (route.cu:35-181): every wave computes router logits (4 rows x 4 columns a wave tile, fp64), the last
-// block to arrive does top-k / weights / shared gate per row (one wave a row) and the grouping.
+// route_group (route.cu:35-181). Workgroups of 16 waves; wave w of workgroup b computes router column
+// c = 4b + (w & 3) (an expert, or the shared gate) for rows r = w >> 2, + 4, ...: each lane takes 8 consecutive h a
+// 512-wide chunk, exact fp64 products and sums (bf16 x bf16 products are exact in fp64; the sums are exact for
+// ordinary data), a DPP reduction across the wave, one rounding to bf16. The last workgroup to arrive (relaxed
+// device-scope counter) ranks each row's experts with one 32-bit key (the logit's bf16 bits made order-preserving,
+// then 0xFFFF - id, so the wave maximum is the largest logit with the lowest id on ties), takes k maxima, the
+// softmax over the picks and the shared gate's sigmoid, and groups the picks.
 // ------------------------------------------------------------------------------------------------------------------
 struct RouteArgs {
     const uint16_t* x;
@@ -175,113 +179,144 @@ struct RouteArgs {
     int x_stride, bf16, R, H, E, k, shared_id, maxm;
 };
 
-constexpr int RT_ROWS = 4, RT_COLS = 4;
+constexpr int RT = 1024;             // threads of a route workgroup
+constexpr int RT_COLS = 4;           // router columns a workgroup
+constexpr int RT_MAX_IDS = 512;      // ids the routing's grouping covers (E + 1 <= 257)
 
-__global__ __launch_bounds__(GT) void route_group_kernel(RouteArgs a) {
+__device__ __forceinline__ double bits16_to_f64(uint32_t h, int bf16) {
+    return bf16 ? (double)bf2f((uint16_t)h) : (double)h2f((uint16_t)h);
+}
+
+// order-preserving unsigned key of a bf16 value (held as the high half of an fp32): larger value, larger key
+__device__ __forceinline__ uint32_t bf16_order(float v) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, v) >> 16;
+    return (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+}
+__device__ __forceinline__ float bf16_unorder(uint32_t k) {
+    const uint32_t h = (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu);
+    return __builtin_bit_cast(float, h << 16);
+}
+
+template <int BF16>
+__global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     __shared__ int last;
     __shared__ int sh_pick[MAX_PICKS];
-    __shared__ GroupSmem g;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ GroupSmemT<RT_MAX_IDS> g;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int has = a.shared_id >= 0, C = a.E + has, slots = a.k + has;
-    const int rtiles = (a.R + RT_ROWS - 1) / RT_ROWS, ctiles = (C + RT_COLS - 1) / RT_COLS;
 
-    // 1. logits
-    for (int t = blockIdx.x * (GT / 64) + wave; t < rtiles * ctiles; t += gridDim.x * (GT / 64)) {
-        const int r0 = (t / ctiles) * RT_ROWS, c0 = (t % ctiles) * RT_COLS;
-        double acc[RT_ROWS][RT_COLS];
+    // 1. logits: column c, rows rg, rg + 4, ...; h in groups of 2048 (4 chunks of 8 a lane). The gate's chunks stay
+    // in registers across the rows and the next row's x is in flight while the current row is summed.
+    {
+        const int c = blockIdx.x * RT_COLS + (wave & 3), rg = wave >> 2;
+        if (c < C && rg < a.R) {
+            const uint16_t* w = c < a.E ? a.gate + (size_t)c * a.H : a.sgate;
+            auto load8 = [&](const uint16_t* p, int h, uint2 (&v)[2]) __attribute__((always_inline)) {
+                if (h < a.H) {
+                    v[0] = *reinterpret_cast<const uint2*>(p + h);
+                    v[1] = *reinterpret_cast<const uint2*>(p + h + 4);
+                } else {
+                    v[0] = v[1] = make_uint2(0u, 0u);
+                }
+            };
+            auto dot = [&](const uint2 (&xv)[4][2], const uint2 (&gv)[4][2], double acc) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < RT_ROWS; ++i)
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t gw[4] = {gv[q][0].x, gv[q][0].y, gv[q][1].x, gv[q][1].y};
+                    const uint32_t xw[4] = {xv[q][0].x, xv[q][0].y, xv[q][1].x, xv[q][1].y};
 #pragma unroll
-            for (int j = 0; j < RT_COLS; ++j) acc[i][j] = 0.0;
-        for (int h = 4 * lane; h < a.H; h += 256) {
-            double xv[RT_ROWS][4], wv[RT_COLS][4];
+                    for (int j = 0; j < 4; ++j) {
+                        acc = __builtin_fma(bits16_to_f64(xw[j] & 0xFFFFu, BF16), bits16_to_f64(gw[j] & 0xFFFFu, BF16), acc);
+                        acc = __builtin_fma(bits16_to_f64(xw[j] >> 16, BF16), bits16_to_f64(gw[j] >> 16, BF16), acc);
+                    }
+                }
+                return acc;
+            };
+            uint2 gv[4][2], xv[4][2], xn[4][2];
+            if (a.H <= 2048) {
 #pragma unroll
-            for (int i = 0; i < RT_ROWS; ++i) {
-                const int r = r0 + i < a.R ? r0 + i : a.R - 1;
-                load4_16(a.x + (size_t)r * a.x_stride + h, a.bf16, xv[i]);
+                for (int q = 0; q < 4; ++q) {
+                    load8(w, 512 * q + 8 * lane, gv[q]);
+                    load8(a.x + (size_t)rg * a.x_stride, 512 * q + 8 * lane, xv[q]);
+                }
+                for (int r = rg; r < a.R; r += 4) {
+                    if (r + 4 < a.R) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) load8(a.x + (size_t)(r + 4) * a.x_stride, 512 * q + 8 * lane, xn[q]);
+                    }
+                    const double s = wave_sum_f64_dpp(dot(xv, gv, 0.0));
+                    if (lane == 0) store_dev(a.logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        xv[q][0] = xn[q][0];
+                        xv[q][1] = xn[q][1];
+                    }
+                }
+            } else {
+                for (int r = rg; r < a.R; r += 4) {
+                    double acc = 0.0;
+                    for (int h0 = 0; h0 < a.H; h0 += 2048) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            load8(w, h0 + 512 * q + 8 * lane, gv[q]);
+                            load8(a.x + (size_t)r * a.x_stride, h0 + 512 * q + 8 * lane, xv[q]);
+                        }
+                        acc = dot(xv, gv, acc);
+                    }
+                    const double s = wave_sum_f64_dpp(acc);
+                    if (lane == 0) store_dev(a.logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
+                }
             }
-#pragma unroll
-            for (int j = 0; j < RT_COLS; ++j) {
-                const int cc = c0 + j < C ? c0 + j : C - 1;
-                const uint16_t* w = cc < a.E ? a.gate + (size_t)cc * a.H : a.sgate;
-                load4_16(w + h, a.bf16, wv[j]);
-            }
-#pragma unroll
-            for (int i = 0; i < RT_ROWS; ++i)
-#pragma unroll
-                for (int j = 0; j < RT_COLS; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[i][j] = __builtin_fma(xv[i][q], wv[j][q], acc[i][j]);
         }
-#pragma unroll
-        for (int i = 0; i < RT_ROWS; ++i)
-#pragma unroll
-            for (int j = 0; j < RT_COLS; ++j) {
-                const double s = wave_sum_f64(acc[i][j]);
-                const int r = r0 + i, cc = c0 + j;
-                if (lane == 0 && r < a.R && cc < C)
-                    store_dev(a.logits + (size_t)r * C + cc, cc < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
-            }
     }
     if (!arrive_last(a.counter, (int)gridDim.x, &last)) return;
 
-    // 2. per row: top-k by logit (lowest id on ties), softmax weights over the picks, the shared gate's sigmoid
-    for (int r = wave; r < a.R; r += GT / 64) {
+    // 2. per row (one wave a row): k maxima of the keys, softmax weights over the picks, the shared gate's sigmoid
+    const int NW = RT / 64;
+    for (int r = wave; r < a.R; r += NW) {
         const float* lr = a.logits + (size_t)r * C;
-        float l[4];
+        uint32_t key[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int e = lane + 64 * q;
-            l[q] = e < a.E ? load_dev(lr + e) : -INFINITY;
+            key[q] = e < a.E ? (bf16_order(load_dev(lr + e)) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
         }
-        float mx = 0.f, psum = 0.f;
+        float mx = 0.f, psum = 0.f, p_mine = 0.f;
+        int e_mine = -1;
         for (int t = 0; t < a.k; ++t) {
-            float bv = -INFINITY;
-            int be = 1 << 30;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = lane + 64 * q;
-                if (e < a.E && (l[q] > bv || (l[q] == bv && e < be))) {
-                    bv = l[q];
-                    be = e;
-                }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oe = __shfl_xor(be, o, 64);
-                if (ov > bv || (ov == bv && oe < be)) {
-                    bv = ov;
-                    be = oe;
-                }
-            }
-            if (t == 0) mx = bv;
-            const float p = expf(bv - mx);
+            uint32_t m = key[0] > key[1] ? key[0] : key[1];
+            const uint32_t m2 = key[2] > key[3] ? key[2] : key[3];
+            m = m > m2 ? m : m2;
+            m = wave_max_u32(m);
+            const int e = (int)(0xFFFFu - (m & 0xFFFFu));
+            const float l = bf16_unorder(m >> 16);
+            if (t == 0) mx = l;
+            const float p = expf(l - mx);
             psum += p;
-            if (lane == 0) {
-                a.pick_out[r * slots + t] = be;
-                a.wts_out[r * slots + t] = p;                      // normalised below
+            if (lane == t) {
+                e_mine = e;
+                p_mine = p;
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if (lane + 64 * q == be) l[q] = -INFINITY;
+                if (lane + 64 * q == e) key[q] = 0u;
         }
-        if (lane == 0) {
-            for (int t = 0; t < a.k; ++t) a.wts_out[r * slots + t] = a.wts_out[r * slots + t] / psum;
-            if (has) {
-                a.pick_out[r * slots + a.k] = a.shared_id;
-                a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
-            }
+        if (lane < a.k) {
+            a.pick_out[r * slots + lane] = e_mine;
+            a.wts_out[r * slots + lane] = p_mine / psum;
+            sh_pick[r * slots + lane] = e_mine;
+        }
+        if (has && lane == 0) {
+            a.pick_out[r * slots + a.k] = a.shared_id;
+            a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
+            sh_pick[r * slots + a.k] = a.shared_id;
         }
     }
-    __threadfence_block();
     __syncthreads();
 
     // 3. grouping of the picks (ids < E + has)
-    const int n = a.R * slots;
-    for (int i = tid; i < n; i += GT) sh_pick[i] = a.pick_out[i];
-    __syncthreads();
-    group_block(sh_pick, n, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    group_block(sh_pick, a.R * slots, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
     if (tid == 0) store_dev(a.counter, 0);
 }
 
@@ -316,7 +351,7 @@ __global__ __launch_bounds__(GT) void group_shared_kernel(const int* __restrict_
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc = __builtin_fma(xv[q], wv[q], acc);
             }
-            const double s = wave_sum_f64(acc);
+            const double s = wave_sum_f64_dpp(acc);
             if (lane == 0) wts_out[r * slots + slots_in] = 1.f / (1.f + expf(-(float)s));
         }
     }
@@ -336,11 +371,13 @@ __global__ __launch_bounds__(256) void rot_in_kernel(const uint16_t* __restrict_
     const int nb = K >> 7;
     if (unit >= (long)P * nb) return;
     const int p = (int)(unit / nb), blk = (int)(unit % nb);
+    const int row = p / slots;
+    // x's load goes out with the pick's; the sign vector's waits for the pick
+    RotIn in = rot128_load(x, x_dtype, (size_t)row * x_stride + blk * 128, suh0, l32);
     const int e = pick[p];
     if (e < 0 || e >= E) return;
-    const int row = p / slots;
-    const uint16_t* suh = (mat ? suh1 : suh0) + (size_t)e * K + blk * 128;
-    const uint2 u = rot128(x, x_dtype, (size_t)row * x_stride + blk * 128, suh, l32);
+    in.su = *reinterpret_cast<const uint2*>((mat ? suh1 : suh0) + (size_t)e * K + blk * 128 + 4 * l32);
+    const uint2 u = rot128_apply(in, x_dtype, l32);
     *reinterpret_cast<uint2*>((mat ? out1 : out0) + (size_t)p * K + blk * 128 + 4 * l32) = u;
 }
 
@@ -452,6 +489,30 @@ __global__ __launch_bounds__(1024) void grouped_kernel(GroupedArgs a) {
 // ------------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
 
+// sum over SK splits (stride apart) of the 4 floats at p, in split order, with up to 8 splits' loads in flight
+__device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t stride, int SK, float (&v)[4]) {
+    for (int q0 = 0; q0 < SK; q0 += 8) {
+        float4 u[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (q0 + i < SK) u[i] = *reinterpret_cast<const float4*>(p + (size_t)(q0 + i) * stride);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (q0 + i == 0) {
+                v[0] = u[0].x; v[1] = u[0].y; v[2] = u[0].z; v[3] = u[0].w;
+            } else if (q0 + i < SK) {
+                v[0] += u[i].x; v[1] += u[i].y; v[2] += u[i].z; v[3] += u[i].w;
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void load4_f16(const uint16_t* p, float (&v)[4]) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    v[0] = h2f((uint16_t)(u.x & 0xFFFFu)); v[1] = h2f((uint16_t)(u.x >> 16));
+    v[2] = h2f((uint16_t)(u.y & 0xFFFFu)); v[3] = h2f((uint16_t)(u.y >> 16));
+}
+
 __global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
                                                               const uint16_t* __restrict__ svh_g,
                                                               const uint16_t* __restrict__ svh_u,
@@ -463,37 +524,33 @@ __global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __res
     const int nb = N >> 7;
     if (unit >= (long)P * nb) return;
     const int p = (int)(unit / nb), blk = (int)(unit % nb);
+    const int n = blk * 128 + 4 * l32;
+    // the splits' loads go out with the pick's (they do not depend on it)
+    float gv[4], uv[4];
+    sum_splits4(Z + (size_t)p * N + n, (size_t)P * N, SK, gv);
+    sum_splits4(Z + ((size_t)SK * P + p) * N + n, (size_t)P * N, SK, uv);
     const int e = pick[p];
     if (e < 0 || e >= E) return;
-    const int n = blk * 128 + 4 * l32;
-    float gv[4], uv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float sg = 0.f, su = 0.f;
-        for (int s = 0; s < SK; ++s) {
-            sg += Z[((size_t)(0 * SK + s) * P + p) * N + n + j];
-            su += Z[((size_t)(1 * SK + s) * P + p) * N + n + j];
-        }
-        gv[j] = sg;
-        uv[j] = su;
-    }
     fwht128(gv, l32);
     fwht128(uv, l32);
+    float sg[4], su[4], sd[4];
+    load4_f16(svh_g + (size_t)e * N + n, sg);
+    load4_f16(svh_u + (size_t)e * N + n, su);
+    load4_f16(suh_d + (size_t)e * N + n, sd);
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const size_t at = (size_t)e * N + n + j;
         float act;
         if (act_mode == 0) {
-            const float gg = fminf(bf16r(gv[j] * HAD_SCALE * h2f(svh_g[at])), limit);
-            const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * h2f(svh_u[at])), -limit), limit);
+            const float gg = fminf(bf16r(gv[j] * HAD_SCALE * sg[j]), limit);
+            const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * su[j]), -limit), limit);
             act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
         } else {
-            const float gg = fminf(gv[j] * HAD_SCALE * h2f(svh_g[at]), limit);
-            const float uu = fminf(fmaxf(uv[j] * HAD_SCALE * h2f(svh_u[at]), -limit), limit);
+            const float gg = fminf(gv[j] * HAD_SCALE * sg[j], limit);
+            const float uu = fminf(fmaxf(uv[j] * HAD_SCALE * su[j], -limit), limit);
             act = gg / (1.f + expf(-gg)) * uu;
         }
-        v[j] = __fmul_rn(act, h2f(suh_d[at]));
+        v[j] = __fmul_rn(act, sd[j]);
     }
     fwht128(v, l32);
 #pragma unroll
@@ -509,19 +566,16 @@ __global__ __launch_bounds__(256) void down_epilogue_kernel(const float* __restr
     const int nb = D >> 7;
     if (unit >= (long)P * nb) return;
     const int p = (int)(unit / nb), blk = (int)(unit % nb);
-    const int e = pick[p];
-    if (e < 0 || e >= E) return;
     const int n = blk * 128 + 4 * l32;
     float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float s = 0.f;
-        for (int q = 0; q < SK; ++q) s += Z[((size_t)q * P + p) * D + n + j];
-        v[j] = s;
-    }
+    sum_splits4(Z + (size_t)p * D + n, (size_t)P * D, SK, v);
+    const int e = pick[p];
+    if (e < 0 || e >= E) return;
+    float sv[4];
+    load4_f16(svh_d + (size_t)e * D + n, sv);
     fwht128(v, l32);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) y[(size_t)p * D + n + j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
+    for (int j = 0; j < 4; ++j) y[(size_t)p * D + n + j] = v[j] * HAD_SCALE * sv[j];
 }
 
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const float* __restrict__ wts,
@@ -548,23 +602,18 @@ __global__ __launch_bounds__(256) void down_combine_kernel(const float* __restri
     const int n0 = blk * 128;
     for (int k = hw; k < slots; k += 8) {
         const int p = r * slots + k;
-        const int e = pick[p];
         const int n = n0 + 4 * l32;
+        float v[4];
+        sum_splits4(Z + (size_t)p * D + n, (size_t)P * D, SK, v);       // in flight with the pick
+        const int e = pick[p];
         float o[4];
         if (e >= 0 && e < E) {
-            float v[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float s = 0.f;
-                for (int q = 0; q < SK; ++q) s += Z[((size_t)q * P + p) * D + n + j];
-                v[j] = s;
-            }
+            float sv[4];
+            load4_f16(svh_d + (size_t)e * D + n, sv);
             fwht128(v, l32);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                o[j] = v[j] * HAD_SCALE * h2f(svh_d[(size_t)e * D + n + j]);
-                y[(size_t)p * D + n + j] = o[j];
-            }
+            for (int j = 0; j < 4; ++j) o[j] = v[j] * HAD_SCALE * sv[j];
+            *reinterpret_cast<float4*>(y + (size_t)p * D + n) = make_float4(o[0], o[1], o[2], o[3]);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = y[(size_t)p * D + n + j];   // an invalid pick reuses y's row
@@ -622,10 +671,13 @@ extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int
     ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
     ESP_REQUIRE(E >= 1 && E <= 256 && k >= 1 && k <= 16 && k <= E && H % 256 == 0 && H > 0,
                 "route_group: shape limits");
+    ESP_REQUIRE(E + has <= RT_MAX_IDS, "route_group: too many router columns");
     ESP_REQUIRE(R >= 1 && R * (k + has) <= MAX_PICKS && k + has <= 32, "route_group: window too large");
     ESP_REQUIRE(!has || sgate, "the shared gate weight is needed with a shared slot");
     ESP_REQUIRE(logits_numel >= R * (E + has), "logits scratch too small");
     ESP_REQUIRE(x_stride >= H && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE(((uintptr_t)x & 7) == 0 && ((uintptr_t)gate & 7) == 0 && (!sgate || ((uintptr_t)sgate & 7) == 0),
+                "route_group: x / gate must be 8-byte aligned");
     ESP_REQUIRE(maxu >= (R * (k + has) < E + has ? R * (k + has) : E + has), "uids too small");
     ESP_REQUIRE(maxm >= 1, "members too small");
     RouteArgs a{};
@@ -647,8 +699,11 @@ extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int
     a.k = (int)k;
     a.shared_id = (int)shared_id;
     a.maxm = (int)maxm;
-    const long tiles = ((R + RT_ROWS - 1) / RT_ROWS) * ((E + has + RT_COLS - 1) / RT_COLS);
-    route_group_kernel<<<units_grid(tiles, GT / 64), GT, 0, (hipStream_t)stream>>>(a);
+    const unsigned grid = (unsigned)((E + has + RT_COLS - 1) / RT_COLS);
+    if (a.bf16)
+        route_group_kernel<1><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+    else
+        route_group_kernel<0><<<grid, RT, 0, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("route_group");
 }
 
