@@ -73,18 +73,23 @@ def ext():
 
 
 def tile_config(K: int, N: int, gateup: bool) -> tuple[int, int, int, int]:
-    """(n tiles a block, waves a workgroup, K splits across workgroups, tiles in flight) for a K -> N projection, from
-    the shape alone so a row's bits never depend on the batch. A gfx950 workgroup is 4 * KW waves on 128 columns; the
-    K range is split KW * SK ways (up to 16, at least 2 32-k steps a wave) so that the handful of experts one token
-    picks still keeps every CU busy. The reference's sm89 choices are experts.py:59-68."""
+    """(n tiles a block, waves a workgroup, K splits, tiles in flight) for a K -> N projection, from the shape alone so
+    a row's bits never depend on the batch. A gfx950 workgroup is 4 * KW waves on 128 columns. From cold sweeps of
+    the BASELINE MoE layer on MI355X (1 and 32 tokens): K splits of 256 (8 32-k steps a workgroup) and 8 waves, which
+    keeps the handful of experts one token picks spread over the CUs. The reference's sm89 choices are
+    experts.py:59-68. ESPALIER_GROUPED_TILE_PLAN="w,sk" (both projections) or "w,sk;w,sk" (gate/up; down) forces."""
     if N % 128 or K % 32:
         raise ValueError(f"no tile setting divides K={K}, N={N}")
-    steps = K // 32
-    splits = 1
-    while splits < 16 and steps // (2 * splits) >= 2 and K % (32 * (2 * splits // min(4, 2 * splits))) == 0:
-        splits *= 2
-    kw = min(4, splits)
-    return 8, 4 * kw, splits // kw, 2
+    forced = env("ESPALIER_GROUPED_TILE_PLAN")
+    if forced:
+        parts = forced.split(";")
+        w, sk = (int(v) for v in parts[0 if gateup or len(parts) == 1 else 1].split(","))
+        return 8, w, sk, 2
+    sk = 1
+    while K % (32 * sk * 2) == 0 and K // (sk * 2) >= 256:
+        sk *= 2
+    steps = K // (32 * sk)
+    return 8, 8 if steps >= 4 else 4, sk, 2
 
 
 @dataclass
