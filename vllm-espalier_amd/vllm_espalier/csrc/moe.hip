@@ -443,28 +443,28 @@ __global__ __launch_bounds__(1024) void grouped_kernel(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
     const int u = blockIdx.x;
-    if (u >= a.ucount[0]) return;
     const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
+    __shared__ int rows_sh[32];
+    __shared__ int nrows;
+    // the count, the expert id and the member rows depend on u alone: all three loads in flight at once
+    // (u < gridDim.x <= the tables' length, so the loads stay in bounds past the count)
+    const int cnt = a.ucount[0];
     const int e = a.uids[u];
+    if (threadIdx.x < 64) {
+        const int m = threadIdx.x;
+        const int code = m < a.maxm && m < 32 ? a.members[(size_t)u * a.maxm + m] : -1;
+        const int rp = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
+        if (m < 32) rows_sh[m] = rp;
+        const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
+        if (m == 0) nrows = __builtin_popcountll(valid);
+    }
+    if (u >= cnt) return;                                   // workgroup-uniform
     const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? a.TP1[e] : a.TP0[e]);
     const int k2 = mat ? a.B1[e] : a.B0[e];
     const int cb = mat ? a.C1[e] : a.C0[e];
     const uint16_t* X = mat ? a.X1 : a.X0;
-    __shared__ int rows_sh[32];
-    __shared__ int nrows;
-    if (threadIdx.x < 32) {
-        const int m = threadIdx.x;
-        const int code = m < a.maxm ? a.members[(size_t)u * a.maxm + m] : -1;
-        rows_sh[m] = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
-    }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int n = 0;
-        while (n < 32 && rows_sh[n] >= 0) ++n;
-        nrows = n;
-    }
-    __syncthreads();
-    if (nrows == 0) return;                                 // members come first: no rows
+    if (nrows == 0) return;
     const bool two = nrows > 16;
     switch (cb * 32 + k2) {
 #define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
