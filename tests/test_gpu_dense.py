@@ -22,7 +22,7 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 
 @pytest.mark.parametrize("cb,k2", sorted(experts.COMPILED))
-@pytest.mark.parametrize("K,N", [(256, 256), (48, 64)])
+@pytest.mark.parametrize("K,N", [(256, 256), (48, 64), (1024, 1024)])
 def test_dequant_bit_exact(dev, ext, cb, k2, K, N):
     print(f"dequant cb={cb} k2={k2} K={K} N={N}", flush=True)
     gen = torch.Generator().manual_seed(1000 + cb * 32 + k2)

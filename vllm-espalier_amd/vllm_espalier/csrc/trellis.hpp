@@ -24,6 +24,7 @@ namespace esp {
 constexpr uint32_t MCG_MUL = 0xCBAC1FEDu;   // experts_grouped.cuh:67
 constexpr uint32_t MCG_MASK = 0x8FFF8FFFu;  // :73
 constexpr uint32_t MCG_XOR = 0x3B603B60u;
+constexpr float E2M1_K = (4.0f / 3.0f) * (1.0f - 0x1p-16f);   // E2M1 snap scale, exact midpoints nudged below
 
 // int5 / int6 grids: k reproduces rintf(v / c) (experts_grouped.cuh:40-42)
 constexpr float GRID_K5 = 0x1.e62c10p+1f;
@@ -118,25 +119,21 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
     if constexpr (CB == 1) {
         return mcg_pair(s0, s1);
     } else if constexpr (CB == 3) {
+        // E2M1 (experts_grouped.cuh:25-38): |v| snapped to 0.75 * {0, .5, 1, 1.5, 2, 3, 4, 6}, a tie going to the
+        // smaller value, with v's sign (so -0 exists). gfx950's FP4 conversion rounds to that grid (x 4/3) to nearest
+        // even, saturating, keeping the sign; scaling by k = 4/3 (1 - 2^-16) in fp32 first puts every exact midpoint
+        // just below (ties then go down) and moves nothing else across one (fp16 values near a midpoint are 2^-11 or
+        // more apart, relative). Back to fp16 through the same instruction pair, then * 0.75 (exact).
         const uint32_t m = mcg_pair(s0, s1);
-        // E2M1 (experts_grouped.cuh:25-38): |v| against 0.75 * {0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5}, summing the grid
-        // steps, then v's sign. Each step is clamp((|v| - t) * 2^14, 0, 1): |v| > t by at least one fp16 ulp of t gives
-        // >= 2, so the step is exactly 0 or 1, and every partial sum is exact in fp16.
-        const f16x2 a = __builtin_bit_cast(f16x2, m & 0x7FFF7FFFu);
-        const f16x2 big = {(_Float16)16384.0f, (_Float16)16384.0f};
-        const f16x2 zero = {(_Float16)0.0f, (_Float16)0.0f}, one = {(_Float16)1.0f, (_Float16)1.0f};
-        constexpr float T[7] = {0.1875f, 0.5625f, 0.9375f, 1.3125f, 1.875f, 2.625f, 3.75f};
-        constexpr float S[7] = {0.375f, 0.375f, 0.375f, 0.375f, 0.75f, 0.75f, 1.5f};
-        f16x2 acc = zero;
-#pragma unroll
-        for (int i = 0; i < 7; ++i) {
-            const f16x2 nt = {(_Float16)(-T[i] * 16384.0f), (_Float16)(-T[i] * 16384.0f)};
-            f16x2 st = __builtin_elementwise_fma(a, big, nt);
-            st = __builtin_elementwise_min(__builtin_elementwise_max(st, zero), one);
-            const f16x2 w = {(_Float16)S[i], (_Float16)S[i]};
-            acc = __builtin_elementwise_fma(st, w, acc);
-        }
-        return __builtin_bit_cast(uint32_t, acc) | (m & 0x80008000u);
+        const float k = E2M1_K;
+        float y0, y1;
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(y0) : "v"(m), "v"(k));
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(y1) : "v"(m), "v"(k));
+        uint32_t code = 0u, h;
+        asm("v_cvt_scalef32_pk_fp4_f32 %0, %1, %2, %3" : "+v"(code) : "v"(y0), "v"(y1), "v"(1.0f));
+        asm("v_cvt_scalef32_pk_f16_fp4 %0, %1, %2" : "=v"(h) : "v"(code), "v"(1.0f));
+        const f16x2 q = __builtin_bit_cast(f16x2, h) * f16x2{(_Float16)0.75f, (_Float16)0.75f};
+        return __builtin_bit_cast(uint32_t, q);
     } else {
         static_assert(CB == 6 || CB == 7 || CB == 22 || CB == 23, "codebook");
         constexpr float k = (CB == 6 || CB == 22) ? GRID_K5 : GRID_K6;
