@@ -41,7 +41,8 @@ int esp_abi_version(void);
 int esp_had(const void* x, const void* pre, const void* post, void* y, int64_t M, int64_t K, void* stream);
 
 /* Replaces `dequant` (experts.cpp:68-77, experts_grouped.cuh:321-340, 379-387): out fp16 [K][N] = the decoded
- * weight of a trellis int16 [K/16][N/16][8 * k2]. */
+ * weight of a trellis int16 [K/16][N/16][8 * k2]. cb 1 / 3 / 6 / 7 as the reference; cb 22 / 23 (this library's
+ * addition) give the int5 / int6 grid index q as fp16 (the dense kernels decode it and scale the sums by c). */
 int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2, int64_t cb, void* stream);
 
 /* Replaces `dense` (experts.cpp:193-211, dense.cu:273-340): for each of n_shards (1..4) matrices sharing x,

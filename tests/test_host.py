@@ -102,3 +102,22 @@ def test_prepare_tables():
     bad = [tuple(_mat(k, n, 4, "e2m1", j) for j, (k, n) in enumerate([(Dm, I), (Dm, I), (I, Dm)]))]
     with pytest.raises(NotImplementedError):
         X.prepare(bad)                                    # E2M1 has no 4-bit instance
+
+
+def test_int6_index_through_magic_sum():
+    """The dense kernels' int6 grid index (csrc/trellis.hpp, codebook 23): fp16(v * k' + 1536) - 1536 with
+    k' = 0x1.f6628p+2 equals the reference's rintf(f32(v) * k) on every mcg value, whether the mixed fma rounds its
+    exact sum straight to fp16 or first to fp32; every v * k' stays more than 2^-13 from a half-integer. Exact rational
+    arithmetic over the 10,746 distinct values."""
+    from fractions import Fraction as F
+    mcg = np.unique(O.codebook_table(1))
+    v = O.f16(mcg).astype(np.float64)
+    q_ref = np.rint((v.astype(np.float32) * np.float32(float.fromhex("0x1.f660bap+2"))).astype(np.float32))
+    kp = F(float.fromhex("0x1.f6628p+2"))
+    for a, q in zip(v.tolist(), q_ref.tolist()):
+        e = F(a) * kp
+        fl = e.numerator // e.denominator
+        assert abs(e - fl - F(1, 2)) > F(1, 8192)
+        direct = fl + 1 if e - fl > F(1, 2) else fl                     # no ties: the distance check above
+        via_f32 = int(np.float16(np.float32(float(e + 1536)))) - 1536
+        assert direct == q and via_f32 == q, (a, q, direct, via_f32)

@@ -284,7 +284,7 @@ extern "C" int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N,
                            void* stream) {
     ESP_REQUIRE(trellis && out, "dequant: null pointer");
     ESP_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 16 == 0, "dequant: K and N must be positive multiples of 16");
-    if (!supported((int)cb, (int)k2))
+    if (!(supported((int)cb, (int)k2) || ((cb == 22 || cb == 23) && supported((int)cb - 16, (int)k2))))
         return esp_host::fail(ESP_ERR_UNSUPPORTED, "no instance for codebook %lld K2 %lld", (long long)cb,
                               (long long)k2);
     hipStream_t s = (hipStream_t)stream;
@@ -301,6 +301,7 @@ extern "C" int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N,
         if (tail) dequant_tail_kernel<CB_, K2_><<<tgrid, 256, 0, s>>>(T, o, (int)K, (int)N);               \
         break;
         ESP_CASES(ESP_DQ)
+        ESP_GRID_CASES(ESP_DQ)
 #undef ESP_DQ
     }
     return esp_host::launch_check("dequant");

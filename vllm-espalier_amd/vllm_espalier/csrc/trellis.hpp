@@ -29,6 +29,11 @@ constexpr float E2M1_K = (4.0f / 3.0f) * (1.0f - 0x1p-16f);   // E2M1 snap scale
 // int5 / int6 grids: k reproduces rintf(v / c) (experts_grouped.cuh:40-42)
 constexpr float GRID_K5 = 0x1.e62c10p+1f;
 constexpr float GRID_K6 = 0x1.f660bap+2f;
+// int6 grid index through one mixed fma a value: fp16(v * GRID_K6M + 1536) = 1536 + q. With this k every mcg value's
+// v * k lies at least 1.5e-4 from a half-integer (so no rounding of the sum, to fp32 and then fp16 or straight to fp16,
+// can move it across one) and rounds to the same q as rintf(v * GRID_K6) does; with GRID_K6 itself two values differ.
+constexpr float GRID_K6M = 0x1.f6628p+2f;
+constexpr float GRID_MAGIC = 1536.0f;                    // fp16 ulp 1 on [1024, 2048): the fraction is rounded off
 __host__ __device__ constexpr float grid_c(int cb) { return cb == 6 ? 3.94921875f / 15.0f : 3.94921875f / 31.0f; }
 
 // Per-lane constants of the MFMA B-operand decode for b = K2/2 bits: word indices (mod TW) and funnel shifts of the
@@ -134,8 +139,15 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
         asm("v_cvt_scalef32_pk_f16_fp4 %0, %1, %2" : "=v"(h) : "v"(code), "v"(1.0f));
         const f16x2 q = __builtin_bit_cast(f16x2, h) * f16x2{(_Float16)0.75f, (_Float16)0.75f};
         return __builtin_bit_cast(uint32_t, q);
+    } else if constexpr (CB == 23) {
+        uint32_t d;                                      // the high half is written next, by v_fma_mixhi_f16
+        const float k = GRID_K6M, m = GRID_MAGIC;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(mcg_one(s0)), "v"(k), "v"(m));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(mcg_one(s1)), "v"(k), "v"(m));
+        const f16x2 q = __builtin_bit_cast(f16x2, d) - f16x2{(_Float16)GRID_MAGIC, (_Float16)GRID_MAGIC};   // exact
+        return __builtin_bit_cast(uint32_t, q);
     } else {
-        static_assert(CB == 6 || CB == 7 || CB == 22 || CB == 23, "codebook");
+        static_assert(CB == 6 || CB == 7 || CB == 22, "codebook");
         constexpr float k = (CB == 6 || CB == 22) ? GRID_K5 : GRID_K6;
         const float q0 = __builtin_rintf(mul_mix(mcg_one(s0), k)), q1 = __builtin_rintf(mul_mix(mcg_one(s1), k));
         if constexpr (CB == 22 || CB == 23) {
@@ -186,6 +198,8 @@ __host__ __device__ constexpr int slot_k(int G, int i) { return 4 * (G & 1) + (i
 #define ESP_CASES(X) \
     X(1, 2) X(1, 4) X(1, 6) X(1, 8) X(1, 10) X(1, 12) X(1, 14) X(1, 16) \
     X(3, 2) X(3, 4) X(3, 6) X(6, 4) X(6, 6) X(6, 8) X(7, 6) X(7, 8) X(7, 10)
+// The dense kernels' grid-index forms of the int5 / int6 pairs (dequantised only to test them)
+#define ESP_GRID_CASES(X) X(22, 4) X(22, 6) X(22, 8) X(23, 6) X(23, 8) X(23, 10)
 
 __host__ __device__ constexpr bool supported(int cb, int k2) {
     return (cb == 1 && k2 >= 2 && k2 <= 16 && k2 % 2 == 0) || (cb == 3 && (k2 == 2 || k2 == 4 || k2 == 6)) ||
