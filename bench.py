@@ -9,12 +9,14 @@ time per layer. Weights are cold: a HIP graph replays the layer over enough dist
 the 256 MB MALL cannot serve them. A step is one replay of that graph; inputs are resident in HBM.
 
 Also reported: us/layer at batch 8 and 32; BASELINE config 1 (one 2048x2048 int6 matrix); config 3 (route_group);
-config 4 (a 256-expert MoE layer, fused routing + six launches, T = 1, 4, 32); `roofline` of the dominant kernel (the
-qkv dense launch: average launch time from a graph of cold launches, with HIP events on the launch stream); and
+config 4 (a 256-expert MoE layer, fused routing + six launches, T = 1, 4, 32); config 5 (the synthetic 40-layer decoder
+of vllm_espalier/step.py: greedy decode us/step and tok/s, one HIP graph a step, and 512-token prefill in 32-row
+windows); `roofline` of the dominant kernel (the qkv dense launch: average launch time from a graph of cold
+launches, with HIP events on the launch stream); and
 `cpu_baseline`: the reference's CPU path on this host (this repo's C restatement of the dequantisation, multithreaded,
 then fp32 Hadamards and torch.matmul), on a bounded sample of the same layer.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-moe]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-moe] [--no-decoder]
 """
 from __future__ import annotations
 
@@ -174,6 +176,56 @@ def bench_moe(dev, steps: int, layers: int, rows=(1, 4, 32)):
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# config 5: the synthetic 40-layer decoder (dense block + route + MoE a layer, mcg LM head), greedy decode and
+# windowed prefill
+# ---------------------------------------------------------------------------------------------------------------
+def bench_decoder(dev, steps: int, warmup: int, layers: int = 40, prefill_tokens: int = 512):
+    import torch
+    from vllm_espalier import step as S
+    t0 = time.perf_counter()
+    dec = S.SyntheticDecoder(n_layers=layers, seed=5, device=dev)
+    torch.cuda.synchronize()
+    log(f"decoder: {layers} layers built in {time.perf_counter() - t0:.1f} s")
+    b = dec.buffers(1)
+    b.ids_in.fill_(1)
+    picks = []
+    dec.forward(1, picks=picks)                  # eager: the experts each layer reads, for the bytes of a step
+    step_bytes = dec.algorithmic_bytes(picks, 1)
+
+    def decode_step():
+        dec.forward(1)
+        b.ids_in.copy_(b.ids_out)                # greedy: the argmax is the next input, on the device
+    g = graph_of(decode_step)
+    ms = time_graph(g, steps, warmup)
+    del g
+    us = ms * 1000
+    gbs = step_bytes / (us * 1e-6) / 1e9
+    res = {"layers": layers, "us_per_step": round(us, 1), "tok_per_s": round(1e6 / us, 1),
+           "bytes_per_step": step_bytes, "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
+    log(f"decode step: {us:.1f} us, {1e6 / us:.1f} tok/s, {step_bytes / 1e9:.3f} GB a step, {gbs:.0f} GB/s")
+
+    # prefill: prefill_tokens ids in windows of 32 rows, the head on the last window only
+    W = S.Dn.MAX_ROWS
+    bw = dec.buffers(W)
+    gen = torch.Generator(device=dev).manual_seed(55)
+    ids_all = torch.randint(0, dec.vocab, (prefill_tokens,), generator=gen, device=dev, dtype=torch.int32)
+    nwin = prefill_tokens // W
+
+    def prefill():
+        for w in range(nwin):
+            bw.ids_in.copy_(ids_all[w * W:(w + 1) * W])
+            dec.forward(W, head=(w == nwin - 1))
+    g = graph_of(prefill)
+    ms = time_graph(g, max(3, steps // 4), 1)
+    del g
+    res["prefill"] = {"tokens": nwin * W, "window": W, "ms": round(ms, 3), "tok_per_s": round(nwin * W / (ms * 1e-3), 1)}
+    log(f"prefill: {nwin * W} tokens in {ms:.2f} ms, {nwin * W / (ms * 1e-3):.0f} tok/s")
+    del dec
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------------------------------
 # CPU baseline: the reference's CPU path (dequantisation + torch matmul) on this host
 # ---------------------------------------------------------------------------------------------------------------
 def cpu_baseline(block, reps: int):
@@ -216,6 +268,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=20)
     a = ap.parse_args()
     if a.gpus != 1:
@@ -305,6 +358,9 @@ def main() -> int:
     moe = route = None
     if not a.no_moe:
         moe, route = bench_moe(dev, max(5, a.steps // 2), 6)
+    decoder = None
+    if not a.no_decoder:
+        decoder = bench_decoder(dev, max(5, a.steps // 2), a.warmup)
 
     cpu = None
     if not a.no_cpu:
@@ -338,6 +394,7 @@ def main() -> int:
         "config1_GBps": round(c1_gbs, 1),
         "moe_layer": moe,
         "route_group": route,
+        "decoder": decoder,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
                      "kernel": "dense_kernel (qkv launch, 5,269,504 B a launch)"},

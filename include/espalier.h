@@ -125,6 +125,24 @@ int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, fl
                       int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots,
                       int64_t E, int64_t n_routed, void* stream);
 
+/* ---- Decode-step glue (csrc/step.hip). No counterpart in the reference extension: in a served model vLLM does
+ * these (VocabParallelEmbedding, fused_add_rms_norm, the greedy sampler). They let the synthetic decoder step run as
+ * one HIP graph whose next token stays on the device. ---- */
+
+/* h [T][D] = table [vocab][D] rows ids[t] (int32 on the device); an id outside [0, vocab) gives a zero row. bf16 or
+ * fp16 (16-bit copy). D % 8 == 0; table and h 16-byte aligned. */
+int esp_embed(const int32_t* ids, const void* table, int64_t vocab, void* h, int64_t T, int64_t D, void* stream);
+
+/* Residual add and RMSNorm: z = h + d1 + d2 in fp32 (d1, d2 may be NULL), h = z in dtype (left as is without
+ * deltas), out = (h * (1 / sqrt(mean(h^2) + eps))) * w in dtype, h as stored. dtype ESP_BF16 or ESP_F16; [T][D]
+ * row-major, D % 8 == 0, D <= 8192, 16-byte aligned. */
+int esp_add_rmsnorm(void* h, const void* d1, const void* d2, const void* w, void* out, int64_t T, int64_t D,
+                    double eps, int dtype, void* stream);
+
+/* ids[t] = argmax of logits row t (rows of `stride` elements, N used), the lowest index among equal maxima, a NaN
+ * counting as the largest (torch.argmax). dtype ESP_BF16 or ESP_F16; rows 16-byte aligned. */
+int esp_argmax(const void* logits, int64_t stride, int64_t T, int64_t N, int dtype, int32_t* ids, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -281,6 +281,47 @@ void had(const at::Tensor& x, const c10::optional<at::Tensor>& pre, const c10::o
                  post.has_value() ? post->data_ptr() : nullptr, y.data_ptr(), M, K, cur_stream()));
 }
 
+// decode-step glue (no reference counterpart; csrc/step.hip)
+void embed(const at::Tensor& ids, const at::Tensor& table, at::Tensor h) {
+    check(ids, at::kInt, "ids");
+    TORCH_CHECK(table.is_cuda() && table.is_contiguous() && table.dim() == 2, "table: [vocab, D] contiguous");
+    TORCH_CHECK(h.is_cuda() && h.is_contiguous() && h.scalar_type() == table.scalar_type() && h.dim() == 2 &&
+                    h.size(1) == table.size(1) && h.size(0) == ids.numel(),
+                "h: [T, D] contiguous, table's dtype, T = ids.numel()");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(h.device());
+    call(esp_embed(cptr<int32_t>(ids), table.data_ptr(), table.size(0), h.data_ptr(), h.size(0), h.size(1),
+                   cur_stream()));
+}
+
+void add_rmsnorm(at::Tensor h, const c10::optional<at::Tensor>& d1, const c10::optional<at::Tensor>& d2,
+                 const at::Tensor& w, at::Tensor out, double eps) {
+    TORCH_CHECK(h.is_cuda() && h.is_contiguous() && h.dim() == 2, "h: [T, D] contiguous");
+    const auto t = h.scalar_type();
+    TORCH_CHECK(t == at::kBFloat16 || t == at::kHalf, "h: bf16 or fp16");
+    for (const auto* d : {&d1, &d2}) {
+        if (!d->has_value()) continue;
+        check(**d, t, "delta");
+        TORCH_CHECK((*d)->sizes() == h.sizes(), "deltas: h's shape");
+    }
+    check(w, t, "w");
+    check(out, t, "out");
+    TORCH_CHECK(w.numel() == h.size(1) && out.sizes() == h.sizes(), "w: [D]; out: h's shape");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(h.device());
+    call(esp_add_rmsnorm(h.data_ptr(), d1.has_value() ? d1->data_ptr() : nullptr,
+                         d2.has_value() ? d2->data_ptr() : nullptr, w.data_ptr(), out.data_ptr(), h.size(0),
+                         h.size(1), eps, dtype_code(h), cur_stream()));
+}
+
+void argmax(const at::Tensor& logits, at::Tensor ids) {
+    TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1, "logits: [T, N], unit column stride");
+    TORCH_CHECK(logits.scalar_type() == at::kBFloat16 || logits.scalar_type() == at::kHalf, "logits: bf16 or fp16");
+    check(ids, at::kInt, "ids");
+    TORCH_CHECK(ids.numel() == logits.size(0), "ids: [T]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(logits.device());
+    call(esp_argmax(logits.data_ptr(), logits.stride(0), logits.size(0), logits.size(1), dtype_code(logits),
+                    mptr<int32_t>(ids), cur_stream()));
+}
+
 PYBIND11_MODULE(espalier_ext, m) {
     m.def("had", &had);
     m.def("route_group", &route_group);
@@ -295,4 +336,7 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("down_epilogue", &down_epilogue);
     m.def("combine", &combine);
     m.def("down_combine", &down_combine);
+    m.def("embed", &embed);
+    m.def("add_rmsnorm", &add_rmsnorm);
+    m.def("argmax", &argmax);
 }

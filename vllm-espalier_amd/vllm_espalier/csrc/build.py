@@ -1,6 +1,6 @@
 """Build the gfx950 kernel layer in-tree with hipcc (no hipify, no JIT cache):
 
-  libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, moe.hip, abi.cpp)
+  libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, moe.hip, step.hip, abi.cpp)
   espalier_ext*.so     the torch extension module (binding.cpp, host code only), linked to libespalier_hip.so
 
 Both land in the vllm_espalier package directory. Usage: python build.py [--jobs N] [--only lib|ext]
@@ -53,7 +53,7 @@ def ext_suffix() -> str:
 def build_lib(jobs: int) -> Path:
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
-    srcs = [CSRC / "dense.hip", CSRC / "moe.hip", CSRC / "abi.cpp"]
+    srcs = [CSRC / "dense.hip", CSRC / "moe.hip", CSRC / "step.hip", CSRC / "abi.cpp"]
     objs = [BUILD / (s.stem + ".o") for s in srcs]
 
     def compile_one(pair):

@@ -1,0 +1,223 @@
+// Decode-step glue for the synthetic decoder step around the trellis layers, on gfx950: the token embedding gather,
+// the residual add fused with RMSNorm, and the greedy argmax over the logits. In a served model vLLM provides these
+// (VocabParallelEmbedding, fused_add_rms_norm, the sampler); the step that measures whole-model decode tok/s on
+// synthetic weights needs them on the device so one HIP graph holds the step and the next token never leaves HBM.
+//
+// Every reduction runs in a fixed order (lane slices, then DPP inside a wave, then the waves in index order), so a
+// row's result depends on that row alone.
+#include "../../../include/espalier.h"
+#include "common.hpp"
+
+namespace esp {
+
+// fp32 sum across a wave through DPP, in every lane (the fixed order of wave_sum_f64_dpp, no LDS)
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, v), 0u));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += dpp_f32<0x142, 0xA>(v);
+    v += dpp_f32<0x143, 0xC>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), 63));
+}
+
+// 8 consecutive 16-bit elements (bf16 or fp16) as fp32
+__device__ __forceinline__ void load8(const uint16_t* p, bool bf, float (&v)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
+        v[2 * i] = bf ? bf2f(lo) : h2f(lo);
+        v[2 * i + 1] = bf ? bf2f(hi) : h2f(hi);
+    }
+}
+
+__device__ __forceinline__ void store8(uint16_t* p, bool bf, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = bf ? f2bf(v[2 * i]) : f2h(v[2 * i]), hi = bf ? f2bf(v[2 * i + 1]) : f2h(v[2 * i + 1]);
+        w[i] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// embed: h[t] = table[ids[t]] (ids outside [0, vocab) give a zero row). One workgroup a row, 16 bytes a lane.
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ table,
+                                                    int64_t vocab, uint16_t* __restrict__ h, int D) {
+    const int t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool valid = id >= 0 && id < vocab;
+    for (int i = threadIdx.x * 8; i < D; i += blockDim.x * 8) {
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (valid) u = *reinterpret_cast<const uint4*>(table + id * D + i);
+        *reinterpret_cast<uint4*>(h + (size_t)t * D + i) = u;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// add_rmsnorm: z = h + d1 + d2 (fp32, each delta optional), h = z rounded to the model dtype, then
+// out = (h * (1 / sqrt(mean(h^2) + eps))) * w, with h read back as rounded, so the norm sees the residual stream as it
+// is stored. One workgroup of 256 a row; D a multiple of 8, at most 8 * 256 * ADD_RMS_CHUNKS.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int ADD_RMS_CHUNKS = 4;
+
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(uint16_t* __restrict__ h, const uint16_t* __restrict__ d1,
+                                                          const uint16_t* __restrict__ d2,
+                                                          const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                          int D, float eps, int bf) {
+    __shared__ float part[4];
+    const int t = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float z[ADD_RMS_CHUNKS][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
+        const int i = (c * 256 + threadIdx.x) * 8;
+        if (i < D) {
+            const size_t o = (size_t)t * D + i;
+            float a[8], b[8];
+            load8(h + o, bf, z[c]);
+            if (d1) {
+                load8(d1 + o, bf, a);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[c][j] += a[j];
+            }
+            if (d2) {
+                load8(d2 + o, bf, b);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[c][j] += b[j];
+            }
+            if (d1 || d2) {
+                store8(h + o, bf, z[c]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {                 // the stored (rounded) residual
+                    const uint16_t r = bf ? f2bf(z[c][j]) : f2h(z[c][j]);
+                    z[c][j] = bf ? bf2f(r) : h2f(r);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += z[c][j] * z[c][j];
+        }
+    }
+    ss = wave_sum_f32(ss);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    const float total = ((part[0] + part[1]) + part[2]) + part[3];
+    const float inv = 1.0f / sqrtf(total / (float)D + eps);
+#pragma unroll
+    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
+        const int i = (c * 256 + threadIdx.x) * 8;
+        if (i < D) {
+            float wv[8], o8[8];
+            load8(w + i, bf, wv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o8[j] = (z[c][j] * inv) * wv[j];
+            store8(out + (size_t)t * D + i, bf, o8);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// argmax: ids[t] = the index of the largest logit of row t, the lowest index among equal ones (torch.argmax);
+// a NaN counts as the largest. Keys: the value's bits made order-preserving, above the complemented index.
+// ------------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t order16(uint16_t b) { return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (b | 0x8000u); }
+
+__device__ __forceinline__ uint64_t key_of(uint16_t b, bool bf, int idx) {
+    uint32_t k;
+    if (bf) {
+        const bool nan = (b & 0x7FFFu) > 0x7F80u;
+        k = nan ? 0xFFFFu : order16(b);
+    } else {
+        const bool nan = (b & 0x7FFFu) > 0x7C00u;
+        k = nan ? 0xFFFFu : order16(b);
+    }
+    return ((uint64_t)k << 32) | (uint32_t)(~(uint32_t)idx);
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t stride, int N,
+                                                      int bf, int32_t* __restrict__ ids) {
+    __shared__ uint64_t part[16];
+    const int t = blockIdx.x;
+    const uint16_t* row = logits + (size_t)t * stride;
+    uint64_t best = 0;
+    const int nv = N & ~7;
+    for (int i = threadIdx.x * 8; i < nv; i += blockDim.x * 8) {
+        const uint4 u = *reinterpret_cast<const uint4*>(row + i);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            best = umax64(best, key_of((uint16_t)(w[j] & 0xFFFFu), bf, i + 2 * j));
+            best = umax64(best, key_of((uint16_t)(w[j] >> 16), bf, i + 2 * j + 1));
+        }
+    }
+    for (int i = nv + (int)threadIdx.x; i < N; i += blockDim.x) best = umax64(best, key_of(row[i], bf, i));
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m), hi = (uint32_t)__shfl_xor((int)(best >> 32), m);
+        best = umax64(best, ((uint64_t)hi << 32) | lo);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) part[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = part[0];
+        for (int q = 1; q < (int)(blockDim.x >> 6); ++q) b = umax64(b, part[q]);
+        ids[t] = (int32_t)~(uint32_t)b;
+    }
+}
+
+}  // namespace esp
+
+// ======================================================================================================================
+// C ABI
+// ======================================================================================================================
+using namespace esp;
+
+extern "C" int esp_embed(const int32_t* ids, const void* table, int64_t vocab, void* h, int64_t T, int64_t D,
+                         void* stream) {
+    ESP_REQUIRE(ids && table && h, "embed: null pointer");
+    ESP_REQUIRE(D > 0 && D % 8 == 0 && vocab > 0, "embed: D must be a positive multiple of 8");
+    ESP_REQUIRE(((uintptr_t)table | (uintptr_t)h) % 16 == 0, "embed: table and h must be 16-byte aligned");
+    if (T <= 0) return esp_host::ok();
+    embed_kernel<<<(unsigned)T, 256, 0, (hipStream_t)stream>>>(ids, static_cast<const uint16_t*>(table), vocab,
+                                                                static_cast<uint16_t*>(h), (int)D);
+    return esp_host::launch_check("embed");
+}
+
+extern "C" int esp_add_rmsnorm(void* h, const void* d1, const void* d2, const void* w, void* out, int64_t T,
+                               int64_t D, double eps, int dtype, void* stream) {
+    ESP_REQUIRE(h && w && out, "add_rmsnorm: null pointer");
+    ESP_REQUIRE(dtype == ESP_BF16 || dtype == ESP_F16, "add_rmsnorm: dtype must be bf16 or fp16");
+    ESP_REQUIRE(D > 0 && D % 8 == 0 && D <= 8 * 256 * ADD_RMS_CHUNKS,
+                "add_rmsnorm: D must be a positive multiple of 8, at most %d", 8 * 256 * ADD_RMS_CHUNKS);
+    ESP_REQUIRE(((uintptr_t)h | (uintptr_t)d1 | (uintptr_t)d2 | (uintptr_t)w | (uintptr_t)out) % 16 == 0,
+                "add_rmsnorm: every tensor must be 16-byte aligned");
+    if (T <= 0) return esp_host::ok();
+    add_rmsnorm_kernel<<<(unsigned)T, 256, 0, (hipStream_t)stream>>>(
+        static_cast<uint16_t*>(h), static_cast<const uint16_t*>(d1), static_cast<const uint16_t*>(d2),
+        static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), (int)D, (float)eps, dtype == ESP_BF16);
+    return esp_host::launch_check("add_rmsnorm");
+}
+
+extern "C" int esp_argmax(const void* logits, int64_t stride, int64_t T, int64_t N, int dtype, int32_t* ids,
+                          void* stream) {
+    ESP_REQUIRE(logits && ids, "argmax: null pointer");
+    ESP_REQUIRE(dtype == ESP_BF16 || dtype == ESP_F16, "argmax: dtype must be bf16 or fp16");
+    ESP_REQUIRE(N > 0 && N < (1ll << 31) && stride >= N, "argmax: need 0 < N < 2^31 and stride >= N");
+    ESP_REQUIRE((uintptr_t)logits % 16 == 0 && stride % 8 == 0, "argmax: rows must be 16-byte aligned");
+    if (T <= 0) return esp_host::ok();
+    argmax_kernel<<<(unsigned)T, 1024, 0, (hipStream_t)stream>>>(static_cast<const uint16_t*>(logits), stride,
+                                                                  (int)N, dtype == ESP_BF16, ids);
+    return esp_host::launch_check("argmax");
+}
