@@ -261,6 +261,50 @@ def cpu_baseline(block, reps: int):
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# rocprofv3 summaries (the text kept under profiles/)
+# ---------------------------------------------------------------------------------------------------------------
+def rocprof_summary(d: str, top: int = 30) -> str:
+    """Markdown from a `rocprofv3 --kernel-trace --stats --output-format csv -o run` directory: the --stats table
+    of this library's kernels, then per-dispatch durations grouped by kernel and launch shape (grid and workgroup, in
+    threads), from the kernel trace. Durations in microseconds."""
+    import csv
+    from collections import defaultdict
+    root = Path(d)
+    stats = next(root.rglob("*kernel_stats.csv"), None)
+    trace = next(root.rglob("*kernel_trace.csv"), None)
+    out = []
+    if stats is not None:
+        rows = [r for r in csv.DictReader(open(stats)) if "esp::" in r["Name"]]
+        rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        out += ["`rocprofv3 --stats` (kernel_stats.csv), kernels of this library:", "",
+                "| kernel | calls | avg us | min us | max us | total ms |", "|---|---:|---:|---:|---:|---:|"]
+        for r in rows[:top]:
+            n = r["Name"].replace("void ", "").split("(")[0]
+            out.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                       f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e6:.2f} |")
+        out.append("")
+    if trace is not None:
+        groups = defaultdict(list)
+        for r in csv.DictReader(open(trace)):
+            if "esp::" not in r["Kernel_Name"]:
+                continue
+            n = r["Kernel_Name"].replace("void ", "").split("(")[0]
+            shape = (f"{r.get('Grid_Size_X', '?')}x{r.get('Grid_Size_Y', '?')}x{r.get('Grid_Size_Z', '?')} / "
+                     f"{r.get('Workgroup_Size_X', '?')}")
+            groups[(n, shape)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        items = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
+        out += ["Kernel trace (kernel_trace.csv), dispatches grouped by kernel and launch shape (grid x*y*z threads / "
+                "workgroup threads):", "", "| kernel | launch shape | calls | avg us | median us | min us | max us |",
+                "|---|---|---:|---:|---:|---:|---:|"]
+        for (n, shape), v in items[:top]:
+            v = sorted(v)
+            out.append(f"| `{n}` | {shape} | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | "
+                       f"{v[-1]:.2f} |")
+        out.append("")
+    return "\n".join(out)
+
+
+# ---------------------------------------------------------------------------------------------------------------
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -270,7 +314,12 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=20)
+    ap.add_argument("--rocprof-summary", metavar="DIR", help="print the markdown summary of a rocprofv3 csv output "
+                    "directory and exit (no GPU work)")
     a = ap.parse_args()
+    if a.rocprof_summary:
+        print(rocprof_summary(a.rocprof_summary))
+        return 0
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the reference path is single-GPU, TP=1); --gpus {a.gpus} is "
               "not supported", file=sys.stderr)
