@@ -66,7 +66,7 @@ def _dense(lib, **over):
 
 @pytest.mark.parametrize("over,needle", [
     (dict(M=0), "rows"), (dict(M=33), "rows"), (dict(n=5), "matrices"), (dict(K=2000), "K"),
-    (dict(W=6), "W"), (dict(ncols=100), "shape"), (dict(col0=100), "past y"), (dict(SK=3), "K"),
+    (dict(W=6), "W"), (dict(ncols=100), "shape"), (dict(col0=100), "past y"), (dict(SK=65), "SK"), (dict(SK=0), "SK"),
 ])
 def test_dense_argument_errors(lib, over, needle):
     rc, msg = _dense(lib, **over)

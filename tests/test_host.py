@@ -22,10 +22,38 @@ def test_tables_match_the_oracle():
 @pytest.mark.parametrize("K,N", SHAPES)
 def test_dense_plan_is_valid(K, N):
     sk, w, pf = D.plan(K, N, 256)
-    assert w in (4, 8, 16) and sk >= 1
-    assert K % (128 * sk) == 0                            # the fused rotation works in 128-wide chunks
-    assert (K // sk) // 32 >= 2 * (w // 4) or (sk == 1 and w == 4)   # every wave has at least two 32-k steps
+    assert w in (4, 8, 16) and 1 <= sk <= K // 32         # splits of whole 32-k steps
+    steps = -(-(K // 32) // sk)                           # the longest split
+    assert steps >= w // 4 * (2 if w > 4 else 1)          # every k slot of the workgroup has work
     assert (N // 128) * sk <= max(N // 128, 256)          # the splits keep to a workgroup a CU
+
+
+def _chunks_max(K, SK):
+    """esp_dense's bound on the 128-blocks one split's rotated rows touch (its shared-memory sizing)."""
+    sq, sr = divmod(K // 32, SK)
+    steps_max = sq + (sr > 0)
+    aligned = sr == 0 and sq % 4 == 0
+    return steps_max // 4 if aligned else (steps_max * 32 + 96 + 127) // 128
+
+
+@pytest.mark.parametrize("K", [128, 256, 384, 512, 1024, 2048, 4096, 6144])
+def test_dense_splits_cover_k_and_fit_the_rotation_buffer(K):
+    """The kernel's split s of S = K/32 = SQ*SK + SR steps starts at s*SQ + min(s, SR) and has SQ + (s < SR): the
+    splits tile the steps in order, and no split's rotated rows (the 128-blocks its range touches) exceed the shared
+    memory esp_dense sizes for them."""
+    S = K // 32
+    for SK in range(1, S + 1):
+        sq, sr = divmod(S, SK)
+        bounds = [(s * sq + min(s, sr), s * sq + min(s, sr) + sq + (s < sr)) for s in range(SK)]
+        assert bounds[0][0] == 0 and bounds[-1][1] == S
+        assert all(b[1] == c[0] for b, c in zip(bounds, bounds[1:]))
+        assert all(b[1] > b[0] for b in bounds)
+        cmax = _chunks_max(K, SK)
+        for s0, s1 in bounds:
+            k0, kr = 32 * s0, 32 * (s1 - s0)
+            chunks = ((k0 + kr + 127) >> 7) - (k0 >> 7)
+            assert chunks <= cmax, (K, SK, s0, s1)
+            assert 32 * (s1 - s0) <= 32 * ((S + SK - 1) // SK)          # the stage buffer's size
 
 
 def test_dense_plan_depends_on_shape_only(monkeypatch):

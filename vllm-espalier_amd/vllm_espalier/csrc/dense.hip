@@ -3,9 +3,10 @@
 // esp_dense: every matrix of one layer (<= 4 sharing the input and the codebook) in one launch, y_s = H(H(x * suh_s)
 // @ W_s) * svh_s written into each matrix's columns of y (dense.cu:1-9, 273-340 define the contract).
 //
-// Work split. A workgroup is 4 waves on one 128-column block (the output Hadamard's width) and one K range (K / SK);
-// wave w owns the block's n tiles 2w, 2w+1 over the whole K range, so no partial sums are exchanged between waves.
-// Per 32-k step a wave decodes 2 B operands (trellis -> fp16 in registers, trellis.hpp) and issues one
+// Work split. A workgroup is 4 * KW waves on one 128-column block (the output Hadamard's width) and one K range: of
+// the S = K / 32 steps of 32 k, = SQ * SK + SR, split s takes the next SQ + (s < SR), so SK need not divide S and a
+// launch can match the CU count. Wave (p, kw) owns n tiles 2p, 2p+1 of the block and every KW-th step of the range
+// (gemm.hpp); the KW partial sums are added in order through shared memory. Per 32-k step a wave decodes 2 B operands (trellis -> fp16 in registers, trellis.hpp) and issues one
 // v_mfma_f32_16x16x32_f16 per B operand and 16-row group (rows 0-15, 16-31): weights stream from HBM once for all
 // rows. Split K (SK > 1) goes through Z, and the last workgroup of a column block to arrive (atomic counter) adds the
 // splits in order and finishes; counters are left zero.
@@ -42,6 +43,7 @@ struct DenseArgs {
     float* Z;
     int* counters;
     int M, K, SK, NBT, fused, xs_stride, stage_bytes;
+    int SQ, SR;              // K / 32 steps = SQ * SK + SR: split s has SQ + (s < SR) steps
 };
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -165,7 +167,9 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const int c = lane & 15, G = lane >> 4;
     const int NTILES = S.nb * 8;
     const int cb_local = nbg - S.nb0;                       // column block inside the matrix
-    const int kr = a.K / a.SK, k0 = split * kr;
+    // of the K / 32 steps = SQ * SK + SR, split s takes SQ + (s < SR) in order: SK need not divide the steps
+    const int s0 = split * a.SQ + (split < a.SR ? split : a.SR);
+    const int k0 = s0 * 32, kr = (a.SQ + (split < a.SR)) * 32;
     const int M = a.M;
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
@@ -181,11 +185,13 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
     RowsA<MG> al;
     if (a.fused) {
+        // the 128-blocks the K range touches (a split may start or end inside one)
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
-        const int chunks = kr >> 7;
+        const int c0 = k0 >> 7, chunks = ((k0 + kr + 127) >> 7) - c0;
         for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
             const int r = idx / chunks, ch = idx % chunks;
-            const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + k0 + ch * 128, S.suh + k0 + ch * 128, l32);
+            const int kb = (c0 + ch) * 128;
+            const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + kb, S.suh + kb, l32);
             *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) = u;
         }
 #pragma unroll
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
             const int row = g * 16 + c;
             al.row[g] = row < M ? xs + (size_t)row * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
         }
-        al.kbase = k0;
+        al.kbase = c0 * 128;
     } else {
         const uint16_t* X = a.xh + (size_t)si * M * a.K;
 #pragma unroll
@@ -328,8 +334,8 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     (void)PF;
     ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "1 to 4 matrices a launch");
     ESP_REQUIRE(M >= 1 && M <= 32, "1 to 32 rows");
-    ESP_REQUIRE(SK >= 1 && K > 0 && K % (128 * SK) == 0 && (K / SK) % 32 == 0,
-                "K must split evenly over SK in 128s");
+    ESP_REQUIRE(K > 0 && K % 128 == 0 && SK >= 1 && SK <= K / 32,
+                "K must be a multiple of 128 and SK at most K / 32 (splits of whole 32-k steps)");
     ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "x / y dtype");
     ESP_REQUIRE(W == 4 || W == 8 || W == 16, "W (waves a workgroup) must be 4, 8 or 16");
     ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "x / y row stride");
@@ -351,9 +357,15 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     a.n = (int)n_shards;
     ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= (int64_t)nbt * CNT_STRIDE),
                 "scratch too small: Z needs SK*M*N floats, counters 32 per 128 columns");
-    const int64_t kr = K / SK;
-    const int xs_stride = (int)kr + 8;                        // pad rows across the LDS banks
-    const bool fused = M * kr * 2 <= rot_smem;
+    const int64_t sq = (K / 32) / SK, sr = (K / 32) % SK;
+    const int64_t steps_max = sq + (sr > 0);                  // the longest split
+    const int64_t kr = steps_max * 32;
+    // 128-blocks a split's rotated rows touch: exact when every split starts and ends on one, else the bound for a
+    // range starting up to 96 past a block's start
+    const bool aligned = sr == 0 && sq % 4 == 0;
+    const int64_t chunks_max = aligned ? steps_max / 4 : (steps_max * 32 + 96 + 127) / 128;
+    const int xs_stride = (int)(chunks_max * 128) + 8;        // pad rows across the LDS banks
+    const bool fused = M * chunks_max * 128 * 2 <= rot_smem;
     a.x = x;
     a.x_dtype = x_dtype;
     a.x_stride = (int)x_stride;
@@ -366,6 +378,8 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     a.M = (int)M;
     a.K = (int)K;
     a.SK = (int)SK;
+    a.SQ = (int)sq;
+    a.SR = (int)sr;
     a.NBT = nbt;
     a.fused = fused;
     a.xs_stride = xs_stride;

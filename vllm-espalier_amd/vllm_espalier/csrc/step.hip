@@ -76,8 +76,13 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(uint16_t* __restrict__
     __shared__ float part[4];
     const int t = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float z[ADD_RMS_CHUNKS][8];
+    float z[ADD_RMS_CHUNKS][8], wv[ADD_RMS_CHUNKS][8];
     float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {            // the weights first: in flight with the rows
+        const int i = (c * 256 + threadIdx.x) * 8;
+        if (i < D) load8(w + i, bf, wv[c]);
+    }
 #pragma unroll
     for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
         const int i = (c * 256 + threadIdx.x) * 8;
@@ -116,10 +121,9 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(uint16_t* __restrict__
     for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
         const int i = (c * 256 + threadIdx.x) * 8;
         if (i < D) {
-            float wv[8], o8[8];
-            load8(w + i, bf, wv);
+            float o8[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o8[j] = (z[c][j] * inv) * wv[j];
+            for (int j = 0; j < 8; ++j) o8[j] = (z[c][j] * inv) * wv[c][j];
             store8(out + (size_t)t * D + i, bf, o8);
         }
     }
@@ -145,6 +149,8 @@ __device__ __forceinline__ uint64_t key_of(uint16_t b, bool bf, int idx) {
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+constexpr int ARGMAX_BATCH = 8;
+
 __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits, int64_t stride, int N,
                                                       int bf, int32_t* __restrict__ ids) {
     __shared__ uint64_t part[16];
@@ -152,13 +158,22 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
     const uint16_t* row = logits + (size_t)t * stride;
     uint64_t best = 0;
     const int nv = N & ~7;
-    for (int i = threadIdx.x * 8; i < nv; i += blockDim.x * 8) {
-        const uint4 u = *reinterpret_cast<const uint4*>(row + i);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    const int step = (int)blockDim.x * 8;
+    for (int i0 = threadIdx.x * 8; i0 < nv; i0 += ARGMAX_BATCH * step) {
+        uint4 u[ARGMAX_BATCH];                                 // a batch of 16-byte loads in flight at once
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            best = umax64(best, key_of((uint16_t)(w[j] & 0xFFFFu), bf, i + 2 * j));
-            best = umax64(best, key_of((uint16_t)(w[j] >> 16), bf, i + 2 * j + 1));
+        for (int b = 0; b < ARGMAX_BATCH; ++b)
+            if (i0 + b * step < nv) u[b] = *reinterpret_cast<const uint4*>(row + i0 + b * step);
+#pragma unroll
+        for (int b = 0; b < ARGMAX_BATCH; ++b) {
+            const int i = i0 + b * step;
+            if (i >= nv) break;
+            const uint32_t w[4] = {u[b].x, u[b].y, u[b].z, u[b].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                best = umax64(best, key_of((uint16_t)(w[j] & 0xFFFFu), bf, i + 2 * j));
+                best = umax64(best, key_of((uint16_t)(w[j] >> 16), bf, i + 2 * j + 1));
+            }
         }
     }
     for (int i = nv + (int)threadIdx.x; i < N; i += blockDim.x) best = umax64(best, key_of(row[i], bf, i));

@@ -24,19 +24,20 @@ _scratch: dict = {}
 def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
     """(K splits SK, waves a workgroup W, tiles in flight) for a K -> N layer of 128-column blocks, from its shape
     alone so a row's bits never depend on the batch (the reference's sm89 heuristic is dense.py:22-39). A gfx950
-    workgroup is 4 * KW waves on one block, KW of them on every 32-k step column. From cold sweeps on MI355X at one
-    row (the decode case): the most splits that keep a workgroup a CU at most, then 16 waves when a workgroup has 8
-    steps or more, 8 from 4, else 4.
+    workgroup is 4 * KW waves on one block, KW of them on every 32-k step column; a split is a run of whole 32-k
+    steps, SK need not divide them. The decode of a workgroup's share is bound by its CU's VALU, so the plan spreads
+    the layer over the CUs, SK = CUs // blocks (one workgroup a CU), but keeps 4 steps a split: below that the
+    fixed costs (rotation, hand-off) outweigh the shorter decode, and 32-row windows lose more to the extra partials
+    than single rows gain (cold sweeps on MI355X). Then 16 waves when a split has 8 steps or more, 8 from 4, else 4.
     ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
     forced = env("ESPALIER_DENSE_TILE_PLAN")
     if forced:
         sk, w, pf = (int(v) for v in forced.split(","))
         return sk, w, pf
     nb = N // 128
-    sk = 1
-    while nb * sk * 2 <= sms and K % (128 * sk * 2) == 0:
-        sk *= 2
-    steps = K // (32 * sk)
+    steps_all = K // 32
+    sk = max(1, min(steps_all // 4, sms // nb))
+    steps = -(-steps_all // sk)
     w = 16 if steps >= 8 else 8 if steps >= 4 else 4
     return sk, w, 2
 
