@@ -125,6 +125,22 @@ int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, fl
                       int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots,
                       int64_t E, int64_t n_routed, void* stream);
 
+/* ---- Fused MoE launch (csrc/moe.hip). No counterpart in the reference extension: a composition of the reference
+ * functions above, with the same arithmetic in the same order (bit-identical results), in one launch instead of three.
+ * counters: int32 zero on entry and left zero, 32 apart (one 128-byte line each). ---- */
+
+/* rot_in + grouped (mats = 2) + gateup_epilogue in one launch: the member rows of each distinct expert are rotated
+ * (x * suh, H) inside the launch, and the last of the 2 * SK programs of an (expert, 128-column block) to arrive runs the
+ * gate/up epilogue of its rows into xd fp16 [P][N]. Arguments as esp_rot_in, esp_grouped and esp_gateup_epilogue;
+ * (K / SK) % 128 == 0; counters >= nexp_max * (N / 128) * 32. */
+int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                   const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1, const int32_t* C0,
+                   const int32_t* C1, const int32_t* uids, int64_t nexp_max, const int32_t* ucount,
+                   const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int32_t* counters,
+                   int64_t counters_numel, const void* svh_g, const void* svh_u, const void* suh_d, void* xd, int64_t K,
+                   int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps, int64_t lo, int64_t hi,
+                   double limit, int64_t act_mode, void* stream);
+
 /* ---- Decode-step glue (csrc/step.hip). No counterpart in the reference extension: in a served model vLLM does
  * these (VocabParallelEmbedding, fused_add_rms_norm, the greedy sampler). They let the synthetic decoder step run as
  * one HIP graph whose next token stays on the device. ---- */

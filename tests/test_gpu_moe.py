@@ -424,3 +424,30 @@ def test_routed2_bf16_equals_routed_fp32_rounded(dev):
         ref32 = G.routed(x, pick, wts, L, s0).clone()
         out, sh = G.routed2(x, pick, wts, L, s0)
         assert sh is None and out.dtype == torch.bfloat16 and torch.equal(out, ref32.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("R,invalid", [(1, False), (4, False), (32, False), (5, True)])
+def test_moe_fused_launches_equal_unfused(dev, layer16, R, invalid, monkeypatch):
+    """routed2 with rot_in, the gate/up GEMM and its epilogue in one launch (esp_moe_gateup) against the reference's
+    launch sequence (rot_in, grouped, gateup_epilogue), bit for bit, at every window width (the production switch uses
+    it for up to FUSED_ROWS rows), with out-of-range picks too."""
+    print(f"moe fused R={R} invalid={invalid}", flush=True)
+    L, *_ = layer16
+    gen = torch.Generator().manual_seed(80 + R)
+    s = G.scratch(L, 32, 9, dev)
+    x = torch.randn((R, D), generator=gen).to(torch.bfloat16).to(dev)
+    pick = distinct_picks(R, 16, 8, gen)
+    if invalid:
+        pick[1, 3] = -1
+        pick[R - 1, 0] = 17                                  # past every table entry (16 routed + shared)
+    pick = pick.to(dev)
+    wts = torch.softmax(torch.randn((R, 8), generator=gen), -1).to(dev)
+    monkeypatch.setattr(G, "FUSED", False)
+    uo, us = (t.clone() for t in G.routed2(x, pick, wts, L, s))
+    monkeypatch.setattr(G, "FUSED", True)
+    monkeypatch.setattr(G, "FUSED_ROWS", 32)
+    fo, fs = (t.clone() for t in G.routed2(x, pick, wts, L, s))
+    torch.cuda.synchronize()
+    assert torch.equal(fo.view(torch.int16), uo.view(torch.int16))
+    assert torch.equal(fs.view(torch.int16), us.view(torch.int16))
+    assert int(s.counters.abs().sum()) == 0                 # every arrival counter left at zero

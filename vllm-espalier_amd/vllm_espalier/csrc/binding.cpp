@@ -281,6 +281,33 @@ void had(const at::Tensor& x, const c10::optional<at::Tensor>& pre, const c10::o
                  post.has_value() ? post->data_ptr() : nullptr, y.data_ptr(), M, K, cur_stream()));
 }
 
+// fused gate/up launch (no reference counterpart: rot_in + grouped + gateup_epilogue in one launch)
+void moe_gateup(const at::Tensor& x, int64_t x_stride, const at::Tensor& suh_g, const at::Tensor& suh_u,
+                const at::Tensor& TP0, const at::Tensor& TP1, const at::Tensor& B0, const at::Tensor& B1,
+                const at::Tensor& C0, const at::Tensor& C1, const at::Tensor& uids, const at::Tensor& ucount,
+                const at::Tensor& members, at::Tensor Z, at::Tensor counters, const at::Tensor& svh_g,
+                const at::Tensor& svh_u, const at::Tensor& suh_d, at::Tensor xd, int64_t K, int64_t N, int64_t P,
+                int64_t SK, int64_t slots, int64_t warps, int64_t lo, int64_t hi, double limit, int64_t act_mode) {
+    TORCH_CHECK(x.is_cuda() && (x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf) && x.stride(-1) == 1,
+                "x: bf16/fp16 rows with unit column stride");
+    using TL = std::initializer_list<const at::Tensor*>;
+    for (const at::Tensor* t : TL{&suh_g, &suh_u, &svh_g, &svh_u, &suh_d, &xd}) check(*t, at::kHalf, "fp16 table");
+    check(TP0, at::kLong, "TP0");
+    check(TP1, at::kLong, "TP1");
+    for (const at::Tensor* t : TL{&B0, &B1, &C0, &C1, &uids, &ucount, &members, &counters})
+        check(*t, at::kInt, "int table");
+    check(Z, at::kFloat, "Z");
+    TORCH_CHECK(members.dim() == 2 && members.size(0) >= uids.numel(), "members: [nexp_max, maxm]");
+    TORCH_CHECK(xd.numel() >= P * N, "xd too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_moe_gateup(x.data_ptr(), dtype_code(x), x_stride, suh_g.data_ptr(), suh_u.data_ptr(), cptr<int64_t>(TP0),
+                        cptr<int64_t>(TP1), cptr<int32_t>(B0), cptr<int32_t>(B1), cptr<int32_t>(C0), cptr<int32_t>(C1),
+                        cptr<int32_t>(uids), uids.numel(), cptr<int32_t>(ucount), cptr<int32_t>(members),
+                        members.size(1), mptr<float>(Z), Z.numel(), mptr<int32_t>(counters), counters.numel(),
+                        svh_g.data_ptr(), svh_u.data_ptr(), suh_d.data_ptr(), xd.data_ptr(), K, N, P, SK, slots, warps,
+                        lo, hi, limit, act_mode, cur_stream()));
+}
+
 // decode-step glue (no reference counterpart; csrc/step.hip)
 void embed(const at::Tensor& ids, const at::Tensor& table, at::Tensor h) {
     check(ids, at::kInt, "ids");
@@ -336,6 +363,7 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("down_epilogue", &down_epilogue);
     m.def("combine", &combine);
     m.def("down_combine", &down_combine);
+    m.def("moe_gateup", &moe_gateup);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);
     m.def("argmax", &argmax);

@@ -209,6 +209,9 @@ __device__ __forceinline__ float4 load_dev4(const float* p) {
     return make_float4(load_dev(p), load_dev(p + 1), load_dev(p + 2), load_dev(p + 3));
 }
 
+constexpr int CNT_STRIDE = 32;   // ints between two arrival counters: one 128-byte line each, so workgroups arriving
+                                 // on different counters never queue on one line's atomics
+
 // True in every thread of the last of `total` workgroups to call it on `counter` (the count is left at total; the
 // last workgroup resets it with store_dev once it has read the partials). Every thread of the workgroup calls it.
 __device__ __forceinline__ bool arrive_last(int* counter, int total, int* sh_flag) {

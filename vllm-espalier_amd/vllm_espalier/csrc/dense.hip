@@ -6,9 +6,9 @@
 // Work split. A workgroup is 4 * KW waves on one 128-column block (the output Hadamard's width) and one K range: of
 // the S = K / 32 steps of 32 k, = SQ * SK + SR, split s takes the next SQ + (s < SR), so SK need not divide S and a
 // launch can match the CU count. Wave (p, kw) owns n tiles 2p, 2p+1 of the block and every KW-th step of the range
-// (gemm.hpp); the KW partial sums are added in order through shared memory. Per 32-k step a wave decodes 2 B operands (trellis -> fp16 in registers, trellis.hpp) and issues one
-// v_mfma_f32_16x16x32_f16 per B operand and 16-row group (rows 0-15, 16-31): weights stream from HBM once for all
-// rows. Split K (SK > 1) goes through Z, and the last workgroup of a column block to arrive (atomic counter) adds the
+// (gemm.hpp); the KW partial sums are added in order through shared memory. Per 32-k step a wave decodes 2 B operands
+// (trellis -> fp16 in registers, trellis.hpp) and issues one v_mfma_f32_16x16x32_f16 per B operand and 16-row group
+// (rows 0-15, 16-31): weights stream from HBM once for all rows. Split K (SK > 1) goes through Z, and the last workgroup of a column block to arrive (atomic counter) adds the
 // splits in order and finishes; counters are left zero.
 //
 // Row invariance: a row's sums depend only on that row (MFMA keeps rows apart), the K split and per-wave ranges
@@ -21,8 +21,6 @@
 namespace esp {
 
 constexpr int MAX_SHARDS = 4;
-constexpr int CNT_STRIDE = 32;   // ints between two column blocks' arrival counters: one 128-byte line each, so the
-                                 // splits of different blocks never queue on one line's atomics
 
 struct Shard {
     const uint32_t* T;       // trellis words [K/16][N/16][4*K2]

@@ -21,13 +21,15 @@ constexpr int STAGE_BYTES = 32 * 1024;
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 typedef __attribute__((address_space(1))) const void* global_void_ptr;
 
+// 32-k steps a stage holds: a step is 2 k tiles x 8 n tiles x 4 * K2 words (>= 8 for K2 <= 16)
+__host__ __device__ constexpr int stage_max_steps(int k2) { return STAGE_BYTES / (2 * 8 * 4 * k2 * 4); }
+
 // LDS layout of a stage: [k tile][8 n tiles][TW words]
 template <int K2>
 struct StagePlan {
     static constexpr int TW = 4 * K2;
     static constexpr int ROW_WORDS = 8 * TW;                                   // one k tile of the block
-    static constexpr int STEP_BYTES = 2 * ROW_WORDS * 4;                       // one 32-k step
-    static constexpr int MAX_STEPS = STAGE_BYTES / STEP_BYTES;                 // >= 8 for K2 <= 16
+    static constexpr int MAX_STEPS = stage_max_steps(K2);
 };
 
 // Copy k tiles [kt0, kt0 + rows) of the block (n tiles nt0..nt0+7) into lds: 16-byte units, 64 a wave instruction.
@@ -45,6 +47,28 @@ __device__ __forceinline__ void issue_stage(const uint32_t* __restrict__ T, int 
             __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
         }
     }
+}
+
+// issue_stage for a K2 known only at run time (a launch whose experts differ in width): the same units in the same
+// LDS places as issue_stage<K2>
+__device__ __forceinline__ void issue_stage_rt(const uint32_t* __restrict__ T, int k2, int NTILES, int kt0, int rows,
+                                               int nt0, uint32_t* lds) {
+    const int TW = 4 * k2, UPR = 2 * TW;
+    const int units = rows * UPR;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int u0 = wave * 64; u0 < units; u0 += (int)blockDim.x) {
+        const int u = u0 + lane;
+        if (u < units) {
+            const int r = u / UPR, w = (u - r * UPR) * 4;
+            const uint32_t* src = T + ((size_t)(kt0 + r) * NTILES + nt0) * TW + w;
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
+        }
+    }
+}
+
+// 32-k steps of the first stage block_gemm expects issued (prologue_issued) for a range of `steps`
+__host__ __device__ constexpr int first_stage_steps(int k2, int steps) {
+    return steps < stage_max_steps(k2) ? steps : stage_max_steps(k2);
 }
 
 __device__ __forceinline__ void wait_stage() {
@@ -153,8 +177,8 @@ __host__ __device__ constexpr int stage_words(int kr) {
 
 // host mirror of stage_words for a runtime K2
 inline int host_stage_words(int k2, int kr) {
-    const int row_words = 32 * k2, step_bytes = 2 * row_words * 4;
-    const int max_steps = STAGE_BYTES / step_bytes;
+    const int row_words = 32 * k2;
+    const int max_steps = stage_max_steps(k2);
     const int steps = kr / 32;
     const int sst = steps < max_steps ? steps : max_steps;
     const int nst = (steps + sst - 1) / sst;

@@ -401,12 +401,28 @@ struct GroupedArgs {
     const int* members;
     float* Z;
     int K, N, P, SK, maxm, slots;
+    // the fused gate/up launch only (esp_moe_gateup: rot_in before, gateup_epilogue after)
+    const void* x;                 // the model's rows, rotated in the launch (gate/up)
+    int x_dtype, x_stride;
+    const uint16_t* suh0;          // [E][K] input signs of gate / up
+    const uint16_t* suh1;
+    const uint16_t* svh0;          // [E][N] output scales of gate / up
+    const uint16_t* svh1;
+    const uint16_t* suh_d;         // [E][N] down input signs (gate/up epilogue)
+    uint16_t* xd;                  // [P][N] fp16 down input
+    float limit;
+    int act_mode;
+    int* counters;                 // arrival counters CNT_STRIDE apart: zero on entry, left zero
+    int stage_bytes, xs_stride;    // rotated rows in shared memory after the stages
 };
 
+// The GEMM of one program. A rows: member m's row is abase + (by_member ? m : its slot row) * astride, holding k from
+// kbase. dev: the partials go to Z with device-scope stores (another workgroup of the launch reads them).
 template <int CB, int K2, int MG>
 __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_t* __restrict__ T,
-                                             const uint16_t* __restrict__ X, const int* rows_sh, int nrows, int mat,
-                                             int split, float scale, uint32_t* stage) {
+                                             const uint16_t* abase, int astride, int kbase, bool by_member,
+                                             const int* rows_sh, int nrows, int mat, int split, float scale,
+                                             uint32_t* stage, bool issued, bool dev) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int c = lane & 15, G = lane >> 4;
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
@@ -416,12 +432,13 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
     RowsA<MG> al;
 #pragma unroll
     for (int g = 0; g < MG; ++g) {
-        const int p = rows_sh[g * 16 + c];
-        al.row[g] = p >= 0 ? X + (size_t)p * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
+        const int m = g * 16 + c;
+        const int p = rows_sh[m];
+        al.row[g] = p >= 0 ? abase + (size_t)(by_member ? m : p) * astride + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
     }
-    al.kbase = 0;
+    al.kbase = kbase;
     f32x4 acc[2][MG];
-    block_gemm<CB, K2, MG>(T, NTILES, nt0, k0, kr, KW, stage, al, acc, false);
+    block_gemm<CB, K2, MG>(T, NTILES, nt0, k0, kr, KW, stage, al, acc, issued);
     // the k slots' partials added in order, then one member row a 32-lane half
     __syncthreads();
     float* red = reinterpret_cast<float*>(stage);
@@ -435,52 +452,11 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
             s4.x += u.x; s4.y += u.y; s4.z += u.z; s4.w += u.w;
         }
         s4.x *= scale; s4.y *= scale; s4.z *= scale; s4.w *= scale;
-        *reinterpret_cast<float4*>(Zm + (size_t)rows_sh[m] * a.N + nt0 * 16 + 4 * l32) = s4;
-    }
-}
-
-__global__ __launch_bounds__(1024) void grouped_kernel(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
-    const int u = blockIdx.x;
-    const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
-    __shared__ int rows_sh[32];
-    __shared__ int nrows;
-    // the count, the expert id and the member rows depend on u alone: all three loads in flight at once
-    // (u < gridDim.x <= the tables' length, so the loads stay in bounds past the count)
-    const int cnt = a.ucount[0];
-    const int e = a.uids[u];
-    if (threadIdx.x < 64) {
-        const int m = threadIdx.x;
-        const int code = m < a.maxm && m < 32 ? a.members[(size_t)u * a.maxm + m] : -1;
-        const int rp = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
-        if (m < 32) rows_sh[m] = rp;
-        const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
-        if (m == 0) nrows = __builtin_popcountll(valid);
-    }
-    if (u >= cnt) return;                                   // workgroup-uniform
-    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? a.TP1[e] : a.TP0[e]);
-    const int k2 = mat ? a.B1[e] : a.B0[e];
-    const int cb = mat ? a.C1[e] : a.C0[e];
-    const uint16_t* X = mat ? a.X1 : a.X0;
-    __syncthreads();
-    if (nrows == 0) return;
-    const bool two = nrows > 16;
-    switch (cb * 32 + k2) {
-#define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
-    case CB_ * 32 + K2_: {                                                                                    \
-        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                          \
-        const float scale = (CB_ == 6 || CB_ == 7) ? grid_c(CB_) : 1.0f;                                      \
-        if (two)                                                                                              \
-            grouped_body<KCB, K2_, 2>(a, T, X, rows_sh, nrows, mat, split, scale, stage);                                   \
-        else                                                                                                  \
-            grouped_body<KCB, K2_, 1>(a, T, X, rows_sh, nrows, mat, split, scale, stage);                                   \
-        break;                                                                                                \
-    }
-        ESP_CASES(ESP_GROUPED_CASE)
-#undef ESP_GROUPED_CASE
-        default:
-            break;                                          // no kernel: Z is left untouched (the host checks tables)
+        float* zp = Zm + (size_t)rows_sh[m] * a.N + nt0 * 16 + 4 * l32;
+        if (dev)
+            store_dev4(zp, s4);
+        else
+            *reinterpret_cast<float4*>(zp) = s4;
     }
 }
 
@@ -489,13 +465,17 @@ __global__ __launch_bounds__(1024) void grouped_kernel(GroupedArgs a) {
 // ------------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
 
-// sum over SK splits (stride apart) of the 4 floats at p, in split order, with up to 8 splits' loads in flight
+// sum over SK splits (stride apart) of the 4 floats at p, in split order, with up to 8 splits' loads in flight;
+// DEV: device-scope loads (partials another workgroup of the same launch stored)
+template <bool DEV = false>
 __device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t stride, int SK, float (&v)[4]) {
     for (int q0 = 0; q0 < SK; q0 += 8) {
         float4 u[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (q0 + i < SK) u[i] = *reinterpret_cast<const float4*>(p + (size_t)(q0 + i) * stride);
+            if (q0 + i < SK)
+                u[i] = DEV ? load_dev4(p + (size_t)(q0 + i) * stride)
+                           : *reinterpret_cast<const float4*>(p + (size_t)(q0 + i) * stride);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             if (q0 + i == 0) {
@@ -511,6 +491,37 @@ __device__ __forceinline__ void load4_f16(const uint16_t* p, float (&v)[4]) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);
     v[0] = h2f((uint16_t)(u.x & 0xFFFFu)); v[1] = h2f((uint16_t)(u.x >> 16));
     v[2] = h2f((uint16_t)(u.y & 0xFFFFu)); v[3] = h2f((uint16_t)(u.y >> 16));
+}
+
+// gate/up epilogue of one (slot row, 4 columns a lane) unit from its summed splits: H, * svh / sqrt(128), SwiGLU
+// (act_mode 1: fp32; 0: with the reference's bf16 roundings; clamped to limit), * suh_d, H / sqrt(128)
+// (experts.cu:120-162). at = e * N + the lane's first column.
+__device__ __forceinline__ void gateup_unit(float (&gv)[4], float (&uv)[4], const uint16_t* __restrict__ svh_g,
+                                            const uint16_t* __restrict__ svh_u, const uint16_t* __restrict__ suh_d,
+                                            size_t at, float limit, int act_mode, int l32, float (&v)[4]) {
+    fwht128(gv, l32);
+    fwht128(uv, l32);
+    float sg[4], su[4], sd[4];
+    load4_f16(svh_g + at, sg);
+    load4_f16(svh_u + at, su);
+    load4_f16(suh_d + at, sd);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float act;
+        if (act_mode == 0) {
+            const float gg = fminf(bf16r(gv[j] * HAD_SCALE * sg[j]), limit);
+            const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * su[j]), -limit), limit);
+            act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
+        } else {
+            const float gg = fminf(gv[j] * HAD_SCALE * sg[j], limit);
+            const float uu = fminf(fmaxf(uv[j] * HAD_SCALE * su[j], -limit), limit);
+            act = gg / (1.f + expf(-gg)) * uu;
+        }
+        v[j] = __fmul_rn(act, sd[j]);
+    }
+    fwht128(v, l32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] *= HAD_SCALE;
 }
 
 __global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
@@ -531,30 +542,8 @@ __global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __res
     sum_splits4(Z + ((size_t)SK * P + p) * N + n, (size_t)P * N, SK, uv);
     const int e = pick[p];
     if (e < 0 || e >= E) return;
-    fwht128(gv, l32);
-    fwht128(uv, l32);
-    float sg[4], su[4], sd[4];
-    load4_f16(svh_g + (size_t)e * N + n, sg);
-    load4_f16(svh_u + (size_t)e * N + n, su);
-    load4_f16(suh_d + (size_t)e * N + n, sd);
     float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float act;
-        if (act_mode == 0) {
-            const float gg = fminf(bf16r(gv[j] * HAD_SCALE * sg[j]), limit);
-            const float uu = fminf(fmaxf(bf16r(uv[j] * HAD_SCALE * su[j]), -limit), limit);
-            act = bf16r(bf16r(gg / (1.f + expf(-gg))) * uu);
-        } else {
-            const float gg = fminf(gv[j] * HAD_SCALE * sg[j], limit);
-            const float uu = fminf(fmaxf(uv[j] * HAD_SCALE * su[j], -limit), limit);
-            act = gg / (1.f + expf(-gg)) * uu;
-        }
-        v[j] = __fmul_rn(act, sd[j]);
-    }
-    fwht128(v, l32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] *= HAD_SCALE;
+    gateup_unit(gv, uv, svh_g, svh_u, suh_d, (size_t)e * N + n, limit, act_mode, l32, v);
     store4(xd, F16, (size_t)p * N + n, v);
 }
 
@@ -588,23 +577,22 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     out[(size_t)r * D + d] = acc;
 }
 
-// down epilogue of every slot of one (row, 128-block) into shared memory, then the routed fma chain in slot order and
-// the shared slot's gated output. n_routed == slots and out_shared == nullptr give down_combine.
+// down epilogue of every slot of one (row r, 128-block) into part, then the routed fma chain in slot order and the
+// shared slot's gated output (experts.cu:340-393); n_routed == slots and out_shared == nullptr give down_combine. At
+// least 256 threads; every thread calls it.
 template <int OUT_DTYPE>
-__global__ __launch_bounds__(256) void down_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
-                                                           const uint16_t* __restrict__ svh_d, float* __restrict__ y,
-                                                           const float* __restrict__ wts, void* __restrict__ out,
-                                                           void* __restrict__ out_shared, int P, int D, int SK, int E,
-                                                           int slots, int n_routed) {
-    __shared__ float part[32][128];
-    const int r = blockIdx.x, blk = blockIdx.y;
-    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5;
+__device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                  const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+                                                  const float* __restrict__ wts, void* __restrict__ out,
+                                                  void* __restrict__ out_shared, int P, int D, int SK, int E,
+                                                  int slots, int n_routed, int r, int blk, float (*part)[128]) {
+    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5, nhw = (int)(blockDim.x >> 5);
     const int n0 = blk * 128;
-    for (int k = hw; k < slots; k += 8) {
+    for (int k = hw; k < slots; k += nhw) {
         const int p = r * slots + k;
         const int n = n0 + 4 * l32;
         float v[4];
-        sum_splits4(Z + (size_t)p * D + n, (size_t)P * D, SK, v);       // in flight with the pick
+        sum_splits4(Z + (size_t)p * D + n, (size_t)P * D, SK, v);            // in flight with the pick
         const int e = pick[p];
         float o[4];
         if (e >= 0 && e < E) {
@@ -630,11 +618,111 @@ __global__ __launch_bounds__(256) void down_combine_kernel(const float* __restri
         if constexpr (OUT_DTYPE == F32) static_cast<float*>(out)[at] = acc;
         else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out)[at] = f2bf(acc);
         else static_cast<uint16_t*>(out)[at] = f2h(acc);
-    } else if (out_shared != nullptr && n_routed < slots) {
+    } else if (threadIdx.x < 256 && out_shared != nullptr && n_routed < slots) {
         const float v = wts[r * slots + n_routed] * part[n_routed][col];
         if constexpr (OUT_DTYPE == F32) static_cast<float*>(out_shared)[at] = v;
         else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out_shared)[at] = f2bf(v);
         else static_cast<uint16_t*>(out_shared)[at] = f2h(v);
+    }
+}
+
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(256) void down_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+                                                           const uint16_t* __restrict__ svh_d, float* __restrict__ y,
+                                                           const float* __restrict__ wts, void* __restrict__ out,
+                                                           void* __restrict__ out_shared, int P, int D, int SK, int E,
+                                                           int slots, int n_routed) {
+    __shared__ float part[32][128];
+    down_combine_unit<OUT_DTYPE>(Z, pick, svh_d, y, wts, out, out_shared, P, D, SK, E, slots, n_routed, blockIdx.x,
+                                 blockIdx.y, part);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The grouped kernel. MODE 0: esp_grouped. MODE 1 (esp_moe_gateup): the member rows' K range rotated into shared
+// memory in the launch (rot_in's arithmetic), and the last of the 2 * SK programs of an (expert, 128-column block) to
+// arrive runs gateup_epilogue for its member rows.
+// ------------------------------------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
+    const int u = blockIdx.x;
+    const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
+    const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
+    const int NW = (int)(blockDim.x >> 6);
+    __shared__ int rows_sh[32];
+    __shared__ int nrows;
+    // the count, the expert id and the member rows depend on u alone: all three loads in flight at once
+    // (u < gridDim.x <= the tables' length, so the loads stay in bounds past the count)
+    const int cnt = a.ucount[0];
+    const int e = a.uids[u];
+    if (threadIdx.x < 64) {
+        const int m = threadIdx.x;
+        const int code = m < a.maxm && m < 32 ? a.members[(size_t)u * a.maxm + m] : -1;
+        const int rp = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
+        if (m < 32) rows_sh[m] = rp;
+        const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
+        if (m == 0) nrows = __builtin_popcountll(valid);
+    }
+    if (u >= cnt) return;                                   // workgroup-uniform
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(mat ? a.TP1[e] : a.TP0[e]);
+    const int k2 = mat ? a.B1[e] : a.B0[e];
+    const int cb = mat ? a.C1[e] : a.C0[e];
+    __syncthreads();
+    if (nrows == 0) return;
+    const int kr = a.K / a.SK, k0 = split * kr;
+    const uint16_t* abase = mat ? a.X1 : a.X0;
+    int astride = a.K, kbase = 0;
+    if constexpr (MODE == 1) {
+        // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory
+        issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), blockIdx.y * 8, stage);
+        uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
+        const uint16_t* suh = (mat ? a.suh1 : a.suh0) + (size_t)e * a.K;
+        const int chunks = kr >> 7;
+        for (int idx = wave * 2 + half; idx < nrows * chunks; idx += 2 * NW) {
+            const int m = idx / chunks, ch = idx - m * chunks;
+            const int row = rows_sh[m] / a.slots;
+            const int kb = k0 + ch * 128;
+            const uint2 v = rot128(a.x, a.x_dtype, (size_t)row * a.x_stride + kb, suh + kb, l32);
+            *reinterpret_cast<uint2*>(xs + (size_t)m * a.xs_stride + ch * 128 + 4 * l32) = v;
+        }
+        abase = xs;
+        astride = a.xs_stride;
+        kbase = k0;
+    }
+    const bool two = nrows > 16;
+    switch (cb * 32 + k2) {
+#define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
+    case CB_ * 32 + K2_: {                                                                                    \
+        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                          \
+        const float scale = (CB_ == 6 || CB_ == 7) ? grid_c(CB_) : 1.0f;                                      \
+        if (two)                                                                                              \
+            grouped_body<KCB, K2_, 2>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
+                                      scale, stage, MODE == 1, MODE == 1);                                    \
+        else                                                                                                  \
+            grouped_body<KCB, K2_, 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
+                                      scale, stage, MODE == 1, MODE == 1);                                    \
+        break;                                                                                                \
+    }
+        ESP_CASES(ESP_GROUPED_CASE)
+#undef ESP_GROUPED_CASE
+        default:
+            break;                                          // no kernel: Z is left untouched (the host checks tables)
+    }
+    if constexpr (MODE == 1) {
+        __shared__ int last;
+        int* cnt_p = a.counters + ((size_t)u * gridDim.y + blockIdx.y) * CNT_STRIDE;
+        if (!arrive_last(cnt_p, 2 * a.SK, &last)) return;
+        const int n = blockIdx.y * 128 + 4 * l32;
+        for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+            const int p = rows_sh[m];
+            float gv[4], uv[4], v[4];
+            sum_splits4<true>(a.Z + (size_t)p * a.N + n, (size_t)a.P * a.N, a.SK, gv);
+            sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv);
+            gateup_unit(gv, uv, a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + n, a.limit, a.act_mode, l32, v);
+            store4(a.xd, F16, (size_t)p * a.N + n, v);
+        }
+        if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every program of the block arrived
     }
 }
 
@@ -786,11 +874,82 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
     const size_t smem = stage > red ? stage : red;
     if (smem > 64 * 1024 &&
-        hipFuncSetAttribute((const void*)grouped_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+        hipFuncSetAttribute((const void*)grouped_kernel_t<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
             hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "grouped: cannot raise the shared memory limit to %zu bytes", smem);
-    grouped_kernel<<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
+    grouped_kernel_t<0><<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("grouped");
+}
+
+static int grouped_launch_gateup(const GroupedArgs& a, int64_t nexp_max, int64_t warps, size_t smem, hipStream_t st) {
+    if (smem > 64 * 1024 && hipFuncSetAttribute((const void*)grouped_kernel_t<1>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "moe_gateup: cannot raise the shared memory limit to %zu bytes", smem);
+    dim3 grid((unsigned)nexp_max, (unsigned)(a.N / 128), (unsigned)(2 * a.SK));
+    grouped_kernel_t<1><<<grid, (unsigned)(64 * warps), smem, st>>>(a);
+    return esp_host::launch_check("moe_gateup");
+}
+
+extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                              const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1,
+                              const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
+                              const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel,
+                              int32_t* counters, int64_t counters_numel, const void* svh_g, const void* svh_u,
+                              const void* suh_d, void* xd, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
+                              int64_t warps, int64_t lo, int64_t hi, double limit, int64_t act_mode, void* stream) {
+    ESP_REQUIRE(x && suh_g && suh_u && TP0 && TP1 && B0 && B1 && C0 && C1 && uids && ucount && members && Z &&
+                    counters && svh_g && svh_u && suh_d && xd,
+                "moe_gateup: null pointer");
+    ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
+    ESP_REQUIRE(SK >= 1 && K > 0 && N > 0 && K % (128 * SK) == 0 && N % 128 == 0,
+                "moe_gateup: K must split into whole 128-blocks, N a multiple of 128");
+    ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE(z_numel >= 2 * SK * P * N, "Z too small");
+    ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
+    ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
+    ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
+    ESP_REQUIRE(warps == 4 || warps == 8 || warps == 16, "warps (waves a workgroup) must be 4, 8 or 16");
+    ESP_REQUIRE(counters_numel >= nexp_max * (N / 128) * CNT_STRIDE, "counters: 32 ints per (expert, 128 columns)");
+    if (nexp_max <= 0) return esp_host::ok();
+    GroupedArgs a{};
+    a.X0 = a.X1 = nullptr;
+    a.TP0 = TP0;
+    a.TP1 = TP1;
+    a.B0 = B0;
+    a.B1 = B1;
+    a.C0 = C0;
+    a.C1 = C1;
+    a.uids = uids;
+    a.ucount = ucount;
+    a.members = members;
+    a.Z = Z;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)P;
+    a.SK = (int)SK;
+    a.maxm = (int)maxm;
+    a.slots = (int)slots;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.x_stride = (int)x_stride;
+    a.suh0 = static_cast<const uint16_t*>(suh_g);
+    a.suh1 = static_cast<const uint16_t*>(suh_u);
+    a.svh0 = static_cast<const uint16_t*>(svh_g);
+    a.svh1 = static_cast<const uint16_t*>(svh_u);
+    a.suh_d = static_cast<const uint16_t*>(suh_d);
+    a.xd = static_cast<uint16_t*>(xd);
+    a.limit = (float)limit;
+    a.act_mode = (int)act_mode;
+    a.counters = counters;
+    const int64_t kr = K / SK;
+    const size_t stage = (size_t)host_stage_words((int)hi, (int)kr) * 4;   // the widest expert's stages
+    a.stage_bytes = (int)stage;
+    a.xs_stride = (int)kr + 8;                                             // pad rows across the LDS banks
+    const size_t xs = (size_t)32 * a.xs_stride * 2;
+    const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;
+    const size_t smem = stage + xs > red ? stage + xs : red;
+    ESP_REQUIRE(smem <= 160 * 1024, "moe_gateup: shared memory exceeds 160 KiB");
+    return grouped_launch_gateup(a, nexp_max, warps, smem, (hipStream_t)stream);
 }
 
 extern "C" int esp_gateup_epilogue(const float* Z, const int32_t* pick, const void* svh_g, const void* svh_u,

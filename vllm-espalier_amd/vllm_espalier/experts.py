@@ -37,6 +37,12 @@ KERNEL_CB = {0: 1, 1: 3, 3: 6, 4: 7}
 COMPILED = {(1, k2) for k2 in range(2, 17, 2)} | {(3, 2), (3, 4), (3, 6), (6, 4), (6, 6), (6, 8), (7, 6), (7, 8),
                                                    (7, 10)}
 ACT_F32 = 1
+# routed2 with rot_in, the gate/up GEMM and its epilogue in one launch (esp_moe_gateup) for windows of up to
+# FUSED_ROWS rows: one launch less than two hand-offs cost (MI355X, 1 token: 2.2 us a layer less). Wider windows keep
+# the reference's sequence, since each (expert, 128 columns) program rotates its rows again. Same bits either way.
+# ESPALIER_MOE_FUSED=0 turns it off.
+FUSED = env("ESPALIER_MOE_FUSED", "1") != "0"
+FUSED_ROWS = 4
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 
@@ -186,6 +192,9 @@ class Scratch:
         self.ids = torch.zeros((maxu,), dtype=torch.int32, device=device)
         self.count = torch.zeros((1,), dtype=torch.int32, device=device)
         self.members = torch.full((maxu * rows,), -1, dtype=torch.int32, device=device)
+        # arrival counters of the fused gate/up launch, one per (expert, 128 columns), 32 ints apart, zero between
+        # launches
+        self.counters = torch.zeros((maxu * (I // 128) * 32,), dtype=torch.int32, device=device)
         self.rows, self.slots, self.E = rows, slots, E
 
     def window(self, R: int):
@@ -271,21 +280,27 @@ def routed2(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     pk, wt = s.pick[:P], s.wts[:P]
     if pick is not None:
         e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pk, wt, ids, s.count, members, R, k, E)
-    e.rot_in(x, x.stride(0), pk, L.suh_g, L.suh_u, s.xg, s.xu, R, D, slots, E)
-    nt, w, sk, pf = s.cfg_gu
-    e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
-              D, I, P, sk, slots, nt, w, pf, L.k2_gu[0], L.k2_gu[1])
-    e.gateup_epilogue(s.z, pk, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, I, sk, slots, E, math.inf, ACT_F32)
-    nt, w, sk, pf = s.cfg_d
-    e.grouped(s.xd, s.xd, L.ptr[2], L.ptr[2], L.k2[2], L.k2[2], L.cb[2], L.cb[2], ids, s.count, members, s.z, 1,
-              I, D, P, sk, slots, nt, w, pf, L.k2_d[0], L.k2_d[1])
     if out is None:
         out = torch.empty((R, D), dtype=x.dtype, device=x.device)
     if L.shared_id >= 0 and out_shared is None:
         out_shared = torch.empty((R, D), dtype=x.dtype, device=x.device)
-    e.down_combine2(s.z, pk, L.svh_d, s.y, wt, out, out_shared if L.shared_id >= 0 else None, R, P, D, sk, slots,
-                    E, k)
-    return out, (out_shared if L.shared_id >= 0 else None)
+    osh = out_shared if L.shared_id >= 0 else None
+    nt, w, sk, pf = s.cfg_gu
+    if FUSED and R <= FUSED_ROWS and (D // sk) % 128 == 0:
+        # rot_in + gate/up + its epilogue in one launch (the same arithmetic in the same order: the same bits)
+        e.moe_gateup(x, x.stride(0), L.suh_g, L.suh_u, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids,
+                     s.count, members, s.z, s.counters, L.svh_g, L.svh_u, L.suh_d, s.xd, D, I, P, sk, slots, w,
+                     L.k2_gu[0], L.k2_gu[1], math.inf, ACT_F32)
+    else:
+        e.rot_in(x, x.stride(0), pk, L.suh_g, L.suh_u, s.xg, s.xu, R, D, slots, E)
+        e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
+                  D, I, P, sk, slots, nt, w, pf, L.k2_gu[0], L.k2_gu[1])
+        e.gateup_epilogue(s.z, pk, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, I, sk, slots, E, math.inf, ACT_F32)
+    nt, w, sk, pf = s.cfg_d
+    e.grouped(s.xd, s.xd, L.ptr[2], L.ptr[2], L.k2[2], L.k2[2], L.cb[2], L.cb[2], ids, s.count, members, s.z, 1,
+              I, D, P, sk, slots, nt, w, pf, L.k2_d[0], L.k2_d[1])
+    e.down_combine2(s.z, pk, L.svh_d, s.y, wt, out, osh, R, P, D, sk, slots, E, k)
+    return out, osh
 
 
 def dequant(trellis: torch.Tensor, K: int, grid: int) -> torch.Tensor:
