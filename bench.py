@@ -32,6 +32,10 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
+# HBM bytes a qkv launch moves at batch 1, from the two rocprofv3 --pmc passes over `bench.py --traffic-probe` (the
+# summary under profiles/): FETCH_SIZE 2762.4 KiB x 2.000 + WRITE_SIZE 498.8 KiB x 1.000, the factors being what the
+# counters read for a 256 MiB copy. Re-measured whenever the dense kernel changes.
+QKV_TRAFFIC_BYTES = 6168115
 COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
 
 
@@ -261,6 +265,31 @@ def cpu_baseline(block, reps: int):
 
 
 # ---------------------------------------------------------------------------------------------------------------
+# HBM traffic of the roofline kernel: the workload rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs read
+# ---------------------------------------------------------------------------------------------------------------
+CALIB_BYTES = 256 << 20
+
+
+def traffic_probe(dev) -> None:
+    """Two replays of the roofline graph (98 cold qkv launches at batch 1, as in the bench) and two copies of
+    CALIB_BYTES, the plain copy kernel whose counters scale the qkv launch's (a copy reads and writes its size)."""
+    import torch
+    probe = dense_stack(1, 1, dev)
+    copies = max(2, -(-COLD_BYTES // block_bytes(probe[0])))
+    del probe
+    stack = dense_stack(copies, 2, dev)
+    g = run_dense(stack, 1, dev, which=[0])
+    for _ in range(2):
+        g.replay()
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"traffic probe: {copies} qkv launches x 2, copy of {CALIB_BYTES} B x 2")
+
+
+# ---------------------------------------------------------------------------------------------------------------
 # rocprofv3 summaries (the text kept under profiles/)
 # ---------------------------------------------------------------------------------------------------------------
 def rocprof_summary(d: str, top: int = 30) -> str:
@@ -301,6 +330,19 @@ def rocprof_summary(d: str, top: int = 30) -> str:
             out.append(f"| `{n}` | {shape} | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | "
                        f"{v[-1]:.2f} |")
         out.append("")
+    pmc = next(root.rglob("*counter_collection.csv"), None)
+    if pmc is not None:
+        groups = defaultdict(list)
+        for r in csv.DictReader(open(pmc)):
+            n = r["Kernel_Name"].replace("void ", "").split("(")[0]
+            shape = r.get("Grid_Size") or f"{r.get('Grid_Size_X', '?')}x{r.get('Grid_Size_Y', '?')}x{r.get('Grid_Size_Z', '?')}"
+            groups[(n[:80], shape, r["Counter_Name"])].append(float(r["Counter_Value"]))
+        items = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
+        out += ["Counters (counter_collection.csv), per dispatch, grouped by kernel, grid size (threads) and counter:", "",
+                "| kernel | grid | counter | dispatches | average | min | max |", "|---|---|---|---:|---:|---:|---:|"]
+        for (n, shape, c), v in items[:top]:
+            out.append(f"| `{n}` | {shape} | {c} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
+        out.append("")
     return "\n".join(out)
 
 
@@ -316,6 +358,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=20)
     ap.add_argument("--rocprof-summary", metavar="DIR", help="print the markdown summary of a rocprofv3 csv output "
                     "directory and exit (no GPU work)")
+    ap.add_argument("--traffic-probe", action="store_true", help="run only the workload of the FETCH_SIZE / "
+                    "WRITE_SIZE counter passes (the roofline graph and a calibration copy) and exit")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
@@ -333,6 +377,9 @@ def main() -> int:
     G.ext()                                   # the HIP extension must be there: no fallback
     name = torch.cuda.get_device_name(dev)
     log(f"device {name}")
+    if a.traffic_probe:
+        traffic_probe(dev)
+        return 0
 
     # ---- config 2 dense block, cold stack
     probe = dense_stack(1, 1, dev)
@@ -445,7 +492,7 @@ def main() -> int:
         "route_group": route,
         "decoder": decoder,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": QKV_TRAFFIC_BYTES,
                      "kernel": "dense_kernel (qkv launch, 5,269,504 B a launch)"},
         "cpu_baseline": cpu,
     }
