@@ -141,6 +141,26 @@ int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh
                    int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps, int64_t lo, int64_t hi,
                    double limit, int64_t act_mode, void* stream);
 
+/* esp_dense with the input rows normalised in the launch: x = RMSNorm(h + d1 + d2) * norm_w (d1, d2 may be NULL),
+ * bit-identical to esp_add_rmsnorm followed by esp_dense; the residual h + d1 + d2 is stored to h_out (not h: other
+ * workgroups still read h). No counterpart in the reference (vLLM runs the norm as its own launch). M <= W / 4,
+ * K <= 8192, bf16/fp16 rows x_stride apart, the fused rotation (M * K / SK * 2 <= rot_smem); no xh. */
+int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, const void* norm_w, double eps, void* h_out,
+                      int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards, const void* const* trellis,
+                      const void* const* suh, const void* const* svh, const int64_t* n_cols, const int64_t* col0,
+                      void* y, int y_dtype, int64_t y_stride, int64_t y_cols, float* Z, int64_t z_numel,
+                      int32_t* counters, int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W,
+                      int64_t rot_smem, void* stream);
+
+/* esp_route_group with the router input normalised in the launch: x = RMSNorm(h + d1) * norm_w, bit-identical to
+ * esp_add_rmsnorm followed by esp_route_group; x is stored to a_out and the residual h + d1 to h_out. No counterpart in
+ * the reference. R <= 4, H <= 8192, rows x_stride apart, 16-byte aligned. */
+int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, double eps, void* h_out, void* a_out,
+                            int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
+                            const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
+                            int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu,
+                            int32_t* ucount, int32_t* members, int64_t maxm, void* stream);
+
 /* ---- Decode-step glue (csrc/step.hip). No counterpart in the reference extension: in a served model vLLM does
  * these (VocabParallelEmbedding, fused_add_rms_norm, the greedy sampler). They let the synthetic decoder step run as
  * one HIP graph whose next token stays on the device. ---- */

@@ -143,3 +143,24 @@ def test_decoder_graph_replay_equals_eager(small_decoder):
         assert torch.equal(b.logits.cpu().view(torch.int16), eager[i][0].view(torch.int16)), i
         assert int(b.ids_out.item()) == eager[i][1], i
         torch.randn((64, 64), device=b.h.device).sum()        # eager work between replays
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_decoder_fused_norms_equal_separate(small_decoder, T, monkeypatch):
+    """The norms inside the qkv, routing and head launches (dense_rmsnorm, route_group_rmsnorm) against add_rmsnorm
+    launches of their own: logits and the residual stream bit for bit."""
+    dec = small_decoder
+    ids = [7, 1234, 4000][:T]
+    res = {}
+    for fused in (False, True):
+        monkeypatch.setattr(S, "FUSE_NORMS", fused)
+        assert dec.fused_norms(T) == fused
+        b = dec.buffers(T)
+        b.ids_in.copy_(torch.tensor(ids, dtype=torch.int32))
+        dec.forward(T)
+        torch.cuda.synchronize()
+        final_residual = b.h2 if fused else b.h               # the fused head stores it to the second buffer
+        res[fused] = (b.logits.cpu().clone(), final_residual.cpu().clone(), b.ids_out.cpu().clone())
+    for x, y in zip(res[False], res[True]):
+        assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x,
+                           y.view(torch.int16) if y.dtype == torch.bfloat16 else y)

@@ -268,6 +268,94 @@ void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optiona
                          members.size(1), cur_stream()));
 }
 
+// dense with its input rows normalised in the launch (no reference counterpart): h, d1, d2 [M, K] contiguous rows
+void dense_rmsnorm(const at::Tensor& h, const c10::optional<at::Tensor>& d1, const c10::optional<at::Tensor>& d2,
+                   const at::Tensor& norm_w, double eps, at::Tensor h_out, const std::vector<at::Tensor>& T,
+                   const std::vector<at::Tensor>& suh, const std::vector<at::Tensor>& svh,
+                   const std::vector<int64_t>& col0, at::Tensor y, at::Tensor Z, at::Tensor counters, int64_t k2,
+                   int64_t cb, int64_t SK, int64_t W, int64_t rot_smem) {
+    TORCH_CHECK(h.is_cuda() && h.dim() == 2 && h.is_contiguous(), "h: CUDA [M, K] contiguous");
+    const auto t = h.scalar_type();
+    TORCH_CHECK(t == at::kBFloat16 || t == at::kHalf, "h: bf16/fp16");
+    for (const auto* d : {&d1, &d2})
+        if (d->has_value()) TORCH_CHECK((*d)->is_contiguous() && (*d)->scalar_type() == t && (*d)->sizes() == h.sizes(),
+                                        "deltas: h's dtype and shape, contiguous");
+    check(norm_w, t, "norm_w");
+    check(h_out, t, "h_out");
+    TORCH_CHECK(norm_w.numel() == h.size(1) && h_out.sizes() == h.sizes(), "norm_w: [K]; h_out: h's shape");
+    TORCH_CHECK(y.is_cuda() && y.dim() == 2 && y.stride(1) == 1, "y: CUDA [M, N], unit column stride");
+    TORCH_CHECK(T.size() == suh.size() && T.size() == svh.size() && T.size() == col0.size(), "one entry a matrix");
+    TORCH_CHECK(T.size() >= 1 && T.size() <= 4, "1 to 4 matrices a launch");
+    const int64_t M = h.size(0), K = h.size(1);
+    std::vector<const void*> tp, sp, vp;
+    std::vector<int64_t> ncols;
+    for (size_t s = 0; s < T.size(); ++s) {
+        TORCH_CHECK(T[s].is_cuda() && T[s].scalar_type() == at::kShort && T[s].is_contiguous() && T[s].dim() == 3,
+                    "trellis: contiguous int16 [K/16, N/16, 16K]");
+        check(suh[s], at::kHalf, "suh");
+        check(svh[s], at::kHalf, "svh");
+        TORCH_CHECK(col0[s] + svh[s].numel() <= y.size(1), "matrix columns past y");
+        TORCH_CHECK(T[s].size(0) * 16 == K && T[s].size(1) * 16 == svh[s].numel() && T[s].size(2) == 8 * k2,
+                    "matrix shape");
+        TORCH_CHECK(suh[s].numel() == K, "suh must have K elements");
+        tp.push_back(T[s].data_ptr());
+        sp.push_back(suh[s].data_ptr());
+        vp.push_back(svh[s].data_ptr());
+        ncols.push_back(svh[s].numel());
+    }
+    check(Z, at::kFloat, "Z");
+    check(counters, at::kInt, "counters");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(h.device());
+    call(esp_dense_rmsnorm(h.data_ptr(), d1.has_value() ? d1->data_ptr() : nullptr,
+                           d2.has_value() ? d2->data_ptr() : nullptr, norm_w.data_ptr(), eps, h_out.data_ptr(),
+                           dtype_code(h), h.stride(0), M, K, (int64_t)T.size(), tp.data(), sp.data(), vp.data(),
+                           ncols.data(), col0.data(), y.data_ptr(), dtype_code(y), y.stride(0), y.size(1),
+                           mptr<float>(Z), Z.numel(), mptr<int32_t>(counters), counters.numel(), k2, cb, SK, W,
+                           rot_smem, cur_stream()));
+}
+
+// route_group with its input normalised in the launch (no reference counterpart): x = RMSNorm(h + d1) * norm_w
+void route_group_rmsnorm(const at::Tensor& h, const c10::optional<at::Tensor>& d1, const at::Tensor& norm_w,
+                         double eps, at::Tensor h_out, at::Tensor a_out, const at::Tensor& gate,
+                         const c10::optional<at::Tensor>& sgate, int64_t k, int64_t shared_id, at::Tensor logits,
+                         at::Tensor counter, at::Tensor pick_out, at::Tensor wts_out, at::Tensor uids,
+                         at::Tensor ucount, at::Tensor members) {
+    TORCH_CHECK(h.is_cuda() && h.dim() == 2 && h.is_contiguous() && gate.is_contiguous(), "h / gate layout");
+    const auto t = h.scalar_type();
+    TORCH_CHECK(t == at::kBFloat16 || t == at::kHalf, "h: bf16/fp16");
+    TORCH_CHECK(gate.scalar_type() == t, "gate and h must share a dtype");
+    if (d1.has_value())
+        TORCH_CHECK(d1->is_contiguous() && d1->scalar_type() == t && d1->sizes() == h.sizes(),
+                    "d1: h's dtype and shape");
+    check(norm_w, t, "norm_w");
+    check(h_out, t, "h_out");
+    check(a_out, t, "a_out");
+    TORCH_CHECK(norm_w.numel() == h.size(1) && h_out.sizes() == h.sizes() && a_out.sizes() == h.sizes(),
+                "norm_w: [H]; h_out / a_out: h's shape");
+    check(logits, at::kFloat, "logits");
+    check(counter, at::kInt, "counter");
+    check(pick_out, at::kInt, "pick_out");
+    check(wts_out, at::kFloat, "wts_out");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    TORCH_CHECK(members.dim() == 2, "members: [nexp_max, maxm]");
+    TORCH_CHECK(gate.dim() == 2 && gate.size(1) == h.size(1), "gate: [E, H]");
+    if (sgate.has_value())
+        TORCH_CHECK(sgate->scalar_type() == t && sgate->is_contiguous() && sgate->numel() == h.size(1),
+                    "sgate: h's dtype, [H]");
+    const int64_t R = h.size(0), H = h.size(1), E = gate.size(0);
+    const int64_t slots = k + (shared_id >= 0);
+    TORCH_CHECK(pick_out.numel() >= R * slots && wts_out.numel() >= R * slots, "pick / wts too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(h.device());
+    call(esp_route_group_rmsnorm(h.data_ptr(), d1.has_value() ? d1->data_ptr() : nullptr, norm_w.data_ptr(), eps,
+                                 h_out.data_ptr(), a_out.data_ptr(), dtype_code(h), h.stride(0), R, H, gate.data_ptr(),
+                                 E, sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits),
+                                 logits.numel(), mptr<int32_t>(counter), mptr<int32_t>(pick_out),
+                                 mptr<float>(wts_out), mptr<int32_t>(uids), uids.numel(), mptr<int32_t>(ucount),
+                                 mptr<int32_t>(members), members.size(1), cur_stream()));
+}
+
 void had(const at::Tensor& x, const c10::optional<at::Tensor>& pre, const c10::optional<at::Tensor>& post,
          at::Tensor y) {
     check(x, at::kHalf, "x");
@@ -364,6 +452,8 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("combine", &combine);
     m.def("down_combine", &down_combine);
     m.def("moe_gateup", &moe_gateup);
+    m.def("dense_rmsnorm", &dense_rmsnorm);
+    m.def("route_group_rmsnorm", &route_group_rmsnorm);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);
     m.def("argmax", &argmax);

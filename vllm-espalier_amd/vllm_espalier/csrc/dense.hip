@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "trellis.hpp"
 #include "gemm.hpp"
+#include "norm.hpp"
 #include "../../../include/espalier.h"
 
 namespace esp {
@@ -42,6 +43,15 @@ struct DenseArgs {
     int* counters;
     int M, K, SK, NBT, fused, xs_stride, stage_bytes;
     int SQ, SR;              // K / 32 steps = SQ * SK + SR: split s has SQ + (s < SR) steps
+    // esp_dense_rmsnorm: the input rows are RMSNorm(h + d1 + d2) * nw (norm.hpp), made in the launch; workgroup (0, 0)
+    // stores the residual h + d1 + d2 to nh_out. Rows of h, d1, d2 and nh_out are x_stride apart.
+    const uint16_t* nh;
+    const uint16_t* nd1;
+    const uint16_t* nd2;
+    const uint16_t* nw;
+    uint16_t* nh_out;
+    float neps;
+    int norm;
 };
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -186,11 +196,28 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         // the 128-blocks the K range touches (a split may start or end inside one)
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const int c0 = k0 >> 7, chunks = ((k0 + kr + 127) >> 7) - c0;
-        for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
-            const int r = idx / chunks, ch = idx % chunks;
-            const int kb = (c0 + ch) * 128;
-            const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + kb, S.suh + kb, l32);
-            *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) = u;
+        if (a.norm) {
+            // every workgroup normalises the rows itself: the whole row's sum of squares, then its K range
+            __shared__ float npart[16], ninv[4];
+            const bool bf = a.x_dtype == BF16;
+            norm_rows_inv(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv);
+            if (nbg == 0 && split == 0) norm_rows_store(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, bf, a.nh_out);
+            for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
+                const int r = idx / chunks, ch = idx % chunks;
+                const int kb = (c0 + ch) * 128;
+                const size_t ro = (size_t)r * a.x_stride;
+                const RotIn in = norm_rot_load(a.nh + ro, a.nd1 ? a.nd1 + ro : nullptr, a.nd2 ? a.nd2 + ro : nullptr,
+                                               a.nw + kb, kb, ninv[r], bf, S.suh + kb, l32);
+                *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) =
+                    rot128_apply(in, a.x_dtype, l32);
+            }
+        } else {
+            for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
+                const int r = idx / chunks, ch = idx % chunks;
+                const int kb = (c0 + ch) * 128;
+                const uint2 u = rot128(a.x, a.x_dtype, (size_t)r * a.x_stride + kb, S.suh + kb, l32);
+                *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) = u;
+            }
         }
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
@@ -323,13 +350,21 @@ extern "C" int esp_had(const void* x, const void* pre, const void* post, void* y
     return esp_host::launch_check("had");
 }
 
-extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
-                         const void* const* trellis, const void* const* suh, const void* const* svh,
-                         const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
-                         int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters,
-                         int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
-                         int64_t rot_smem, void* stream) {
-    (void)PF;
+struct DenseNorm {
+    const void* h;
+    const void* d1;
+    const void* d2;
+    const void* w;
+    void* h_out;
+    double eps;
+};
+
+static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                      const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
+                      const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,
+                      int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel,
+                      int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t rot_smem, const DenseNorm* nrm,
+                      void* stream) {
     ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "1 to 4 matrices a launch");
     ESP_REQUIRE(M >= 1 && M <= 32, "1 to 32 rows");
     ESP_REQUIRE(K > 0 && K % 128 == 0 && SK >= 1 && SK <= K / 32,
@@ -364,6 +399,23 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     const int64_t chunks_max = aligned ? steps_max / 4 : (steps_max * 32 + 96 + 127) / 128;
     const int xs_stride = (int)(chunks_max * 128) + 8;        // pad rows across the LDS banks
     const bool fused = M * chunks_max * 128 * 2 <= rot_smem;
+    if (nrm) {
+        ESP_REQUIRE(nrm->h && nrm->w && nrm->h_out, "dense_rmsnorm: null pointer");
+        ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "dense_rmsnorm: rows must be bf16 or fp16");
+        ESP_REQUIRE(M <= W / 4, "dense_rmsnorm: at most W / 4 rows (four waves normalise a row)");
+        ESP_REQUIRE(K % 8 == 0 && K <= NORM_MAX_D && x_stride % 8 == 0 &&
+                        ((uintptr_t)nrm->h | (uintptr_t)nrm->d1 | (uintptr_t)nrm->d2 | (uintptr_t)nrm->w |
+                         (uintptr_t)nrm->h_out) % 16 == 0,
+                    "dense_rmsnorm: K at most 8192, rows 16-byte aligned");
+        ESP_REQUIRE(fused, "dense_rmsnorm: the rows must fit the fused rotation's shared memory");
+        a.nh = static_cast<const uint16_t*>(nrm->h);
+        a.nd1 = static_cast<const uint16_t*>(nrm->d1);
+        a.nd2 = static_cast<const uint16_t*>(nrm->d2);
+        a.nw = static_cast<const uint16_t*>(nrm->w);
+        a.nh_out = static_cast<uint16_t*>(nrm->h_out);
+        a.neps = (float)nrm->eps;
+        a.norm = 1;
+    }
     a.x = x;
     a.x_dtype = x_dtype;
     a.x_stride = (int)x_stride;
@@ -411,4 +463,28 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     }
     if (rc) return rc;
     return esp_host::launch_check("dense");
+}
+
+extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                         const void* const* trellis, const void* const* suh, const void* const* svh,
+                         const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                         int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters,
+                         int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+                         int64_t rot_smem, void* stream) {
+    (void)PF;
+    ESP_REQUIRE(x, "dense: null x");
+    return dense_impl(x, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
+                      y_cols, xh, xh_numel, Z, z_numel, counters, counters_numel, k2, cb, SK, W, rot_smem, nullptr,
+                      stream);
+}
+
+extern "C" int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, const void* norm_w, double eps,
+                                 void* h_out, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                                 const void* const* trellis, const void* const* suh, const void* const* svh,
+                                 const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                                 int64_t y_cols, float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel,
+                                 int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t rot_smem, void* stream) {
+    const DenseNorm nrm{h, d1, d2, norm_w, h_out, eps};
+    return dense_impl(h, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
+                      y_cols, nullptr, 0, Z, z_numel, counters, counters_numel, k2, cb, SK, W, rot_smem, &nrm, stream);
 }

@@ -8,6 +8,7 @@
 #include "common.hpp"
 #include "trellis.hpp"
 #include "gemm.hpp"
+#include "norm.hpp"
 #include "../../../include/espalier.h"
 
 namespace esp {
@@ -177,6 +178,15 @@ struct RouteArgs {
     int* ucount;
     int* members;
     int x_stride, bf16, R, H, E, k, shared_id, maxm;
+    // esp_route_group_rmsnorm: x = RMSNorm(h + d1) * nw (norm.hpp), made in the launch into shared memory; workgroup 0
+    // stores it to na_out and the residual h + d1 to nh_out. Rows of h, d1, nh_out and na_out are x_stride apart.
+    const uint16_t* nh;
+    const uint16_t* nd1;
+    const uint16_t* nw;
+    uint16_t* nh_out;
+    uint16_t* na_out;
+    float neps;
+    int norm;
 };
 
 constexpr int RT = 1024;             // threads of a route workgroup
@@ -199,12 +209,45 @@ __device__ __forceinline__ float bf16_unorder(uint32_t k) {
 
 template <int BF16>
 __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
+    extern __shared__ __align__(16) unsigned char rsmem[];     // norm: the normalised rows [R][H]
     __shared__ int last;
     __shared__ int sh_pick[MAX_PICKS];
     __shared__ GroupSmemT<RT_MAX_IDS> g;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int has = a.shared_id >= 0, C = a.E + has, slots = a.k + has;
+    const uint16_t* xrows = a.x;
+    int xstride = a.x_stride;
+    if (a.norm) {
+        // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them
+        __shared__ float npart[16], ninv[4];
+        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, a.R, a.H, a.neps, BF16, npart, ninv);
+        uint16_t* xs = reinterpret_cast<uint16_t*>(rsmem);
+        const int r = tid >> 8, t = tid & 255;
+        if (r < a.R) {
+            const size_t o = (size_t)r * a.x_stride;
+#pragma unroll
+            for (int c = 0; c < NORM_CHUNKS; ++c) {
+                const int i = (c * 256 + t) * 8;
+                if (i < a.H) {
+                    float z[8], w8[8], o8[8];
+                    norm_z8(a.nh + o, a.nd1 ? a.nd1 + o : nullptr, nullptr, i, BF16, z);
+                    load8_16(a.nw + i, BF16, w8);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o8[j] = (z[j] * ninv[r]) * w8[j];
+                    const uint4 q = pack8_16(o8, BF16);
+                    *reinterpret_cast<uint4*>(xs + (size_t)r * a.H + i) = q;
+                    if (blockIdx.x == 0) {
+                        *reinterpret_cast<uint4*>(a.na_out + o + i) = q;
+                        *reinterpret_cast<uint4*>(a.nh_out + o + i) = pack8_16(z, BF16);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        xrows = xs;
+        xstride = a.H;
+    }
 
     // 1. logits: column c, rows rg, rg + 4, ...; h in groups of 2048 (4 chunks of 8 a lane). The gate's chunks stay
     // in registers across the rows and the next row's x is in flight while the current row is summed.
@@ -238,12 +281,12 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     load8(w, 512 * q + 8 * lane, gv[q]);
-                    load8(a.x + (size_t)rg * a.x_stride, 512 * q + 8 * lane, xv[q]);
+                    load8(xrows + (size_t)rg * xstride, 512 * q + 8 * lane, xv[q]);
                 }
                 for (int r = rg; r < a.R; r += 4) {
                     if (r + 4 < a.R) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) load8(a.x + (size_t)(r + 4) * a.x_stride, 512 * q + 8 * lane, xn[q]);
+                        for (int q = 0; q < 4; ++q) load8(xrows + (size_t)(r + 4) * xstride, 512 * q + 8 * lane, xn[q]);
                     }
                     const double s = wave_sum_f64_dpp(dot(xv, gv, 0.0));
                     if (lane == 0) store_dev(a.logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
@@ -260,7 +303,7 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             load8(w, h0 + 512 * q + 8 * lane, gv[q]);
-                            load8(a.x + (size_t)r * a.x_stride, h0 + 512 * q + 8 * lane, xv[q]);
+                            load8(xrows + (size_t)r * xstride, h0 + 512 * q + 8 * lane, xv[q]);
                         }
                         acc = dot(xv, gv, acc);
                     }
@@ -748,11 +791,19 @@ extern "C" int esp_group(const int32_t* pick, int32_t* uids, int64_t maxu, int32
     return esp_host::launch_check("group");
 }
 
-extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
-                               int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
-                               int64_t logits_numel, int32_t* counter, int32_t* pick_out, float* wts_out,
-                               int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm,
-                               void* stream) {
+struct RouteNorm {
+    const void* h;
+    const void* d1;
+    const void* w;
+    void* h_out;
+    void* a_out;
+    double eps;
+};
+
+static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
+                      const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
+                      int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu,
+                      int32_t* ucount, int32_t* members, int64_t maxm, const RouteNorm* nrm, void* stream) {
     const int has = shared_id >= 0;
     ESP_REQUIRE(x && gate && logits && counter && pick_out && wts_out && uids && ucount && members,
                 "route_group: null pointer");
@@ -787,12 +838,52 @@ extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int
     a.k = (int)k;
     a.shared_id = (int)shared_id;
     a.maxm = (int)maxm;
+    size_t smem = 0;
+    if (nrm) {
+        ESP_REQUIRE(nrm->h && nrm->w && nrm->h_out && nrm->a_out, "route_group_rmsnorm: null pointer");
+        ESP_REQUIRE(R <= RT / 256, "route_group_rmsnorm: at most 4 rows (four waves normalise a row)");
+        ESP_REQUIRE(H <= NORM_MAX_D && x_stride % 8 == 0 &&
+                        ((uintptr_t)nrm->h | (uintptr_t)nrm->d1 | (uintptr_t)nrm->w | (uintptr_t)nrm->h_out |
+                         (uintptr_t)nrm->a_out) % 16 == 0,
+                    "route_group_rmsnorm: H at most 8192, rows 16-byte aligned");
+        a.nh = static_cast<const uint16_t*>(nrm->h);
+        a.nd1 = static_cast<const uint16_t*>(nrm->d1);
+        a.nw = static_cast<const uint16_t*>(nrm->w);
+        a.nh_out = static_cast<uint16_t*>(nrm->h_out);
+        a.na_out = static_cast<uint16_t*>(nrm->a_out);
+        a.neps = (float)nrm->eps;
+        a.norm = 1;
+        smem = (size_t)R * H * 2;
+    }
     const unsigned grid = (unsigned)((E + has + RT_COLS - 1) / RT_COLS);
+    const void* fn = a.bf16 ? (const void*)route_group_kernel<1> : (const void*)route_group_kernel<0>;
+    if (smem > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "route_group: cannot raise the shared memory limit to %zu bytes", smem);
     if (a.bf16)
-        route_group_kernel<1><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+        route_group_kernel<1><<<grid, RT, smem, (hipStream_t)stream>>>(a);
     else
-        route_group_kernel<0><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+        route_group_kernel<0><<<grid, RT, smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("route_group");
+}
+
+extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
+                               int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
+                               int64_t logits_numel, int32_t* counter, int32_t* pick_out, float* wts_out,
+                               int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm,
+                               void* stream) {
+    return route_impl(x, x_dtype, x_stride, R, H, gate, E, sgate, k, shared_id, logits, logits_numel, counter,
+                      pick_out, wts_out, uids, maxu, ucount, members, maxm, nullptr, stream);
+}
+
+extern "C" int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, double eps, void* h_out,
+                                       void* a_out, int x_dtype, int64_t x_stride, int64_t R, int64_t H,
+                                       const void* gate, int64_t E, const void* sgate, int64_t k, int64_t shared_id,
+                                       float* logits, int64_t logits_numel, int32_t* counter, int32_t* pick_out,
+                                       float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount,
+                                       int32_t* members, int64_t maxm, void* stream) {
+    const RouteNorm nrm{h, d1, norm_w, h_out, a_out, eps};
+    return route_impl(h, x_dtype, x_stride, R, H, gate, E, sgate, k, shared_id, logits, logits_numel, counter,
+                      pick_out, wts_out, uids, maxu, ucount, members, maxm, &nrm, stream);
 }
 
 extern "C" int esp_group_shared(const int32_t* pick_in, const float* wts_in, const void* x, int x_dtype,

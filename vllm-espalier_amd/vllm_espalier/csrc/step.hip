@@ -7,45 +7,9 @@
 // row's result depends on that row alone.
 #include "../../../include/espalier.h"
 #include "common.hpp"
+#include "norm.hpp"
 
 namespace esp {
-
-// fp32 sum across a wave through DPP, in every lane (the fixed order of wave_sum_f64_dpp, no LDS)
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, v), 0u));
-}
-__device__ __forceinline__ float wave_sum_f32(float v) {
-    v += dpp_f32<0xB1>(v);
-    v += dpp_f32<0x4E>(v);
-    v += dpp_f32<0x141>(v);
-    v += dpp_f32<0x140>(v);
-    v += dpp_f32<0x142, 0xA>(v);
-    v += dpp_f32<0x143, 0xC>(v);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), 63));
-}
-
-// 8 consecutive 16-bit elements (bf16 or fp16) as fp32
-__device__ __forceinline__ void load8(const uint16_t* p, bool bf, float (&v)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
-        v[2 * i] = bf ? bf2f(lo) : h2f(lo);
-        v[2 * i + 1] = bf ? bf2f(hi) : h2f(hi);
-    }
-}
-
-__device__ __forceinline__ void store8(uint16_t* p, bool bf, const float (&v)[8]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = bf ? f2bf(v[2 * i]) : f2h(v[2 * i]), hi = bf ? f2bf(v[2 * i + 1]) : f2h(v[2 * i + 1]);
-        w[i] = lo | (hi << 16);
-    }
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
-}
 
 // ------------------------------------------------------------------------------------------------------------------
 // embed: h[t] = table[ids[t]] (ids outside [0, vocab) give a zero row). One workgroup a row, 16 bytes a lane.
@@ -63,68 +27,35 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// add_rmsnorm: z = h + d1 + d2 (fp32, each delta optional), h = z rounded to the model dtype, then
-// out = (h * (1 / sqrt(mean(h^2) + eps))) * w, with h read back as rounded, so the norm sees the residual stream as it
-// is stored. One workgroup of 256 a row; D a multiple of 8, at most 8 * 256 * ADD_RMS_CHUNKS.
+// add_rmsnorm: h = z (the residual, rounded), out = (z * inv) * w, in norm.hpp's order. One workgroup of 256 a row.
 // ------------------------------------------------------------------------------------------------------------------
-constexpr int ADD_RMS_CHUNKS = 4;
-
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(uint16_t* __restrict__ h, const uint16_t* __restrict__ d1,
                                                           const uint16_t* __restrict__ d2,
                                                           const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
                                                           int D, float eps, int bf) {
-    __shared__ float part[4];
-    const int t = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float z[ADD_RMS_CHUNKS][8], wv[ADD_RMS_CHUNKS][8];
-    float ss = 0.f;
+    __shared__ float part[4], inv_sh[1];
+    const int t = threadIdx.x;
+    const size_t o = (size_t)blockIdx.x * D;
+    const uint16_t* r1 = d1 ? d1 + o : nullptr;
+    const uint16_t* r2 = d2 ? d2 + o : nullptr;
+    float wv[NORM_CHUNKS][8];
 #pragma unroll
-    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {            // the weights first: in flight with the rows
-        const int i = (c * 256 + threadIdx.x) * 8;
-        if (i < D) load8(w + i, bf, wv[c]);
+    for (int c = 0; c < NORM_CHUNKS; ++c) {                 // the weights first: in flight with the rows
+        const int i = (c * 256 + t) * 8;
+        if (i < D) load8_16(w + i, bf, wv[c]);
     }
+    norm_rows_inv(h + o, r1, r2, D, 1, D, eps, bf, part, inv_sh);   // every read of h is done before h is written
+    const float inv = inv_sh[0];
 #pragma unroll
-    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
-        const int i = (c * 256 + threadIdx.x) * 8;
+    for (int c = 0; c < NORM_CHUNKS; ++c) {
+        const int i = (c * 256 + t) * 8;
         if (i < D) {
-            const size_t o = (size_t)t * D + i;
-            float a[8], b[8];
-            load8(h + o, bf, z[c]);
-            if (d1) {
-                load8(d1 + o, bf, a);
+            float z[8], o8[8];
+            norm_z8(h + o, r1, r2, i, bf, z);
+            if (d1 || d2) *reinterpret_cast<uint4*>(h + o + i) = pack8_16(z, bf);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) z[c][j] += a[j];
-            }
-            if (d2) {
-                load8(d2 + o, bf, b);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) z[c][j] += b[j];
-            }
-            if (d1 || d2) {
-                store8(h + o, bf, z[c]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {                 // the stored (rounded) residual
-                    const uint16_t r = bf ? f2bf(z[c][j]) : f2h(z[c][j]);
-                    z[c][j] = bf ? bf2f(r) : h2f(r);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ss += z[c][j] * z[c][j];
-        }
-    }
-    ss = wave_sum_f32(ss);
-    if (lane == 0) part[wave] = ss;
-    __syncthreads();
-    const float total = ((part[0] + part[1]) + part[2]) + part[3];
-    const float inv = 1.0f / sqrtf(total / (float)D + eps);
-#pragma unroll
-    for (int c = 0; c < ADD_RMS_CHUNKS; ++c) {
-        const int i = (c * 256 + threadIdx.x) * 8;
-        if (i < D) {
-            float o8[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o8[j] = (z[c][j] * inv) * wv[c][j];
-            store8(out + (size_t)t * D + i, bf, o8);
+            for (int j = 0; j < 8; ++j) o8[j] = (z[j] * inv) * wv[c][j];
+            *reinterpret_cast<uint4*>(out + o + i) = pack8_16(o8, bf);
         }
     }
 }
@@ -214,8 +145,8 @@ extern "C" int esp_add_rmsnorm(void* h, const void* d1, const void* d2, const vo
                                int64_t D, double eps, int dtype, void* stream) {
     ESP_REQUIRE(h && w && out, "add_rmsnorm: null pointer");
     ESP_REQUIRE(dtype == ESP_BF16 || dtype == ESP_F16, "add_rmsnorm: dtype must be bf16 or fp16");
-    ESP_REQUIRE(D > 0 && D % 8 == 0 && D <= 8 * 256 * ADD_RMS_CHUNKS,
-                "add_rmsnorm: D must be a positive multiple of 8, at most %d", 8 * 256 * ADD_RMS_CHUNKS);
+    ESP_REQUIRE(D > 0 && D % 8 == 0 && D <= NORM_MAX_D, "add_rmsnorm: D must be a positive multiple of 8, at most %d",
+                NORM_MAX_D);
     ESP_REQUIRE(((uintptr_t)h | (uintptr_t)d1 | (uintptr_t)d2 | (uintptr_t)w | (uintptr_t)out) % 16 == 0,
                 "add_rmsnorm: every tensor must be 16-byte aligned");
     if (T <= 0) return esp_host::ok();

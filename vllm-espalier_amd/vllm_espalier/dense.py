@@ -111,3 +111,23 @@ class Dense:
             ext().dense(x, [trellis[i] for i in idx], [suh[i] for i in idx], [svh[i] for i in idx],
                         [self.col0[i] for i in idx], y, xh, z, self.counters, k2, cb, sk, w, pf, ROT_SMEM)
         return y
+
+    def norm_fusable(self, M: int) -> bool:
+        """Whether forward_rmsnorm runs in one launch for M rows: one launch group, four waves a row, and the rotated
+        rows in the fused rotation's shared memory."""
+        if len(self.groups) != 1:
+            return False
+        sk, w, _ = self.plans[0]
+        steps = -(-(self.K // 32) // sk)
+        chunks = -(-(steps * 32 + 96) // 128)
+        return M <= w // 4 and self.K <= 8192 and M * chunks * 128 * 2 <= ROT_SMEM
+
+    def forward_rmsnorm(self, h, d1, d2, norm_w, eps: float, h_out, out):
+        """forward(RMSNorm(h + d1 + d2) * norm_w) with the residual h + d1 + d2 stored to h_out, the norm made inside
+        the launch (bit-identical to add_rmsnorm then forward). h, d1, d2: [M, K] contiguous, the model's dtype."""
+        z, _ = scratch(h.device, 0, 0)
+        (idx, k2, cb), (sk, w, pf) = self.groups[0], self.plans[0]
+        ext().dense_rmsnorm(h, d1, d2, norm_w, eps, h_out, [self.mats[i].trellis for i in idx],
+                            [self.mats[i].suh for i in idx], [self.mats[i].svh for i in idx],
+                            [self.col0[i] for i in idx], out, z, self.counters, k2, cb, sk, w, ROT_SMEM)
+        return out

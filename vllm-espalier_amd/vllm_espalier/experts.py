@@ -248,6 +248,16 @@ def route(x: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
                       s.wts[:R * s.slots], ids, s.count, members)
 
 
+def route_rmsnorm(h: torch.Tensor, d1: torch.Tensor | None, norm_w: torch.Tensor, eps: float, h_out: torch.Tensor,
+                  a_out: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
+    """route() of a_out = RMSNorm(h + d1) * norm_w, the norm made inside the routing launch (bit-identical to
+    add_rmsnorm then route); stores a_out and the residual h + d1 to h_out. At most 4 rows."""
+    R = h.shape[0]
+    ids, members = s.window(R)
+    ext().route_group_rmsnorm(h, d1, norm_w, eps, h_out, a_out, gate, L.gate_w, k, L.shared_id, s.logits,
+                              s.route_counter, s.pick[:R * s.slots], s.wts[:R * s.slots], ids, s.count, members)
+
+
 def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: Scratch,
             k: int | None = None, gate: torch.Tensor | None = None):
     """routed2 over windows of s.rows tokens (prefill), each window as in decode; with gate (and pick=None) route()

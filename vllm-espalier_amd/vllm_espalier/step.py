@@ -7,10 +7,14 @@ Per layer, on rows h (bf16 [T, 2048], the residual stream):
         attention is not part of this layer set: o reads q itself (qkv[:, :4096]) as a placeholder
   o   = o(q)                                              one dense launch (4096 -> 2048, int6)
   a   = RMSNorm(h + o)                                    add_rmsnorm
-  route_group, then the six grouped launches             256 routed experts (top-8) + the gated shared expert
+  route_group, then the grouped launches                  256 routed experts (top-8) + the gated shared expert
 then RMSNorm, the LM head (one dense launch, 2048 -> vocab, 6-bit mcg) and the argmax, which writes the next ids on
 the device. The shared expert of the dense block is the MoE's shared slot, counted once. Every op is a kernel of this
 package, nothing allocates after construction, so a HIP graph holds a whole step.
+
+For up to 4 rows (decode) each norm runs inside its consumer's launch instead (dense_rmsnorm for qkv and the head,
+route_group_rmsnorm for the router), with the same arithmetic in the same order, so the bits do not change: the qkv
+launch stores the residual to a second buffer, which the routing launch reads and adds o to, back into h.
 
 Rows never interact (the dense and grouped kernels keep rows apart, norms are per row), so a window of T rows
 gives each row the bits it gets alone.
@@ -32,6 +36,7 @@ EXPERT_I = 512
 VOCAB = 151936
 TOPK = 8
 EPS = 1e-6
+FUSE_NORMS = True            # the norms inside their consumers' launches for up to 4 rows (same bits)
 
 
 @dataclass
@@ -75,6 +80,7 @@ class Buffers:
         self.ids_in = torch.zeros((T,), dtype=torch.int32, device=dev)
         self.ids_out = torch.zeros((T,), dtype=torch.int32, device=dev)
         self.h = torch.zeros((T, D), dtype=bf, device=dev)
+        self.h2 = torch.zeros((T, D), dtype=bf, device=dev)      # the residual between the qkv and routing launches
         self.a = torch.zeros((T, D), dtype=bf, device=dev)
         self.qkv = torch.zeros((T, Q_OUT + 2 * KV_OUT), dtype=bf, device=dev)
         self.o = torch.zeros((T, D), dtype=bf, device=dev)
@@ -103,14 +109,23 @@ class SyntheticDecoder:
             self._bufs[T] = Buffers(T, self.vocab, self.dev)
         return self._bufs[T]
 
+    def fused_norms(self, T: int) -> bool:
+        return FUSE_NORMS and T <= 4 and self.layers[0].qkv.norm_fusable(T) and self.head.norm_fusable(T)
+
     def layer_forward(self, L: DecoderLayer, b: Buffers, first: bool, picks: list | None = None):
         e = ext()
         q = b.qkv[:, :Q_OUT]
-        e.add_rmsnorm(b.h, None if first else b.moe, None if first else b.moe_shared, L.norm1, b.a, EPS)
-        L.qkv.forward(b.a, out=b.qkv)
-        L.o.forward(q, out=b.o)
-        e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
-        G.route(b.a, L.router, TOPK, L.moe, self.scratch)
+        d1, d2 = (None, None) if first else (b.moe, b.moe_shared)
+        if self.fused_norms(b.T):
+            L.qkv.forward_rmsnorm(b.h, d1, d2, L.norm1, EPS, b.h2, out=b.qkv)
+            L.o.forward(q, out=b.o)
+            G.route_rmsnorm(b.h2, b.o, L.norm2, EPS, b.h, b.a, L.router, TOPK, L.moe, self.scratch)
+        else:
+            e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
+            L.qkv.forward(b.a, out=b.qkv)
+            L.o.forward(q, out=b.o)
+            e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
+            G.route(b.a, L.router, TOPK, L.moe, self.scratch)
         if picks is not None:                     # eager runs only: the distinct experts this layer reads
             n = int(self.scratch.count.item())
             picks.append(self.scratch.ids[:n].clone())
@@ -124,8 +139,11 @@ class SyntheticDecoder:
         for i, L in enumerate(self.layers):
             self.layer_forward(L, b, i == 0, picks)
         if head:
-            e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
-            self.head.forward(b.a, out=b.logits)
+            if self.fused_norms(T):
+                self.head.forward_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, EPS, b.h2, out=b.logits)
+            else:
+                e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
+                self.head.forward(b.a, out=b.logits)
             e.argmax(b.logits, b.ids_out)
         return b
 
