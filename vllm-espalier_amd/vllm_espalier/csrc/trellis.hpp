@@ -129,11 +129,8 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
         // even, saturating, keeping the sign; scaling by k = 4/3 (1 - 2^-16) in fp32 first puts every exact midpoint
         // just below (ties then go down) and moves nothing else across one (fp16 values near a midpoint are 2^-11 or
         // more apart, relative). Back to fp16 through the same instruction pair, then * 0.75 (exact).
-        const uint32_t m = mcg_pair(s0, s1);
         const float k = E2M1_K;
-        float y0, y1;
-        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(y0) : "v"(m), "v"(k));
-        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(y1) : "v"(m), "v"(k));
+        const float y0 = mul_mix(mcg_one(s0), k), y1 = mul_mix(mcg_one(s1), k);   // no packing of the two values
         uint32_t code = 0u, h;
         asm("v_cvt_scalef32_pk_fp4_f32 %0, %1, %2, %3" : "+v"(code) : "v"(y0), "v"(y1), "v"(1.0f));
         asm("v_cvt_scalef32_pk_f16_fp4 %0, %1, %2" : "=v"(h) : "v"(code), "v"(1.0f));
