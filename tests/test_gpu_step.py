@@ -154,7 +154,7 @@ def test_decoder_fused_norms_equal_separate(small_decoder, T, monkeypatch):
     res = {}
     for fused in (False, True):
         monkeypatch.setattr(S, "FUSE_NORMS", fused)
-        assert dec.fused_norms(T) == fused
+        assert dec.fused_norms(T) == fused and dec.fused_head_norm(T) == fused
         b = dec.buffers(T)
         b.ids_in.copy_(torch.tensor(ids, dtype=torch.int32))
         dec.forward(T)

@@ -110,7 +110,11 @@ class SyntheticDecoder:
         return self._bufs[T]
 
     def fused_norms(self, T: int) -> bool:
-        return FUSE_NORMS and T <= 4 and self.layers[0].qkv.norm_fusable(T) and self.head.norm_fusable(T)
+        """Whether the layers' norms run inside the qkv and routing launches for T rows."""
+        return FUSE_NORMS and T <= 4 and self.layers[0].qkv.norm_fusable(T)
+
+    def fused_head_norm(self, T: int) -> bool:
+        return FUSE_NORMS and self.head.norm_fusable(T)
 
     def layer_forward(self, L: DecoderLayer, b: Buffers, first: bool, picks: list | None = None):
         e = ext()
@@ -139,7 +143,7 @@ class SyntheticDecoder:
         for i, L in enumerate(self.layers):
             self.layer_forward(L, b, i == 0, picks)
         if head:
-            if self.fused_norms(T):
+            if self.fused_head_norm(T):
                 self.head.forward_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, EPS, b.h2, out=b.logits)
             else:
                 e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
