@@ -33,9 +33,9 @@ sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
 # HBM bytes a qkv launch moves at batch 1, from the two rocprofv3 --pmc passes over `bench.py --traffic-probe` (the
-# summary under profiles/): FETCH_SIZE 2762.4 KiB x 2.000 + WRITE_SIZE 498.8 KiB x 1.000, the factors being what the
+# summary under profiles/): FETCH_SIZE 2774.4 KiB x 2.000 + WRITE_SIZE 498.8 KiB x 1.000, the factors being what the
 # counters read for a 256 MiB copy. Re-measured whenever the dense kernel changes.
-QKV_TRAFFIC_BYTES = 6168115
+QKV_TRAFFIC_BYTES = 6192742
 COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
 
 
@@ -271,8 +271,9 @@ CALIB_BYTES = 256 << 20
 
 
 def traffic_probe(dev) -> None:
-    """Two replays of the roofline graph (98 cold qkv launches at batch 1, as in the bench) and two copies of
-    CALIB_BYTES, the plain copy kernel whose counters scale the qkv launch's (a copy reads and writes its size)."""
+    """Two replays of the roofline graph (98 cold qkv launches at batch 1, as in the bench), one of the same launches
+    at 32 rows, and two copies of CALIB_BYTES, the plain copy kernel whose counters scale the qkv launch's (a copy
+    reads and writes its size)."""
     import torch
     probe = dense_stack(1, 1, dev)
     copies = max(2, -(-COLD_BYTES // block_bytes(probe[0])))
@@ -281,12 +282,16 @@ def traffic_probe(dev) -> None:
     g = run_dense(stack, 1, dev, which=[0])
     for _ in range(2):
         g.replay()
+    del g
+    g = run_dense(stack, 32, dev, which=[0])          # the 32-row tiles (dense_kernel<23, 8, 2>), for MFMA use
+    g.replay()
+    del g
     src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(2):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"traffic probe: {copies} qkv launches x 2, copy of {CALIB_BYTES} B x 2")
+    log(f"traffic probe: {copies} qkv launches x 2 at 1 row, x 1 at 32 rows, copy of {CALIB_BYTES} B x 2")
 
 
 # ---------------------------------------------------------------------------------------------------------------
