@@ -88,3 +88,43 @@ def test_dequant_errors(lib):
     assert "multiples of 16" in lib.esp_last_error().decode()
     assert f(16, 16, 32, 32, 9, 7, None) == 2            # odd K2: no instance
     assert f(None, 16, 32, 32, 8, 7, None) == 1
+
+
+def _dense_rmsnorm(lib, **over):
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    f = lib.esp_dense_rmsnorm
+    f.restype = ctypes.c_int
+    f.argtypes = [P, P, P, P, ctypes.c_double, P, ctypes.c_int, I64, I64, I64, I64, ctypes.POINTER(P),
+                  ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(I64), ctypes.POINTER(I64), P, ctypes.c_int, I64,
+                  I64, P, I64, P, I64, I64, I64, I64, I64, I64, P]
+    a = dict(M=1, K=2048, W=16, SK=8, h=16, w=16, h_out=16, d1=None, x_dtype=1, rot_smem=64 * 1024)
+    a.update(over)
+    one = (P * 1)(16)
+    nc, c0 = (I64 * 1)(2048), (I64 * 1)(0)
+    rc = f(a["h"], a["d1"], None, a["w"], 1e-6, a["h_out"], a["x_dtype"], a["K"], a["M"], a["K"], 1, one, one, one, nc,
+           c0, 16, 1, 2048, 2048, 16, 1 << 30, 16, 1 << 20, 8, 7, a["SK"], a["W"], a["rot_smem"], None)
+    return rc, lib.esp_last_error().decode()
+
+
+@pytest.mark.parametrize("over,needle", [
+    (dict(M=5), "rows"), (dict(W=8, M=3), "rows"), (dict(h_out=None), "null"), (dict(x_dtype=2), "bf16"),
+    (dict(d1=8), "aligned"), (dict(rot_smem=0), "shared memory"),
+])
+def test_dense_rmsnorm_argument_errors(lib, over, needle):
+    """The fused-norm dense entry point refuses, before any HIP call, what its in-launch norm cannot do: more rows than
+    four waves each, unaligned rows, fp32 rows, rows that do not fit the fused rotation."""
+    rc, msg = _dense_rmsnorm(lib, **over)
+    assert rc == 1, msg
+    assert needle in msg
+
+
+def test_route_group_rmsnorm_argument_errors(lib):
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    f = lib.esp_route_group_rmsnorm
+    f.restype = ctypes.c_int
+    f.argtypes = [P, P, P, ctypes.c_double, P, P, ctypes.c_int, I64, I64, I64, P, I64, P, I64, I64, ctypes.c_void_p,
+                  I64, P, P, P, P, I64, P, P, I64, P]
+    args = lambda R, h_out: (16, None, 16, 1e-6, h_out, 16, 1, 2048, R, 2048, 16, 256, 16, 8, 256, 16, 1 << 20, 16,  # noqa
+                             16, 16, 16, 257, 16, 16, 32, None)
+    assert f(*args(5, 16)) == 1 and "4 rows" in lib.esp_last_error().decode()
+    assert f(*args(1, None)) == 1 and "null" in lib.esp_last_error().decode()
