@@ -182,6 +182,8 @@ uint16_t eo_decode(uint32_t s, int cb) {
         }
         case 22:
         case 23: return eo_f32_to_f16((float)eo_grid_q(s, cb));   /* :49-55 */
+        /* 19: not a reference codebook; the GEMMs' unscaled E2M1 form (the value / 0.75, exact), checked against it */
+        case 19: return eo_f32_to_f16(eo_f16_to_f32(eo_e2m1(s)) / 0.75f);
         default: return 0x7E00u;
     }
 }
@@ -226,7 +228,7 @@ void eo_position(int p, int* k, int* n) {
 static int dequant_any(const int16_t* trellis, int K, int N, int k2, int cb, uint16_t* out16, float* out32,
                        int threads) {
     /* 22 / 23 decode the int5 / int6 index q at the widths of 6 / 7 */
-    if (!eo_supported(cb >= 22 ? cb - 16 : cb, k2) || K % 16 || N % 16) return -1;
+    if (!eo_supported(cb >= 22 ? cb - 16 : cb == 19 ? 3 : cb, k2) || K % 16 || N % 16) return -1;
     const int KT = K / 16, NT = N / 16, TW = 4 * k2;
     int pos_k[256], pos_n[256];
     for (int p = 0; p < 256; ++p) eo_position(p, &pos_k[p], &pos_n[p]);

@@ -34,10 +34,10 @@ def test_dequant_bit_exact(dev, ext, cb, k2, K, N):
     assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} values differ"
 
 
-@pytest.mark.parametrize("cb,k2", [(22, 4), (22, 6), (22, 8), (23, 6), (23, 8), (23, 10)])
+@pytest.mark.parametrize("cb,k2", [(19, 2), (19, 4), (19, 6), (22, 4), (22, 6), (22, 8), (23, 6), (23, 8), (23, 10)])
 def test_dequant_grid_index_bit_exact(dev, ext, cb, k2):
-    """The dense kernels' int5 / int6 decode (the grid index q, scaled by c after the sums) against the oracle's q, over
-    a million random states (all 65536 but about 0.01 expected missing), the sign of a zero q aside."""
+    """The GEMMs' decode forms (E2M1 / 0.75, the int5 / int6 grid index q; the sums are scaled after) against the
+    oracle's, over a million random states (all 65536 but about 0.01 expected missing), the sign of a zero q aside."""
     print(f"dequant grid index cb={cb} k2={k2}", flush=True)
     gen = torch.Generator().manual_seed(2000 + cb * 32 + k2)
     t = torch.randint(-32768, 32768, (64, 64, 8 * k2), dtype=torch.int32, generator=gen).to(torch.int16)
@@ -45,7 +45,8 @@ def test_dequant_grid_index_bit_exact(dev, ext, cb, k2):
     out = torch.full((1024, 1024), float("nan"), dtype=torch.float16, device=dev)
     ext.dequant(t.to(dev), out, k2, cb)
     got = bits(out)
-    got[got == 0x8000] = 0                   # q = -0 (rintf of a small negative product) only ever enters sums
+    if cb != 19:
+        got[got == 0x8000] = 0               # q = -0 (rintf of a small negative product) only ever enters sums
     assert np.array_equal(got, want), f"{int((got != want).sum())} of {got.size} values differ"
 
 

@@ -132,6 +132,16 @@ def test_e2m1_nearest_grid_point(mcg):
     assert int(np.sum(t == 0x8000)) == 4331
 
 
+def test_e2m1_gemm_form_times_three_quarters(mcg):
+    """The GEMMs' E2M1 form (19) is the fp4 grid itself, {0, .5, 1, 1.5, 2, 3, 4, 6} with the sign (and -0), and 0.75
+    times it is the reference value exactly (the GEMM scales its fp32 sums by 0.75)."""
+    t3 = O.f16(O.codebook_table(3)).astype(np.float64)
+    t19 = O.f16(O.codebook_table(19)).astype(np.float64)
+    assert set(np.abs(t19).tolist()) <= {0, 0.5, 1, 1.5, 2, 3, 4, 6}
+    assert np.array_equal(t19 * 0.75, t3)
+    assert np.array_equal(np.signbit(t19), np.signbit(t3))
+
+
 @pytest.mark.parametrize("cb,top", [(6, 15), (7, 31)])
 def test_int_grid_by_division(mcg, cb, top):
     """q = rint(v * k) of the kernels equals rint(v / c) on every mcg value (the definition, experts_grouped.cuh:40-43)

@@ -28,7 +28,7 @@ struct Shard {
     const uint16_t* suh;     // [K]
     const uint16_t* svh;     // [N]
     int nb0, nb, col0;       // first 128-column block in the launch, blocks, first output column
-    float scale;             // grid step c when the int5 / int6 index is decoded, else 1
+    float scale;             // factor of the sums of the decoded form (gemm_scale: c, 0.75 or 1)
 };
 
 struct DenseArgs {
@@ -315,7 +315,8 @@ extern "C" int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N,
                            void* stream) {
     ESP_REQUIRE(trellis && out, "dequant: null pointer");
     ESP_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 16 == 0, "dequant: K and N must be positive multiples of 16");
-    if (!(supported((int)cb, (int)k2) || ((cb == 22 || cb == 23) && supported((int)cb - 16, (int)k2))))
+    if (!(supported((int)cb, (int)k2) || ((cb == 22 || cb == 23) && supported((int)cb - 16, (int)k2)) ||
+          (cb == 19 && supported(3, (int)k2))))
         return esp_host::fail(ESP_ERR_UNSUPPORTED, "no instance for codebook %lld K2 %lld", (long long)cb,
                               (long long)k2);
     hipStream_t s = (hipStream_t)stream;
@@ -377,7 +378,7 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
                               (long long)k2);
     DenseArgs a{};
     int nbt = 0;
-    const float c = (cb == 6 || cb == 7) ? grid_c((int)cb) : 1.0f;
+    const float c = gemm_scale((int)cb);
     for (int s = 0; s < n_shards; ++s) {
         const int64_t N = n_cols[s];
         ESP_REQUIRE(N > 0 && N % 128 == 0, "matrix shape");
@@ -453,7 +454,7 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
     switch (cb * 32 + k2) {
 #define ESP_DENSE_CASE(CB_, K2_)                                                                           \
     case CB_ * 32 + K2_: {                                                                                 \
-        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                       \
+        constexpr int KCB = gemm_cb(CB_);                                                                  \
         rc = mg == 1 ? launch_dense<KCB, K2_, 1>(a, grid, (int)W, smem, st)                                 \
                      : launch_dense<KCB, K2_, 2>(a, grid, (int)W, smem, st);                                \
         break;                                                                                             \

@@ -737,8 +737,8 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     switch (cb * 32 + k2) {
 #define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
     case CB_ * 32 + K2_: {                                                                                    \
-        constexpr int KCB = (CB_ == 6 || CB_ == 7) ? CB_ + 16 : CB_;                                          \
-        const float scale = (CB_ == 6 || CB_ == 7) ? grid_c(CB_) : 1.0f;                                      \
+        constexpr int KCB = gemm_cb(CB_);                                                                     \
+        const float scale = gemm_scale(CB_);                                                                  \
         if (two)                                                                                              \
             grouped_body<KCB, K2_, 2>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
                                       scale, stage, MODE == 1, MODE == 1);                                    \

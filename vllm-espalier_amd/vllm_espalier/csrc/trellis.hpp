@@ -36,6 +36,14 @@ constexpr float GRID_K6M = 0x1.f6628p+2f;
 constexpr float GRID_MAGIC = 1536.0f;                    // fp16 ulp 1 on [1024, 2048): the fraction is rounded off
 __host__ __device__ constexpr float grid_c(int cb) { return cb == 6 ? 3.94921875f / 15.0f : 3.94921875f / 31.0f; }
 
+// The form a GEMM decodes codebook cb in, and the factor its fp32 sums take afterwards: the int5 / int6 grids as their
+// index q (22 / 23, sums * c), E2M1 on its unscaled grid {0, .5, 1, 1.5, 2, 3, 4, 6} (19, sums * 0.75); mcg as it is.
+// Every product is exact either way (fp16 x fp16 in fp32); only the order of the roundings in the sums moves.
+__host__ __device__ constexpr int gemm_cb(int cb) { return cb == 6 || cb == 7 ? cb + 16 : cb == 3 ? 19 : cb; }
+__host__ __device__ constexpr float gemm_scale(int cb) {
+    return cb == 6 || cb == 7 ? grid_c(cb) : cb == 3 ? 0.75f : 1.0f;
+}
+
 // Per-lane constants of the MFMA B-operand decode for b = K2/2 bits: word indices (mod TW) and funnel shifts of the
 // two runs. The same for every tile of a matrix.
 template <int K2>
@@ -117,13 +125,13 @@ __device__ __forceinline__ float mul_mix(_Float16 v, float k) {
     return r;
 }
 
-// Codebook value pair. CB: 1 mcg; 3 E2M1 snap; 6 / 7 fp16(q * c) on the int5 / int6 grid; 22 / 23 the grid index q
-// itself (fp16, exact), whose sums the caller scales by c.
+// Codebook value pair. CB: 1 mcg; 3 E2M1 snap; 6 / 7 fp16(q * c) on the int5 / int6 grid; the GEMM forms (gemm_cb):
+// 19 the E2M1 snap / 0.75 and 22 / 23 the grid index q itself (fp16, exact), whose sums the caller scales.
 template <int CB>
 __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
     if constexpr (CB == 1) {
         return mcg_pair(s0, s1);
-    } else if constexpr (CB == 3) {
+    } else if constexpr (CB == 3 || CB == 19) {
         // E2M1 (experts_grouped.cuh:25-38): |v| snapped to 0.75 * {0, .5, 1, 1.5, 2, 3, 4, 6}, a tie going to the
         // smaller value, with v's sign (so -0 exists). gfx950's FP4 conversion rounds to that grid (x 4/3) to nearest
         // even, saturating, keeping the sign; scaling by k = 4/3 (1 - 2^-16) in fp32 first puts every exact midpoint
@@ -134,6 +142,7 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
         uint32_t code = 0u, h;
         asm("v_cvt_scalef32_pk_fp4_f32 %0, %1, %2, %3" : "+v"(code) : "v"(y0), "v"(y1), "v"(1.0f));
         asm("v_cvt_scalef32_pk_f16_fp4 %0, %1, %2" : "=v"(h) : "v"(code), "v"(1.0f));
+        if constexpr (CB == 19) return h;                  // the unscaled grid: the GEMM scales its sums by 0.75
         const f16x2 q = __builtin_bit_cast(f16x2, h) * f16x2{(_Float16)0.75f, (_Float16)0.75f};
         return __builtin_bit_cast(uint32_t, q);
     } else if constexpr (CB == 23) {
@@ -195,8 +204,8 @@ __host__ __device__ constexpr int slot_k(int G, int i) { return 4 * (G & 1) + (i
 #define ESP_CASES(X) \
     X(1, 2) X(1, 4) X(1, 6) X(1, 8) X(1, 10) X(1, 12) X(1, 14) X(1, 16) \
     X(3, 2) X(3, 4) X(3, 6) X(6, 4) X(6, 6) X(6, 8) X(7, 6) X(7, 8) X(7, 10)
-// The dense kernels' grid-index forms of the int5 / int6 pairs (dequantised only to test them)
-#define ESP_GRID_CASES(X) X(22, 4) X(22, 6) X(22, 8) X(23, 6) X(23, 8) X(23, 10)
+// The GEMMs' forms of the E2M1 / int5 / int6 pairs (gemm_cb; dequantised only to test them)
+#define ESP_GRID_CASES(X) X(19, 2) X(19, 4) X(19, 6) X(22, 4) X(22, 6) X(22, 8) X(23, 6) X(23, 8) X(23, 10)
 
 __host__ __device__ constexpr bool supported(int cb, int k2) {
     return (cb == 1 && k2 >= 2 && k2 <= 16 && k2 % 2 == 0) || (cb == 3 && (k2 == 2 || k2 == 4 || k2 == 6)) ||
