@@ -218,6 +218,23 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     const int has = a.shared_id >= 0, C = a.E + has, slots = a.k + has;
     const uint16_t* xrows = a.x;
     int xstride = a.x_stride;
+    // this wave's router column c, rows rg, rg + 4, ...; h in groups of 2048 (4 chunks of 8 a lane)
+    const int c = blockIdx.x * RT_COLS + (wave & 3), rg = wave >> 2;
+    const bool active = c < C && rg < a.R;
+    const uint16_t* w = c < a.E ? a.gate + (size_t)c * a.H : a.sgate;
+    auto load8 = [&](const uint16_t* p, int h, uint2 (&v)[2]) __attribute__((always_inline)) {
+        if (h < a.H) {
+            v[0] = *reinterpret_cast<const uint2*>(p + h);
+            v[1] = *reinterpret_cast<const uint2*>(p + h + 4);
+        } else {
+            v[0] = v[1] = make_uint2(0u, 0u);
+        }
+    };
+    uint2 gv[4][2];
+    if (active && a.H <= 2048) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) load8(w, 512 * q + 8 * lane, gv[q]);   // in flight while the rows are normalised
+    }
     if (a.norm) {
         // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them
         __shared__ float npart[16], ninv[4];
@@ -249,20 +266,10 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         xstride = a.H;
     }
 
-    // 1. logits: column c, rows rg, rg + 4, ...; h in groups of 2048 (4 chunks of 8 a lane). The gate's chunks stay
-    // in registers across the rows and the next row's x is in flight while the current row is summed.
+    // 1. logits. The gate's chunks stay in registers across the rows and the next row's x is in flight while the
+    // current row is summed.
     {
-        const int c = blockIdx.x * RT_COLS + (wave & 3), rg = wave >> 2;
-        if (c < C && rg < a.R) {
-            const uint16_t* w = c < a.E ? a.gate + (size_t)c * a.H : a.sgate;
-            auto load8 = [&](const uint16_t* p, int h, uint2 (&v)[2]) __attribute__((always_inline)) {
-                if (h < a.H) {
-                    v[0] = *reinterpret_cast<const uint2*>(p + h);
-                    v[1] = *reinterpret_cast<const uint2*>(p + h + 4);
-                } else {
-                    v[0] = v[1] = make_uint2(0u, 0u);
-                }
-            };
+        if (active) {
             auto dot = [&](const uint2 (&xv)[4][2], const uint2 (&gv)[4][2], double acc) __attribute__((always_inline)) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -276,13 +283,10 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
                 }
                 return acc;
             };
-            uint2 gv[4][2], xv[4][2], xn[4][2];
+            uint2 xv[4][2], xn[4][2];
             if (a.H <= 2048) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    load8(w, 512 * q + 8 * lane, gv[q]);
-                    load8(xrows + (size_t)rg * xstride, 512 * q + 8 * lane, xv[q]);
-                }
+                for (int q = 0; q < 4; ++q) load8(xrows + (size_t)rg * xstride, 512 * q + 8 * lane, xv[q]);
                 for (int r = rg; r < a.R; r += 4) {
                     if (r + 4 < a.R) {
 #pragma unroll
