@@ -191,25 +191,37 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     }
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
-    RowsA<MG> al;
+    RowsA<MG, true> al;       // fused: the rotated rows in shared memory
+    RowsA<MG, false> ag;      // else the rot launch's xh
     if (a.fused) {
         // the 128-blocks the K range touches (a split may start or end inside one)
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const int c0 = k0 >> 7, chunks = ((k0 + kr + 127) >> 7) - c0;
         if (a.norm) {
-            // every workgroup normalises the rows itself: the whole row's sum of squares, then its K range
+            // every workgroup normalises the rows itself: the whole row's sum of squares, with the z of its K range
+            // kept in xs (the rotation then turns it into its rotated input in place, one half-wave a 128-block);
+            // the norm and sign weights of a half-wave's first block are in flight with the rows
             __shared__ float npart[16], ninv[4];
             const bool bf = a.x_dtype == BF16;
-            norm_rows_inv(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv);
-            if (nbg == 0 && split == 0) norm_rows_store(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, bf, a.nh_out);
-            for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
+            int idx = wave * 2 + half;
+            uint2 wq = make_uint2(0u, 0u), su = make_uint2(0u, 0u);
+            auto weights = [&](int i) __attribute__((always_inline)) {
+                const int kb = (c0 + i % chunks) * 128 + 4 * l32;
+                wq = *reinterpret_cast<const uint2*>(a.nw + kb);
+                su = *reinterpret_cast<const uint2*>(S.suh + kb);
+            };
+            if (idx < M * chunks) weights(idx);
+            uint4 zq[NORM_CHUNKS];
+            norm_rows_inv(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv, zq, xs, a.xs_stride,
+                          c0 * 128, (c0 + chunks) * 128);
+            if (nbg == 0 && split == 0) norm_rows_store(zq, M, a.K, a.x_stride, a.nh_out);
+            while (idx < M * chunks) {
                 const int r = idx / chunks, ch = idx % chunks;
-                const int kb = (c0 + ch) * 128;
-                const size_t ro = (size_t)r * a.x_stride;
-                const RotIn in = norm_rot_load(a.nh + ro, a.nd1 ? a.nd1 + ro : nullptr, a.nd2 ? a.nd2 + ro : nullptr,
-                                               a.nw + kb, kb, ninv[r], bf, S.suh + kb, l32);
-                *reinterpret_cast<uint2*>(xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32) =
-                    rot128_apply(in, a.x_dtype, l32);
+                uint16_t* xp = xs + (size_t)r * a.xs_stride + ch * 128 + 4 * l32;
+                const RotIn in = norm_rot_in(*reinterpret_cast<const uint2*>(xp), wq, su, ninv[r], bf);
+                *reinterpret_cast<uint2*>(xp) = rot128_apply(in, a.x_dtype, l32);
+                idx += 2 * NW;
+                if (idx < M * chunks) weights(idx);
             }
         } else {
             for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
@@ -222,7 +234,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
             const int row = g * 16 + c;
-            al.row[g] = row < M ? xs + (size_t)row * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
+            al.set(g, row < M ? xs + (size_t)row * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
         }
         al.kbase = c0 * 128;
     } else {
@@ -230,14 +242,17 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
             const int row = g * 16 + c;
-            al.row[g] = row < M ? X + (size_t)row * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
+            ag.set(g, row < M ? X + (size_t)row * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
         }
-        al.kbase = 0;
+        ag.kbase = 0;
     }
 
     // 2. the K loop (its first wait is a workgroup barrier, after which the rotated rows are visible)
     f32x4 acc[2][MG];
-    block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, al, acc, true);
+    if (a.fused)
+        block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, al, acc, true);
+    else
+        block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, ag, acc, true);
 
     // 3. the block's [M][128] sums: every wave's partials in shared memory (the stages are no longer read), the KW
     // k slots added in order

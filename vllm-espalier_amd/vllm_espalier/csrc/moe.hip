@@ -236,27 +236,31 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         for (int q = 0; q < 4; ++q) load8(w, 512 * q + 8 * lane, gv[q]);   // in flight while the rows are normalised
     }
     if (a.norm) {
-        // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them
+        // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them. The norm
+        // weights of a thread's chunks are in flight with the rows.
         __shared__ float npart[16], ninv[4];
-        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, a.R, a.H, a.neps, BF16, npart, ninv);
-        uint16_t* xs = reinterpret_cast<uint16_t*>(rsmem);
         const int r = tid >> 8, t = tid & 255;
+        uint4 wq[NORM_CHUNKS];
+#pragma unroll
+        for (int c = 0; c < NORM_CHUNKS; ++c) {
+            const int i = (c * 256 + t) * 8;
+            wq[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (r < a.R && i < a.H) wq[c] = *reinterpret_cast<const uint4*>(a.nw + i);
+        }
+        uint4 zq[NORM_CHUNKS];
+        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, a.R, a.H, a.neps, BF16, npart, ninv, zq);
+        uint16_t* xs = reinterpret_cast<uint16_t*>(rsmem);
         if (r < a.R) {
             const size_t o = (size_t)r * a.x_stride;
 #pragma unroll
             for (int c = 0; c < NORM_CHUNKS; ++c) {
                 const int i = (c * 256 + t) * 8;
                 if (i < a.H) {
-                    float z[8], w8[8], o8[8];
-                    norm_z8(a.nh + o, a.nd1 ? a.nd1 + o : nullptr, nullptr, i, BF16, z);
-                    load8_16(a.nw + i, BF16, w8);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) o8[j] = (z[j] * ninv[r]) * w8[j];
-                    const uint4 q = pack8_16(o8, BF16);
+                    const uint4 q = norm_scale8(zq[c], wq[c], ninv[r], BF16);
                     *reinterpret_cast<uint4*>(xs + (size_t)r * a.H + i) = q;
                     if (blockIdx.x == 0) {
                         *reinterpret_cast<uint4*>(a.na_out + o + i) = q;
-                        *reinterpret_cast<uint4*>(a.nh_out + o + i) = pack8_16(z, BF16);
+                        *reinterpret_cast<uint4*>(a.nh_out + o + i) = zq[c];
                     }
                 }
             }
@@ -464,8 +468,9 @@ struct GroupedArgs {
 };
 
 // The GEMM of one program. A rows: member m's row is abase + (by_member ? m : its slot row) * astride, holding k from
-// kbase. dev: the partials go to Z with device-scope stores (another workgroup of the launch reads them).
-template <int CB, int K2, int MG>
+// kbase, in shared memory (LDS) or global memory. dev: the partials go to Z with device-scope stores (another
+// workgroup of the launch reads them).
+template <int CB, int K2, int MG, bool LDS>
 __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_t* __restrict__ T,
                                              const uint16_t* abase, int astride, int kbase, bool by_member,
                                              const int* rows_sh, int nrows, int mat, int split, float scale,
@@ -476,12 +481,12 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
     const int NTILES = a.N >> 4;
     const int nt0 = blockIdx.y * 8;
     const int kr = a.K / a.SK, k0 = split * kr;
-    RowsA<MG> al;
+    RowsA<MG, LDS> al;
 #pragma unroll
     for (int g = 0; g < MG; ++g) {
         const int m = g * 16 + c;
         const int p = rows_sh[m];
-        al.row[g] = p >= 0 ? abase + (size_t)(by_member ? m : p) * astride + 16 * (G >> 1) + 4 * (G & 1) : nullptr;
+        al.set(g, p >= 0 ? abase + (size_t)(by_member ? m : p) * astride + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
     }
     al.kbase = kbase;
     f32x4 acc[2][MG];
@@ -744,10 +749,10 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
         constexpr int KCB = gemm_cb(CB_);                                                                     \
         const float scale = gemm_scale(CB_);                                                                  \
         if (two)                                                                                              \
-            grouped_body<KCB, K2_, 2>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
+            grouped_body<KCB, K2_, 2, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
                                       scale, stage, MODE == 1, MODE == 1);                                    \
         else                                                                                                  \
-            grouped_body<KCB, K2_, 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
+            grouped_body<KCB, K2_, 1, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
                                       scale, stage, MODE == 1, MODE == 1);                                    \
         break;                                                                                                \
     }

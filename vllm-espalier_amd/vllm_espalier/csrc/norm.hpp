@@ -29,18 +29,6 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), 63));
 }
 
-// 8 consecutive 16-bit elements (bf16 or fp16) as fp32
-__device__ __forceinline__ void load8_16(const uint16_t* p, bool bf, float (&v)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
-        v[2 * i] = bf ? bf2f(lo) : h2f(lo);
-        v[2 * i + 1] = bf ? bf2f(hi) : h2f(hi);
-    }
-}
-
 __device__ __forceinline__ uint16_t to16(float v, bool bf) { return bf ? f2bf(v) : f2h(v); }
 __device__ __forceinline__ float from16(uint16_t b, bool bf) { return bf ? bf2f(b) : h2f(b); }
 
@@ -51,84 +39,56 @@ __device__ __forceinline__ uint4 pack8_16(const float (&v)[8], bool bf) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// z of the 8 elements at offset o (a multiple of 8) of a row
-__device__ __forceinline__ void norm_z8(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, size_t o, bool bf,
-                                        float (&z)[8]) {
-    load8_16(h + o, bf, z);
-    if (d1) {
-        float a[8];
-        load8_16(d1 + o, bf, a);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) z[j] += a[j];
-    }
-    if (d2) {
-        float b[8];
-        load8_16(d2 + o, bf, b);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) z[j] += b[j];
-    }
-    if (d1 || d2) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) z[j] = from16(to16(z[j], bf), bf);     // the stored (rounded) residual
-    }
-}
-
-// z of the 4 elements at offset o (a multiple of 4) of a row: the same arithmetic as norm_z8
-__device__ __forceinline__ void norm_z4(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, size_t o, bool bf,
-                                        float (&z)[4]) {
-    auto load4 = [&](const uint16_t* p, float (&v)[4]) {
-        const uint2 u = *reinterpret_cast<const uint2*>(p + o);
-        v[0] = from16((uint16_t)(u.x & 0xFFFFu), bf); v[1] = from16((uint16_t)(u.x >> 16), bf);
-        v[2] = from16((uint16_t)(u.y & 0xFFFFu), bf); v[3] = from16((uint16_t)(u.y >> 16), bf);
-    };
-    load4(h, z);
-    if (d1) {
-        float a[4];
-        load4(d1, a);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) z[j] += a[j];
-    }
-    if (d2) {
-        float b[4];
-        load4(d2, b);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) z[j] += b[j];
-    }
-    if (d1 || d2) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) z[j] = from16(to16(z[j], bf), bf);
-    }
-}
-
-// the rotation's input (RotIn, 16-bit raw) of lane32's 4 elements at row offset o + 4 * lane32, normalised:
-// (z * inv) * w in the model dtype; w holds the norm weights from the same column, suh the sign vector's
-__device__ __forceinline__ RotIn norm_rot_load(const uint16_t* h, const uint16_t* d1, const uint16_t* d2,
-                                               const uint16_t* w, size_t o, float inv, bool bf, const uint16_t* suh,
-                                               int lane32) {
-    float z[4];
-    norm_z4(h, d1, d2, o + 4 * lane32, bf, z);
-    const uint2 wu = *reinterpret_cast<const uint2*>(w + 4 * lane32);
-    const float wv[4] = {from16((uint16_t)(wu.x & 0xFFFFu), bf), from16((uint16_t)(wu.x >> 16), bf),
-                         from16((uint16_t)(wu.y & 0xFFFFu), bf), from16((uint16_t)(wu.y >> 16), bf)};
-    uint16_t q[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) q[j] = to16((z[j] * inv) * wv[j], bf);
-    RotIn r;
-    r.raw = make_uint4((uint32_t)q[0] | ((uint32_t)q[1] << 16), (uint32_t)q[2] | ((uint32_t)q[3] << 16), 0u, 0u);
-    r.su = *reinterpret_cast<const uint2*>(suh + 4 * lane32);
-    return r;
-}
-
-// thread t's share of the sum of squares of row (h, d1, d2)
-__device__ __forceinline__ float norm_partial(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int D,
-                                              bool bf, int t) {
-    float ss = 0.f;
+// Thread t's chunks of row (h, d1, d2) (elements (c * 256 + t) * 8 .. + 8, c < NORM_CHUNKS, those below D): z packed
+// in the model dtype (the stored residual, exact; h itself when no delta is added) and its share of the sum of squares.
+// Every load is issued before any is used, so the three operands cost one memory round trip.
+__device__ __forceinline__ float norm_z_rows(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int D, bool bf,
+                                             int t, uint4 (&zq)[NORM_CHUNKS]) {
+    const uint16_t* p1 = d1 ? d1 : h;             // a stand-in row keeps the loads free of the delta branches
+    const uint16_t* p2 = d2 ? d2 : h;
+    uint4 uh[NORM_CHUNKS], u1[NORM_CHUNKS], u2[NORM_CHUNKS];
 #pragma unroll
     for (int c = 0; c < NORM_CHUNKS; ++c) {
         const int i = (c * 256 + t) * 8;
+        uh[c] = u1[c] = u2[c] = make_uint4(0u, 0u, 0u, 0u);
         if (i < D) {
+            uh[c] = *reinterpret_cast<const uint4*>(h + i);
+            u1[c] = *reinterpret_cast<const uint4*>(p1 + i);
+            u2[c] = *reinterpret_cast<const uint4*>(p2 + i);
+        }
+    }
+    auto unpack = [bf](uint4 u, float (&v)[8]) __attribute__((always_inline)) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = from16((uint16_t)(w[k] & 0xFFFFu), bf);
+            v[2 * k + 1] = from16((uint16_t)(w[k] >> 16), bf);
+        }
+    };
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NORM_CHUNKS; ++c) {
+        zq[c] = uh[c];
+        if ((c * 256 + t) * 8 < D) {
             float z[8];
-            norm_z8(h, d1, d2, i, bf, z);
+            unpack(uh[c], z);
+            if (d1) {
+                float a[8];
+                unpack(u1[c], a);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] += a[j];
+            }
+            if (d2) {
+                float b[8];
+                unpack(u2[c], b);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] += b[j];
+            }
+            if (d1 || d2) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] = from16(to16(z[j], bf), bf);     // the stored (rounded) residual
+                zq[c] = pack8_16(z, bf);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += z[j] * z[j];
         }
@@ -142,36 +102,72 @@ __device__ __forceinline__ float norm_inv(const float* part4, int D, float eps) 
     return 1.0f / sqrtf(total / (float)D + eps);
 }
 
-// The residual rows of a workgroup's norm_rows_inv (waves 4r..4r+3 on row r < R) stored to out (the same stride)
-__device__ __forceinline__ void norm_rows_store(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int stride,
-                                                int R, int D, bool bf, uint16_t* out) {
-    const int r = (int)(threadIdx.x >> 8), t = threadIdx.x & 255;
-    if (r >= R) return;
-    const size_t o = (size_t)r * stride;
-#pragma unroll
-    for (int c = 0; c < NORM_CHUNKS; ++c) {
-        const int i = (c * 256 + t) * 8;
-        if (i < D) {
-            float z[8];
-            norm_z8(h + o, d1 ? d1 + o : nullptr, d2 ? d2 + o : nullptr, i, bf, z);
-            *reinterpret_cast<uint4*>(out + o + i) = pack8_16(z, bf);
-        }
-    }
-}
-
-// Rows r < R of a workgroup of at least 256 * R threads: waves 4r..4r+3 take row r. Every thread calls it; on return
-// inv_sh[r] holds row r's scale (two workgroup barriers inside). Row r of h / d1 / d2 starts at r * stride.
+// Rows r < R of a workgroup of at least 256 * R threads: waves 4r..4r+3 take row r (thread t = tid & 255). Every
+// thread calls it; on return inv_sh[r] holds row r's scale and zq thread t's chunks of row r's z (norm_z_rows). With
+// zs (shared memory), the z elements i in [lo, hi) of row r are also stored at zs[r * zs_stride + i - lo], visible to
+// the whole workgroup on return (lo and hi multiples of 8). Two workgroup barriers inside. Row r of h / d1 / d2
+// starts at r * stride.
 __device__ __forceinline__ void norm_rows_inv(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int stride,
-                                              int R, int D, float eps, bool bf, float* part_sh, float* inv_sh) {
+                                              int R, int D, float eps, bool bf, float* part_sh, float* inv_sh,
+                                              uint4 (&zq)[NORM_CHUNKS], uint16_t* zs = nullptr, int zs_stride = 0,
+                                              int lo = 0, int hi = 0) {
     const int wave = threadIdx.x >> 6, r = wave >> 2, t = threadIdx.x & 255;
     if (r < R) {
         const size_t o = (size_t)r * stride;
-        const float ss = wave_sum_f32(norm_partial(h + o, d1 ? d1 + o : nullptr, d2 ? d2 + o : nullptr, D, bf, t));
+        const float ss = wave_sum_f32(norm_z_rows(h + o, d1 ? d1 + o : nullptr, d2 ? d2 + o : nullptr, D, bf, t, zq));
         if ((threadIdx.x & 63) == 0) part_sh[wave] = ss;
+        if (zs) {
+#pragma unroll
+            for (int c = 0; c < NORM_CHUNKS; ++c) {
+                const int i = (c * 256 + t) * 8;
+                if (i < D && i >= lo && i < hi) *reinterpret_cast<uint4*>(zs + (size_t)r * zs_stride + (i - lo)) = zq[c];
+            }
+        }
     }
     __syncthreads();
     if ((int)threadIdx.x < R) inv_sh[threadIdx.x] = norm_inv(part_sh + 4 * threadIdx.x, D, eps);
     __syncthreads();
+}
+
+// thread t's chunks of its row (norm_rows_inv's zq) stored at row (o = r * stride) of out
+__device__ __forceinline__ void norm_rows_store(const uint4 (&zq)[NORM_CHUNKS], int R, int D, size_t stride,
+                                                uint16_t* out) {
+    const int r = (int)(threadIdx.x >> 8), t = threadIdx.x & 255;
+    if (r >= R) return;
+#pragma unroll
+    for (int c = 0; c < NORM_CHUNKS; ++c) {
+        const int i = (c * 256 + t) * 8;
+        if (i < D) *reinterpret_cast<uint4*>(out + (size_t)r * stride + i) = zq[c];
+    }
+}
+
+// (z * inv) * w of 8 packed elements, packed in the model dtype
+__device__ __forceinline__ uint4 norm_scale8(uint4 zq, uint4 wq, float inv, bool bf) {
+    const uint32_t zw[4] = {zq.x, zq.y, zq.z, zq.w}, ww[4] = {wq.x, wq.y, wq.z, wq.w};
+    float o8[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        o8[2 * k] = (from16((uint16_t)(zw[k] & 0xFFFFu), bf) * inv) * from16((uint16_t)(ww[k] & 0xFFFFu), bf);
+        o8[2 * k + 1] = (from16((uint16_t)(zw[k] >> 16), bf) * inv) * from16((uint16_t)(ww[k] >> 16), bf);
+    }
+    return pack8_16(o8, bf);
+}
+
+// the rotation's input (RotIn, 16-bit raw) of 4 elements from their z (packed), norm weights w and signs su:
+// (z * inv) * w in the model dtype
+__device__ __forceinline__ RotIn norm_rot_in(uint2 zq, uint2 wq, uint2 su, float inv, bool bf) {
+    const uint32_t zw[2] = {zq.x, zq.y}, ww[2] = {wq.x, wq.y};
+    uint32_t q[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint16_t lo = to16((from16((uint16_t)(zw[k] & 0xFFFFu), bf) * inv) * from16((uint16_t)(ww[k] & 0xFFFFu), bf), bf);
+        const uint16_t hi = to16((from16((uint16_t)(zw[k] >> 16), bf) * inv) * from16((uint16_t)(ww[k] >> 16), bf), bf);
+        q[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    RotIn r;
+    r.raw = make_uint4(q[0], q[1], 0u, 0u);
+    r.su = su;
+    return r;
 }
 
 }  // namespace esp

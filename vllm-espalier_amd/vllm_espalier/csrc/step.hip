@@ -36,26 +36,23 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(uint16_t* __restrict__
     __shared__ float part[4], inv_sh[1];
     const int t = threadIdx.x;
     const size_t o = (size_t)blockIdx.x * D;
-    const uint16_t* r1 = d1 ? d1 + o : nullptr;
-    const uint16_t* r2 = d2 ? d2 + o : nullptr;
-    float wv[NORM_CHUNKS][8];
+    uint4 wq[NORM_CHUNKS];
 #pragma unroll
     for (int c = 0; c < NORM_CHUNKS; ++c) {                 // the weights first: in flight with the rows
         const int i = (c * 256 + t) * 8;
-        if (i < D) load8_16(w + i, bf, wv[c]);
+        wq[c] = make_uint4(0u, 0u, 0u, 0u);
+        if (i < D) wq[c] = *reinterpret_cast<const uint4*>(w + i);
     }
-    norm_rows_inv(h + o, r1, r2, D, 1, D, eps, bf, part, inv_sh);   // every read of h is done before h is written
+    uint4 zq[NORM_CHUNKS];
+    // every read of h is done before h is written
+    norm_rows_inv(h + o, d1 ? d1 + o : nullptr, d2 ? d2 + o : nullptr, D, 1, D, eps, bf, part, inv_sh, zq);
     const float inv = inv_sh[0];
 #pragma unroll
     for (int c = 0; c < NORM_CHUNKS; ++c) {
         const int i = (c * 256 + t) * 8;
         if (i < D) {
-            float z[8], o8[8];
-            norm_z8(h + o, r1, r2, i, bf, z);
-            if (d1 || d2) *reinterpret_cast<uint4*>(h + o + i) = pack8_16(z, bf);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o8[j] = (z[j] * inv) * wv[c][j];
-            *reinterpret_cast<uint4*>(out + o + i) = pack8_16(o8, bf);
+            if (d1 || d2) *reinterpret_cast<uint4*>(h + o + i) = zq[c];
+            *reinterpret_cast<uint4*>(out + o + i) = norm_scale8(zq[c], wq[c], inv, bf);
         }
     }
 }
