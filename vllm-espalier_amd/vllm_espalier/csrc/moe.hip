@@ -539,6 +539,28 @@ __device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t 
     }
 }
 
+// sum_splits4 of two partial sets (gate at pg, up at pu) with all 2 * SK loads in flight at once (SK <= 8), each summed
+// in split order as sum_splits4 does
+template <bool DEV>
+__device__ __forceinline__ void sum_splits4x2(const float* __restrict__ pg, const float* __restrict__ pu, size_t stride,
+                                              int SK, float (&g)[4], float (&u)[4]) {
+    float4 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (i < SK) {
+            a[i] = DEV ? load_dev4(pg + (size_t)i * stride) : *reinterpret_cast<const float4*>(pg + (size_t)i * stride);
+            b[i] = DEV ? load_dev4(pu + (size_t)i * stride) : *reinterpret_cast<const float4*>(pu + (size_t)i * stride);
+        }
+    g[0] = a[0].x; g[1] = a[0].y; g[2] = a[0].z; g[3] = a[0].w;
+    u[0] = b[0].x; u[1] = b[0].y; u[2] = b[0].z; u[3] = b[0].w;
+#pragma unroll
+    for (int i = 1; i < 8; ++i)
+        if (i < SK) {
+            g[0] += a[i].x; g[1] += a[i].y; g[2] += a[i].z; g[3] += a[i].w;
+            u[0] += b[i].x; u[1] += b[i].y; u[2] += b[i].z; u[3] += b[i].w;
+        }
+}
+
 __device__ __forceinline__ void load4_f16(const uint16_t* p, float (&v)[4]) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);
     v[0] = h2f((uint16_t)(u.x & 0xFFFFu)); v[1] = h2f((uint16_t)(u.x >> 16));
@@ -548,15 +570,29 @@ __device__ __forceinline__ void load4_f16(const uint16_t* p, float (&v)[4]) {
 // gate/up epilogue of one (slot row, 4 columns a lane) unit from its summed splits: H, * svh / sqrt(128), SwiGLU
 // (act_mode 1: fp32; 0: with the reference's bf16 roundings; clamped to limit), * suh_d, H / sqrt(128)
 // (experts.cu:120-162). at = e * N + the lane's first column.
-__device__ __forceinline__ void gateup_unit(float (&gv)[4], float (&uv)[4], const uint16_t* __restrict__ svh_g,
-                                            const uint16_t* __restrict__ svh_u, const uint16_t* __restrict__ suh_d,
-                                            size_t at, float limit, int act_mode, int l32, float (&v)[4]) {
+// the three fp16 scale vectors gateup_unit reads, 4 columns a lane (raw bits)
+struct GateupScales {
+    uint2 g, u, d;
+};
+__device__ __forceinline__ GateupScales gateup_scales(const uint16_t* __restrict__ svh_g, const uint16_t* __restrict__ svh_u,
+                                                      const uint16_t* __restrict__ suh_d, size_t at) {
+    return GateupScales{*reinterpret_cast<const uint2*>(svh_g + at), *reinterpret_cast<const uint2*>(svh_u + at),
+                        *reinterpret_cast<const uint2*>(suh_d + at)};
+}
+
+__device__ __forceinline__ void unpack4_f16(uint2 u, float (&v)[4]) {
+    v[0] = h2f((uint16_t)(u.x & 0xFFFFu)); v[1] = h2f((uint16_t)(u.x >> 16));
+    v[2] = h2f((uint16_t)(u.y & 0xFFFFu)); v[3] = h2f((uint16_t)(u.y >> 16));
+}
+
+__device__ __forceinline__ void gateup_unit(float (&gv)[4], float (&uv)[4], const GateupScales& sc, float limit,
+                                            int act_mode, int l32, float (&v)[4]) {
     fwht128(gv, l32);
     fwht128(uv, l32);
     float sg[4], su[4], sd[4];
-    load4_f16(svh_g + at, sg);
-    load4_f16(svh_u + at, su);
-    load4_f16(suh_d + at, sd);
+    unpack4_f16(sc.g, sg);
+    unpack4_f16(sc.u, su);
+    unpack4_f16(sc.d, sd);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         float act;
@@ -595,7 +631,7 @@ __global__ __launch_bounds__(256) void gateup_epilogue_kernel(const float* __res
     const int e = pick[p];
     if (e < 0 || e >= E) return;
     float v[4];
-    gateup_unit(gv, uv, svh_g, svh_u, suh_d, (size_t)e * N + n, limit, act_mode, l32, v);
+    gateup_unit(gv, uv, gateup_scales(svh_g, svh_u, suh_d, (size_t)e * N + n), limit, act_mode, l32, v);
     store4(xd, F16, (size_t)p * N + n, v);
 }
 
@@ -640,6 +676,8 @@ __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, c
                                                   int slots, int n_routed, int r, int blk, float (*part)[128]) {
     const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5, nhw = (int)(blockDim.x >> 5);
     const int n0 = blk * 128;
+    __shared__ float wts_sh[32];
+    if ((int)threadIdx.x < slots) wts_sh[threadIdx.x] = wts[r * slots + threadIdx.x];   // in flight with the splits
     for (int k = hw; k < slots; k += nhw) {
         const int p = r * slots + k;
         const int n = n0 + 4 * l32;
@@ -666,12 +704,12 @@ __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, c
     const size_t at = (size_t)r * D + n0 + col;
     if (threadIdx.x < 128) {
         float acc = 0.f;
-        for (int q = 0; q < n_routed; ++q) acc = fmaf(wts[r * slots + q], part[q][col], acc);
+        for (int q = 0; q < n_routed; ++q) acc = fmaf(wts_sh[q], part[q][col], acc);
         if constexpr (OUT_DTYPE == F32) static_cast<float*>(out)[at] = acc;
         else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out)[at] = f2bf(acc);
         else static_cast<uint16_t*>(out)[at] = f2h(acc);
     } else if (threadIdx.x < 256 && out_shared != nullptr && n_routed < slots) {
-        const float v = wts[r * slots + n_routed] * part[n_routed][col];
+        const float v = wts_sh[n_routed] * part[n_routed][col];
         if constexpr (OUT_DTYPE == F32) static_cast<float*>(out_shared)[at] = v;
         else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out_shared)[at] = f2bf(v);
         else static_cast<uint16_t*>(out_shared)[at] = f2h(v);
@@ -725,9 +763,12 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     const int kr = a.K / a.SK, k0 = split * kr;
     const uint16_t* abase = mat ? a.X1 : a.X0;
     int astride = a.K, kbase = 0;
+    GateupScales sc{};
     if constexpr (MODE == 1) {
-        // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory
+        // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory; the
+        // epilogue's scales (the expert's, for this lane's 4 columns) ride along, for the workgroup that runs it
         issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), blockIdx.y * 8, stage);
+        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + blockIdx.y * 128 + 4 * l32);
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const uint16_t* suh = (mat ? a.suh1 : a.suh0) + (size_t)e * a.K;
         const int chunks = kr >> 7;
@@ -769,9 +810,14 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
         for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
             const int p = rows_sh[m];
             float gv[4], uv[4], v[4];
-            sum_splits4<true>(a.Z + (size_t)p * a.N + n, (size_t)a.P * a.N, a.SK, gv);
-            sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv);
-            gateup_unit(gv, uv, a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + n, a.limit, a.act_mode, l32, v);
+            if (a.SK <= 8) {
+                sum_splits4x2<true>(a.Z + (size_t)p * a.N + n, a.Z + ((size_t)a.SK * a.P + p) * a.N + n,
+                                    (size_t)a.P * a.N, a.SK, gv, uv);
+            } else {
+                sum_splits4<true>(a.Z + (size_t)p * a.N + n, (size_t)a.P * a.N, a.SK, gv);
+                sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv);
+            }
+            gateup_unit(gv, uv, sc, a.limit, a.act_mode, l32, v);
             store4(a.xd, F16, (size_t)p * a.N + n, v);
         }
         if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every program of the block arrived
