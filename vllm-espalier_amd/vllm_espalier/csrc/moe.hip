@@ -103,6 +103,36 @@ __device__ void group_block(const int* sh_pick, int n, int R, int slots, int nid
     }
 }
 
+// group_block's tables for n <= 64 picks, by one wave (lane i holds pick i) with no barriers: a pick's member rank is
+// the number of earlier picks (pick order) with its id -- what group_block gives whether or not an id repeats inside a
+// row -- and an id's place the number of smaller distinct ids. Every lane of the wave calls it.
+__device__ void group_wave(const int* sh_pick, int n, int slots, int nid, int maxm, int* __restrict__ uids,
+                           int* __restrict__ ucount, int* __restrict__ members) {
+    const int lane = threadIdx.x & 63;
+    const int e = lane < n ? sh_pick[lane] : -1;
+    const bool valid = e >= 0 && e < nid;
+    int rank = 0, cnt = 0;
+    for (int j = 0; j < n; ++j) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        const bool same = valid && ej == e;
+        rank += same && j < lane;
+        cnt += same;
+    }
+    const uint64_t first = __ballot(valid && rank == 0);
+    int place = 0;
+    for (int j = 0; j < n; ++j) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        place += ((first >> j) & 1u) && ej < e;
+    }
+    if (lane == 0) *ucount = __builtin_popcountll(first);
+    if (!valid) return;
+    if (rank == 0) {
+        uids[place] = e;
+        for (int m = cnt; m < maxm; ++m) members[place * maxm + m] = -1;
+    }
+    if (rank < maxm) members[place * maxm + rank] = (lane / slots) * 32 + (lane % slots);
+}
+
 __global__ __launch_bounds__(GT) void group_kernel(const int* __restrict__ pick, int* __restrict__ uids,
                                                    int* __restrict__ ucount, int* __restrict__ members, int R,
                                                    int slots, int E, int maxm) {
@@ -333,7 +363,8 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
             const int e = lane + 64 * q;
             key[q] = e < a.E ? (bf16_order(load_dev(lr + e)) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
         }
-        float mx = 0.f, psum = 0.f, p_mine = 0.f;
+        // the k maxima first (lane t keeps pick t), then their exponentials at once; the sum runs in pick order
+        float l_mine = 0.f;
         int e_mine = -1;
         for (int t = 0; t < a.k; ++t) {
             uint32_t m = key[0] > key[1] ? key[0] : key[1];
@@ -341,18 +372,19 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
             m = m > m2 ? m : m2;
             m = wave_max_u32(m);
             const int e = (int)(0xFFFFu - (m & 0xFFFFu));
-            const float l = bf16_unorder(m >> 16);
-            if (t == 0) mx = l;
-            const float p = expf(l - mx);
-            psum += p;
             if (lane == t) {
                 e_mine = e;
-                p_mine = p;
+                l_mine = bf16_unorder(m >> 16);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 if (lane + 64 * q == e) key[q] = 0u;
         }
+        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_mine), 0));   // pick 0's
+        const float p_mine = expf(l_mine - mx);
+        float psum = 0.f;
+        for (int t = 0; t < a.k; ++t)
+            psum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_mine), t));
         if (lane < a.k) {
             a.pick_out[r * slots + lane] = e_mine;
             a.wts_out[r * slots + lane] = p_mine / psum;
@@ -366,8 +398,12 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     }
     __syncthreads();
 
-    // 3. grouping of the picks (ids < E + has)
-    group_block(sh_pick, a.R * slots, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    // 3. grouping of the picks (ids < E + has): one wave when they fit in it
+    if (a.R * slots <= 64) {
+        if (wave == 0) group_wave(sh_pick, a.R * slots, slots, C, a.maxm, a.uids, a.ucount, a.members);
+    } else {
+        group_block(sh_pick, a.R * slots, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    }
     if (tid == 0) store_dev(a.counter, 0);
 }
 
