@@ -176,8 +176,12 @@ int esp_add_rmsnorm(void* h, const void* d1, const void* d2, const void* w, void
                     double eps, int dtype, void* stream);
 
 /* ids[t] = argmax of logits row t (rows of `stride` elements, N used), the lowest index among equal maxima, a NaN
- * counting as the largest (torch.argmax). dtype ESP_BF16 or ESP_F16; rows 16-byte aligned. */
-int esp_argmax(const void* logits, int64_t stride, int64_t T, int64_t N, int dtype, int32_t* ids, void* stream);
+ * counting as the largest (torch.argmax). dtype ESP_BF16 or ESP_F16; rows 16-byte aligned. With scratch (part: at
+ * least T * ceil(N / 4096) int64 keys; counters: T * 32 int32, zero on entry and left zero) a row is split over
+ * workgroups of 4096 elements and the last to arrive reduces their keys; without (both NULL), one workgroup a row.
+ * The same ids either way. */
+int esp_argmax(const void* logits, int64_t stride, int64_t T, int64_t N, int dtype, int32_t* ids, int64_t* part,
+               int64_t part_numel, int32_t* counters, int64_t counters_numel, void* stream);
 
 #ifdef __cplusplus
 }

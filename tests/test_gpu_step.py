@@ -60,33 +60,67 @@ def test_add_rmsnorm(dev, ext, dtype, deltas):
     assert u.max() <= 1 and (u == 0).mean() > 0.99, (u.max(), (u == 0).mean())
 
 
+def _argmax_scratch(dev, T, N):
+    """esp_argmax's split scratch: ceil(N / 4096) keys and one 32-int counter line a row."""
+    return (torch.zeros((T * -(-N // 4096),), dtype=torch.int64, device=dev),
+            torch.zeros((T * 32,), dtype=torch.int32, device=dev))
+
+
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_argmax_ties_nan_and_tail(dev, ext, dtype):
+def test_argmax_ties_nan_and_tail(dev, ext, dtype, split):
     gen = torch.Generator().manual_seed(3)
     N = 151936
     x = torch.randn((4, N), generator=gen).to(dtype)
     x[1, 70000] = 40.0
-    x[1, 9] = 40.0                                   # a tie: the lower index wins
+    x[1, 9] = 40.0                                   # a tie across slices: the lower index wins
     x[2, 123456] = float("nan")                       # NaN counts as the largest
     x[3, N - 1] = 50.0                                 # the last element
     ids = torch.empty((4,), dtype=torch.int32, device=dev)
-    ext.argmax(x.to(dev), ids)
-    got = ids.cpu().tolist()
-    assert got[0] == int(torch.argmax(x[0].float()))
-    assert got[1:] == [9, 123456, N - 1]
+    scratch = _argmax_scratch(dev, 4, N) if split else (None, None)
+    for _ in range(2):                                # twice: the counters are left zero for the next call
+        ids.fill_(-1)
+        ext.argmax(x.to(dev), ids, *scratch)
+        got = ids.cpu().tolist()
+        assert got[0] == int(torch.argmax(x[0].float()))
+        assert got[1:] == [9, 123456, N - 1]
+    if split:
+        assert int(scratch[1].abs().sum()) == 0
     # an odd width and a strided view (rows of a wider buffer)
     y = torch.randn((3, 1000), generator=gen).to(dtype)
     yg = torch.zeros((3, 1008), dtype=dtype, device=dev)
     yg[:, :1000] = y.to(dev)
     yg[:, 1000:] = 100.0                              # outside N: never read
     ids3 = torch.empty((3,), dtype=torch.int32, device=dev)
-    ext.argmax(yg[:, :999], ids3)
+    ext.argmax(yg[:, :999], ids3, *(_argmax_scratch(dev, 3, 999) if split else (None, None)))
     assert ids3.cpu().tolist() == torch.argmax(y[:, :999].float(), dim=1).tolist()
+
+
+@pytest.mark.parametrize("N", [4097, 8195, 12288, 40003])
+def test_argmax_split_slices(dev, ext, N):
+    """Slice edges: the maximum in the first, the last, a partial last group, and equal maxima in two slices."""
+    gen = torch.Generator().manual_seed(N)
+    W = (N + 7) // 8 * 8
+    x = torch.randn((5, W), generator=gen).to(torch.bfloat16)
+    x[0, 0] = 30.0
+    x[1, N - 1] = 30.0
+    x[2, 4096] = 30.0
+    x[3, 4095] = 30.0
+    x[3, N - 2] = 30.0
+    x[4, :] = -1.0                                    # all equal: index 0
+    xd = x.to(dev)
+    ids = torch.empty((5,), dtype=torch.int32, device=dev)
+    part, cnt = _argmax_scratch(dev, 5, N)
+    ext.argmax(xd[:, :N], ids, part, cnt)
+    want = torch.argmax(x[:, :N].float(), dim=1).to(torch.int32)
+    assert torch.equal(ids.cpu(), want)
+    assert ids.cpu().tolist()[:5] == [0, N - 1, 4096, 4095, 0]
+    assert int(cnt.abs().sum()) == 0
 
 
 @pytest.fixture(scope="module")
 def small_decoder(dev):
-    return S.SyntheticDecoder(n_layers=2, seed=9, device=dev, E=16, vocab=4096)
+    return S.SyntheticDecoder(n_layers=2, seed=9, device=dev, E=16, vocab=5120)   # two argmax slices
 
 
 def _run(dec, ids):

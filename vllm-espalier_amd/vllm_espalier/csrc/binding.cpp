@@ -427,14 +427,22 @@ void add_rmsnorm(at::Tensor h, const c10::optional<at::Tensor>& d1, const c10::o
                          h.size(1), eps, dtype_code(h), cur_stream()));
 }
 
-void argmax(const at::Tensor& logits, at::Tensor ids) {
+void argmax(const at::Tensor& logits, at::Tensor ids, std::optional<at::Tensor> part,
+            std::optional<at::Tensor> counters) {
     TORCH_CHECK(logits.is_cuda() && logits.dim() == 2 && logits.stride(1) == 1, "logits: [T, N], unit column stride");
     TORCH_CHECK(logits.scalar_type() == at::kBFloat16 || logits.scalar_type() == at::kHalf, "logits: bf16 or fp16");
     check(ids, at::kInt, "ids");
     TORCH_CHECK(ids.numel() == logits.size(0), "ids: [T]");
+    TORCH_CHECK(part.has_value() == counters.has_value(), "argmax: part and counters go together");
+    if (part.has_value()) {
+        check(*part, at::kLong, "part");
+        check(*counters, at::kInt, "counters");
+    }
     c10::hip::HIPGuardMasqueradingAsCUDA guard(logits.device());
     call(esp_argmax(logits.data_ptr(), logits.stride(0), logits.size(0), logits.size(1), dtype_code(logits),
-                    mptr<int32_t>(ids), cur_stream()));
+                    mptr<int32_t>(ids), part.has_value() ? mptr<int64_t>(*part) : nullptr,
+                    part.has_value() ? part->numel() : 0, counters.has_value() ? mptr<int32_t>(*counters) : nullptr,
+                    counters.has_value() ? counters->numel() : 0, cur_stream()));
 }
 
 PYBIND11_MODULE(espalier_ext, m) {
@@ -456,5 +464,6 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("route_group_rmsnorm", &route_group_rmsnorm);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);
-    m.def("argmax", &argmax);
+    m.def("argmax", &argmax, py::arg("logits"), py::arg("ids"), py::arg("part") = py::none(),
+          py::arg("counters") = py::none());
 }

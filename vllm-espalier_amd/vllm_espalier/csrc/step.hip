@@ -120,6 +120,67 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
     }
 }
 
+// The maximum key of a workgroup of 256 threads (4 waves), in thread 0
+__device__ __forceinline__ uint64_t block_max_key256(uint64_t best, uint64_t* sh) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m), hi = (uint32_t)__shfl_xor((int)(best >> 32), m);
+        best = umax64(best, ((uint64_t)hi << 32) | lo);
+    }
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = best;
+    __syncthreads();
+    return umax64(umax64(sh[0], sh[1]), umax64(sh[2], sh[3]));
+}
+
+// argmax over many workgroups: workgroup (b, t) takes slice b of row t (SL elements, a multiple of 8, at most 4096:
+// two 16-byte loads a thread, both in flight), its largest key goes to part[t * NB + b], and the last of the NB to
+// arrive on counter t takes the largest of the NB keys. The keys are argmax_kernel's, so the result is the same.
+constexpr int ARGMAX_SLICE = 4096;
+constexpr int ARGMAX_MAX_SLICES = 1024;
+
+__global__ __launch_bounds__(256) void argmax_split_kernel(const uint16_t* __restrict__ logits, int64_t stride, int N,
+                                                           int SL, int bf, unsigned long long* __restrict__ part,
+                                                           int* __restrict__ counters, int32_t* __restrict__ ids) {
+    __shared__ uint64_t sh[4];
+    __shared__ int last;
+    const int b = blockIdx.x, t = blockIdx.y, NB = gridDim.x, tid = threadIdx.x;
+    const uint16_t* row = logits + (size_t)t * stride;
+    const int s0 = b * SL, s1 = max(s0, min(N, s0 + SL));  // a slice past N is empty
+    const int nv = s0 + ((s1 - s0) & ~7);                  // the slice's whole 8-element groups end here
+    uint64_t best = 0;
+    uint4 u[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = s0 + 8 * (tid + 256 * j);
+        if (i < nv) u[j] = *reinterpret_cast<const uint4*>(row + i);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = s0 + 8 * (tid + 256 * j);
+        if (i < nv) {
+            const uint32_t w[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                best = umax64(best, key_of((uint16_t)(w[q] & 0xFFFFu), bf, i + 2 * q));
+                best = umax64(best, key_of((uint16_t)(w[q] >> 16), bf, i + 2 * q + 1));
+            }
+        }
+    }
+    for (int i = nv + tid; i < s1; i += 256) best = umax64(best, key_of(row[i], bf, i));
+    best = block_max_key256(best, sh);
+    if (tid == 0) store_dev(part + (size_t)t * NB + b, (unsigned long long)best);
+    int* cnt = counters + (size_t)t * CNT_STRIDE;
+    if (!arrive_last(cnt, NB, &last)) return;
+    __syncthreads();                                        // sh is reused below
+    uint64_t k = 0;
+    for (int q = tid; q < NB; q += 256) k = umax64(k, load_dev(part + (size_t)t * NB + q));
+    k = block_max_key256(k, sh);
+    if (tid == 0) {
+        ids[t] = (int32_t)~(uint32_t)k;
+        store_dev(cnt, 0);                                  // every slice of the row arrived
+    }
+}
+
 }  // namespace esp
 
 // ======================================================================================================================
@@ -154,12 +215,23 @@ extern "C" int esp_add_rmsnorm(void* h, const void* d1, const void* d2, const vo
 }
 
 extern "C" int esp_argmax(const void* logits, int64_t stride, int64_t T, int64_t N, int dtype, int32_t* ids,
-                          void* stream) {
+                          int64_t* part, int64_t part_numel, int32_t* counters, int64_t counters_numel, void* stream) {
     ESP_REQUIRE(logits && ids, "argmax: null pointer");
     ESP_REQUIRE(dtype == ESP_BF16 || dtype == ESP_F16, "argmax: dtype must be bf16 or fp16");
     ESP_REQUIRE(N > 0 && N < (1ll << 31) && stride >= N, "argmax: need 0 < N < 2^31 and stride >= N");
     ESP_REQUIRE((uintptr_t)logits % 16 == 0 && stride % 8 == 0, "argmax: rows must be 16-byte aligned");
+    ESP_REQUIRE((part == nullptr) == (counters == nullptr), "argmax: part and counters go together");
     if (T <= 0) return esp_host::ok();
+    const int64_t nb = (N + ARGMAX_SLICE - 1) / ARGMAX_SLICE;
+    if (part && nb > 1 && nb <= ARGMAX_MAX_SLICES && T <= 65535) {
+        ESP_REQUIRE(part_numel >= T * nb, "argmax: part needs ceil(N / %d) keys a row", ARGMAX_SLICE);
+        ESP_REQUIRE(counters_numel >= T * CNT_STRIDE, "argmax: counters need %d ints a row", CNT_STRIDE);
+        const int64_t sl = ((N + nb - 1) / nb + 7) / 8 * 8;   // <= ARGMAX_SLICE, a multiple of 8
+        argmax_split_kernel<<<dim3((unsigned)nb, (unsigned)T), 256, 0, (hipStream_t)stream>>>(
+            static_cast<const uint16_t*>(logits), stride, (int)N, (int)sl, dtype == ESP_BF16,
+            reinterpret_cast<unsigned long long*>(part), counters, ids);
+        return esp_host::launch_check("argmax");
+    }
     argmax_kernel<<<(unsigned)T, 1024, 0, (hipStream_t)stream>>>(static_cast<const uint16_t*>(logits), stride,
                                                                   (int)N, dtype == ESP_BF16, ids);
     return esp_host::launch_check("argmax");

@@ -87,6 +87,8 @@ class Buffers:
         self.moe = torch.zeros((T, D), dtype=bf, device=dev)
         self.moe_shared = torch.zeros((T, D), dtype=bf, device=dev)
         self.logits = torch.zeros((T, vocab), dtype=bf, device=dev)
+        self.argmax_part = torch.zeros((T * -(-vocab // 4096),), dtype=torch.int64, device=dev)   # a key a slice
+        self.argmax_cnt = torch.zeros((T * 32,), dtype=torch.int32, device=dev)                   # zero between uses
 
 
 class SyntheticDecoder:
@@ -148,7 +150,7 @@ class SyntheticDecoder:
             else:
                 e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
                 self.head.forward(b.a, out=b.logits)
-            e.argmax(b.logits, b.ids_out)
+            e.argmax(b.logits, b.ids_out, b.argmax_part, b.argmax_cnt)
         return b
 
     def algorithmic_bytes(self, picks: list[torch.Tensor], tokens: int, head: bool = True) -> int:
