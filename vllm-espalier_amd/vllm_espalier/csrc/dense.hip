@@ -43,6 +43,7 @@ struct DenseArgs {
     int* counters;
     int M, K, SK, NBT, fused, xs_stride, stage_bytes;
     int SQ, SR;              // K / 32 steps = SQ * SK + SR: split s has SQ + (s < SR) steps
+    int gather;              // the last workgroup loads the M * SK partials one a 32-lane half (shared memory holds them)
     // esp_dense_rmsnorm: the input rows are RMSNorm(h + d1 + d2) * nw (norm.hpp), made in the launch; workgroup (0, 0)
     // stores the residual h + d1 + d2 to nh_out. Rows of h, d1, d2 and nh_out are x_stride apart.
     const uint16_t* nh;
@@ -285,6 +286,29 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         store_dev4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
     if (!arrive_last(a.counters + (size_t)nbg * CNT_STRIDE, a.SK, &last)) return;
     const size_t zsplit = (size_t)M * zrow;
+    if (a.gather) {
+        // every (row, split) partial in flight at once, one a 32-lane half, through shared memory (the k slots'
+        // partials there are no longer read); then each row's splits added in split order
+        float4* zs = reinterpret_cast<float4*>(smem);
+        const int idx = wave * 2 + half;
+        if (idx < M * a.SK) {
+            const int r = idx / a.SK, q = idx - r * a.SK;
+            zs[idx * 32 + l32] = load_dev4(a.Z + (size_t)q * zsplit + (size_t)r * zrow + nbg * 128 + 4 * l32);
+        }
+        __syncthreads();
+        for (int r = wave * 2 + half; r < M; r += 2 * NW) {
+            float4 s = zs[(r * a.SK) * 32 + l32];
+            for (int q = 1; q < a.SK; ++q) {
+                const float4 u = zs[(r * a.SK + q) * 32 + l32];
+                s.x += u.x; s.y += u.y; s.z += u.z; s.w += u.w;
+            }
+            float v[4] = {s.x, s.y, s.z, s.w};
+            finish(v, l32, sv, S.scale);
+            store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
+        }
+        if (threadIdx.x == 0) store_dev(a.counters + (size_t)nbg * CNT_STRIDE, 0);
+        return;
+    }
     for (int r = wave * 2 + half; r < M; r += 2 * NW) {
         const float* zp = a.Z + (size_t)r * zrow + nbg * 128 + 4 * l32;
         float4 s;
@@ -463,6 +487,8 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
     const size_t smem_red = (size_t)(W / 4) * M * 128 * 4;
     const size_t smem = smem_x > smem_red ? smem_x : smem_red;
     ESP_REQUIRE(smem <= 160 * 1024, "dense: shared memory for the fused rotation exceeds 160 KiB");
+    // more splits than one batch of loads: spread them over the last workgroup's 32-lane halves when they all fit
+    a.gather = SK > 8 && M * SK <= 2 * W && (size_t)M * SK * 32 * 16 <= smem;
     dim3 grid((unsigned)nbt, (unsigned)SK);
     const int mg = M > 16 ? 2 : 1;
     int rc = ESP_OK;
