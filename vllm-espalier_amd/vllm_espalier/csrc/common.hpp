@@ -63,27 +63,18 @@ __device__ __forceinline__ void store4(void* p, int dtype, size_t i, const float
     }
 }
 
-// lane ^ M inside each 32-lane half of the wave, all in VALU (no LDS round trips): quad DPP for 1 and 2; for 4,
-// quad_perm [3,2,1,0] (lane ^ 3) then row_half_mirror (lane ^ 7 inside 8); for 8, row_ror:8 inside a 16-lane row; for
-// 16, v_permlane16_swap, which trades odd and even 16-lane rows of its two operands (the first result holds the even
-// rows in the odd ones, the second the odd rows in the even ones).
+// lane ^ M inside each 32-lane half of the wave: quad DPP for 1 and 2, ds_swizzle's bitmask mode above. (An all-VALU
+// form -- quad_perm + row_half_mirror for 4, row_ror:8, v_permlane16_swap for 16 -- was measured on MI355X: no faster
+// where a rotation is latency-bound, 1.3 % slower on 32-row dense blocks, where the extra VALU work competes.)
 template <int M>
 __device__ __forceinline__ float xor_lane32(float v) {
     int i = __builtin_bit_cast(int, v);
-    if constexpr (M == 1) {
+    if constexpr (M == 1)
         i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);     // quad_perm [1,0,3,2]
-    } else if constexpr (M == 2) {
+    else if constexpr (M == 2)
         i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);     // quad_perm [2,3,0,1]
-    } else if constexpr (M == 4) {
-        i = __builtin_amdgcn_update_dpp(0, i, 0x1B, 0xF, 0xF, false);     // quad_perm [3,2,1,0]
-        i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);    // row_half_mirror
-    } else if constexpr (M == 8) {
-        i = __builtin_amdgcn_update_dpp(0, i, 0x128, 0xF, 0xF, false);    // row_ror:8
-    } else {
-        static_assert(M == 16, "lane ^ 1, 2, 4, 8 or 16");
-        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)i, (uint32_t)i, false, false);
-        i = (int)((threadIdx.x & 16) ? r[0] : r[1]);
-    }
+    else
+        i = __builtin_amdgcn_ds_swizzle(i, (M << 10) | 0x1F);             // and 0x1F, or 0, xor M
     return __builtin_bit_cast(float, i);
 }
 

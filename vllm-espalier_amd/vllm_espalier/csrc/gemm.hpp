@@ -185,26 +185,17 @@ inline int host_stage_words(int k2, int kr) {
     return (nst > 1 ? 2 : 1) * 2 * sst * row_words;
 }
 
-// A operand from fp16 rows in shared memory (LDS = true) or global memory: row group g's lane row is row[g] (has[g]
-// false: a zero row); slots [4(G&1) + 0..3, 8 + 4(G&1) + 0..3] of the lane's k tile (G >> 1), as trellis.hpp's B slots.
-// The rows carry their address space so the loads are ds_read or global_load, never flat: a flat load counts against
-// vmcnt, which returns in order, so each step's A load would also wait for the trellis copies still in flight.
-template <bool LDS>
-struct RowPtr;
-template <>
-struct RowPtr<true> {
-    typedef __attribute__((address_space(3))) const uint16_t* u16;
-    typedef __attribute__((address_space(3))) const uint64_t* u64;
-};
-template <>
-struct RowPtr<false> {
-    typedef __attribute__((address_space(1))) const uint16_t* u16;
-    typedef __attribute__((address_space(1))) const uint64_t* u64;
-};
-
+// A operand from fp16 rows in shared memory (LDS = true) or global memory: row group g's lane row, slots
+// [4(G&1) + 0..3, 8 + 4(G&1) + 0..3] of the lane's k tile (G >> 1), as trellis.hpp's B slots; a missing row reads as
+// zeros. Shared-memory rows carry their address space, so their loads are ds_read and never flat: a flat load counts
+// against vmcnt, which returns in order, so each step's A load would also wait for the trellis copies still in flight.
 template <int MG, bool LDS>
-struct RowsA {
-    typedef typename RowPtr<LDS>::u16 ptr_t;
+struct RowsA;
+
+template <int MG>
+struct RowsA<MG, true> {
+    typedef __attribute__((address_space(3))) const uint16_t* ptr_t;
+    typedef __attribute__((address_space(3))) const uint64_t* u64_t;
     ptr_t row[MG];
     bool has[MG];
     int kbase;          // absolute k of row[g][0]
@@ -217,10 +208,29 @@ struct RowsA {
         uint64_t lo = 0, hi = 0;
         if (has[g]) {
             const ptr_t p = row[g] + (k - kbase);
-            lo = *(typename RowPtr<LDS>::u64)(p);
-            hi = *(typename RowPtr<LDS>::u64)(p + 8);
+            lo = *(u64_t)(p);
+            hi = *(u64_t)(p + 8);
         }
         const u32x4_t t = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+        av = __builtin_bit_cast(f16x8, t);
+    }
+};
+
+// rows in global memory (generic pointers: this form measured faster than address-space-1 loads with a flag)
+template <int MG>
+struct RowsA<MG, false> {
+    const uint16_t* row[MG];
+    int kbase;          // absolute k of row[g][0]
+    __device__ __forceinline__ void set(int g, const uint16_t* p) { row[g] = p; }
+    __device__ __forceinline__ void operator()(int g, int k, f16x8& av) const {
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
+        if (row[g] != nullptr) {
+            const uint16_t* p = row[g] + (k - kbase);
+            lo = *reinterpret_cast<const uint2*>(p);
+            hi = *reinterpret_cast<const uint2*>(p + 8);
+        }
+        const u32x4_t t = {lo.x, lo.y, hi.x, hi.y};
         av = __builtin_bit_cast(f16x8, t);
     }
 };

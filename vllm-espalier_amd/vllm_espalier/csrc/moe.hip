@@ -105,7 +105,10 @@ __device__ void group_block(const int* sh_pick, int n, int R, int slots, int nid
 
 // group_block's tables for n <= 64 picks, by one wave (lane i holds pick i) with no barriers: a pick's member rank is
 // the number of earlier picks (pick order) with its id -- what group_block gives whether or not an id repeats inside a
-// row -- and an id's place the number of smaller distinct ids. Every lane of the wave calls it.
+// row -- and an id's place the number of smaller distinct ids. Every lane of the wave calls it. Its two passes are
+// serial in n (about 12 dependent instructions a pick each), so it beats group_block's four barriers only for a few
+// picks (one token's 9 on MI355X: 0.65 us less a routing launch; 36 picks take 1.6 us more).
+constexpr int GROUP_WAVE_MAX = 16;
 __device__ void group_wave(const int* sh_pick, int n, int slots, int nid, int maxm, int* __restrict__ uids,
                            int* __restrict__ ucount, int* __restrict__ members) {
     const int lane = threadIdx.x & 63;
@@ -398,8 +401,8 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     }
     __syncthreads();
 
-    // 3. grouping of the picks (ids < E + has): one wave when they fit in it
-    if (a.R * slots <= 64) {
+    // 3. grouping of the picks (ids < E + has): one wave for a few
+    if (a.R * slots <= GROUP_WAVE_MAX) {
         if (wave == 0) group_wave(sh_pick, a.R * slots, slots, C, a.maxm, a.uids, a.ucount, a.members);
     } else {
         group_block(sh_pick, a.R * slots, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
