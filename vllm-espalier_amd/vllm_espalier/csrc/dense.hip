@@ -183,12 +183,19 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
 
-    // 0. the first stage of trellis copies, in flight while the input rows are rotated; the block's output scales
+    // 0. the first stage of trellis copies, in flight while the input rows are rotated; the block's output scales.
+    // With the norm in the launch and waves to spare, the copies come from the waves that do not normalise (4 a row
+    // do), so the norm's loads are not queued behind them (vmcnt returns in order) and its barriers can leave them
+    // in flight.
     const uint2 sv = *reinterpret_cast<const uint2*>(S.svh + cb_local * 128 + 4 * l32);
+    const bool norm_apart = a.norm && 4 * M < NW;
     {
         const int steps = kr >> 5;
         const int sst = steps < StagePlan<K2>::MAX_STEPS ? steps : StagePlan<K2>::MAX_STEPS;
-        issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
+        if (norm_apart)
+            issue_stage_waves<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage, 4 * M, NW - 4 * M);
+        else
+            issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
     }
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
@@ -213,8 +220,12 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
             };
             if (idx < M * chunks) weights(idx);
             uint4 zq[NORM_CHUNKS];
-            norm_rows_inv(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv, zq, xs, a.xs_stride,
-                          c0 * 128, (c0 + chunks) * 128);
+            if (norm_apart)
+                norm_rows_inv<true>(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv, zq, xs,
+                                    a.xs_stride, c0 * 128, (c0 + chunks) * 128);
+            else
+                norm_rows_inv(a.nh, a.nd1, a.nd2, a.x_stride, M, a.K, a.neps, bf, npart, ninv, zq, xs, a.xs_stride,
+                              c0 * 128, (c0 + chunks) * 128);
             if (nbg == 0 && split == 0) norm_rows_store(zq, M, a.K, a.x_stride, a.nh_out);
             while (idx < M * chunks) {
                 const int r = idx / chunks, ch = idx % chunks;

@@ -32,7 +32,26 @@ struct StagePlan {
     static constexpr int MAX_STEPS = stage_max_steps(K2);
 };
 
-// Copy k tiles [kt0, kt0 + rows) of the block (n tiles nt0..nt0+7) into lds: 16-byte units, 64 a wave instruction.
+// Copy k tiles [kt0, kt0 + rows) of the block (n tiles nt0..nt0+7) into lds: 16-byte units, 64 a wave instruction,
+// issued by waves w0 .. w0 + nw - 1 of the workgroup (the others issue nothing).
+template <int K2>
+__device__ __forceinline__ void issue_stage_waves(const uint32_t* __restrict__ T, int NTILES, int kt0, int rows,
+                                                  int nt0, uint32_t* lds, int w0, int nw) {
+    constexpr int TW = 4 * K2, UPR = 2 * TW;                                   // 16-byte units a k tile row
+    const int units = rows * UPR;
+    const int wave = (int)(threadIdx.x >> 6) - w0, lane = threadIdx.x & 63;
+    if (wave < 0 || wave >= nw) return;
+    for (int u0 = wave * 64; u0 < units; u0 += nw * 64) {
+        const int u = u0 + lane;
+        if (u < units) {
+            const int r = u / UPR, w = (u - r * UPR) * 4;
+            const uint32_t* src = T + ((size_t)(kt0 + r) * NTILES + nt0) * TW + w;
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
+        }
+    }
+}
+
+// issue_stage_waves by every wave of the workgroup
 template <int K2>
 __device__ __forceinline__ void issue_stage(const uint32_t* __restrict__ T, int NTILES, int kt0, int rows, int nt0,
                                             uint32_t* lds) {

@@ -39,6 +39,39 @@ __device__ __forceinline__ uint4 pack8_16(const float (&v)[8], bool bf) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// z of 8 elements from their raw h, d1, d2 (16-bit, 8 a uint4; a delta only when has1 / has2): h + d1 + d2 in fp32,
+// rounded to the model dtype when a delta was added (the stored residual, exact). Returns z packed.
+__device__ __forceinline__ uint4 norm_z8_of(uint4 uh, uint4 u1, uint4 u2, bool has1, bool has2, bool bf,
+                                            float (&z)[8]) {
+    auto unpack = [bf](uint4 u, float (&v)[8]) __attribute__((always_inline)) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = from16((uint16_t)(w[k] & 0xFFFFu), bf);
+            v[2 * k + 1] = from16((uint16_t)(w[k] >> 16), bf);
+        }
+    };
+    unpack(uh, z);
+    if (has1) {
+        float a[8];
+        unpack(u1, a);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z[j] += a[j];
+    }
+    if (has2) {
+        float b[8];
+        unpack(u2, b);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z[j] += b[j];
+    }
+    if (has1 || has2) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z[j] = from16(to16(z[j], bf), bf);     // the stored (rounded) residual
+        return pack8_16(z, bf);
+    }
+    return uh;
+}
+
 // Thread t's chunks of row (h, d1, d2) (elements (c * 256 + t) * 8 .. + 8, c < NORM_CHUNKS, those below D): z packed
 // in the model dtype (the stored residual, exact; h itself when no delta is added) and its share of the sum of squares.
 // Every load is issued before any is used, so the three operands cost one memory round trip.
@@ -57,38 +90,13 @@ __device__ __forceinline__ float norm_z_rows(const uint16_t* h, const uint16_t* 
             u2[c] = *reinterpret_cast<const uint4*>(p2 + i);
         }
     }
-    auto unpack = [bf](uint4 u, float (&v)[8]) __attribute__((always_inline)) {
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            v[2 * k] = from16((uint16_t)(w[k] & 0xFFFFu), bf);
-            v[2 * k + 1] = from16((uint16_t)(w[k] >> 16), bf);
-        }
-    };
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NORM_CHUNKS; ++c) {
         zq[c] = uh[c];
         if ((c * 256 + t) * 8 < D) {
             float z[8];
-            unpack(uh[c], z);
-            if (d1) {
-                float a[8];
-                unpack(u1[c], a);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) z[j] += a[j];
-            }
-            if (d2) {
-                float b[8];
-                unpack(u2[c], b);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) z[j] += b[j];
-            }
-            if (d1 || d2) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) z[j] = from16(to16(z[j], bf), bf);     // the stored (rounded) residual
-                zq[c] = pack8_16(z, bf);
-            }
+            zq[c] = norm_z8_of(uh[c], u1[c], u2[c], d1 != nullptr, d2 != nullptr, bf, z);
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += z[j] * z[j];
         }
@@ -103,10 +111,17 @@ __device__ __forceinline__ float norm_inv(const float* part4, int D, float eps) 
 }
 
 // Rows r < R of a workgroup of at least 256 * R threads: waves 4r..4r+3 take row r (thread t = tid & 255). Every
-// thread calls it; on return inv_sh[r] holds row r's scale and zq thread t's chunks of row r's z (norm_z_rows). With
+// thread calls it (LDS_ONLY: its barriers wait only for shared-memory work, see lds_barrier); on return inv_sh[r] holds row r's scale and zq thread t's chunks of row r's z (norm_z_rows). With
 // zs (shared memory), the z elements i in [lo, hi) of row r are also stored at zs[r * zs_stride + i - lo], visible to
 // the whole workgroup on return (lo and hi multiples of 8). Two workgroup barriers inside. Row r of h / d1 / d2
 // starts at r * stride.
+// A workgroup barrier that waits only for this wave's shared-memory work (not for its global loads or LDS copies in
+// flight, as __syncthreads' fence does): for exchanges through shared memory while trellis copies stream in.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <bool LDS_ONLY = false>
 __device__ __forceinline__ void norm_rows_inv(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int stride,
                                               int R, int D, float eps, bool bf, float* part_sh, float* inv_sh,
                                               uint4 (&zq)[NORM_CHUNKS], uint16_t* zs = nullptr, int zs_stride = 0,
@@ -124,9 +139,9 @@ __device__ __forceinline__ void norm_rows_inv(const uint16_t* h, const uint16_t*
             }
         }
     }
-    __syncthreads();
+    if constexpr (LDS_ONLY) lds_barrier(); else __syncthreads();
     if ((int)threadIdx.x < R) inv_sh[threadIdx.x] = norm_inv(part_sh + 4 * threadIdx.x, D, eps);
-    __syncthreads();
+    if constexpr (LDS_ONLY) lds_barrier(); else __syncthreads();
 }
 
 // thread t's chunks of its row (norm_rows_inv's zq) stored at row (o = r * stride) of out

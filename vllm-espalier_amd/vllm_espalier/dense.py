@@ -19,6 +19,7 @@ MAX_ROWS = 32
 COUNTER_STRIDE = 32          # ints between two 128-column blocks' arrival counters (one 128-byte line each)
 ROT_SMEM = int(os.environ.get("ESPALIER_DENSE_ROTATION_SMEM", 64 * 1024))   # fuse the input rotation up to this much LDS
 _scratch: dict = {}
+_outgrown: list = []         # scratch a growth replaced: kept alive, since graphs captured before it still use it
 
 
 def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
@@ -46,11 +47,14 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
 
 
 def scratch(device, z_floats: int, xh_halves: int):
-    """Shared scratch, grown while layers are prepared (before any graph capture), never during a forward."""
+    """Shared scratch, grown while layers are prepared, never during a forward. A buffer that a growth replaces is
+    never freed: a graph captured before the growth keeps writing to the buffer it was captured with."""
     s = _scratch.get(device)
     if s is None or s[0].numel() < z_floats or s[1].numel() < xh_halves:
         z = max(z_floats, s[0].numel() if s else 0, 1)
         h = max(xh_halves, s[1].numel() if s else 0, 1)
+        if s is not None:
+            _outgrown.append(s)
         s = (torch.empty(z, dtype=torch.float32, device=device), torch.empty(h, dtype=torch.half, device=device))
         _scratch[device] = s
     return s
