@@ -167,11 +167,46 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int last;
     const int nbg = blockIdx.x, split = blockIdx.y;
+    // What the first copy needs -- every shard's trellis pointer, first block and width, the split and the launch
+    // shape -- in one round of kernel-argument loads, consumed together by one empty asm: an indexed load of the
+    // workgroup's shard would wait for the shard's selection, and each later first use for its own round trip.
+    const Shard* sa = a.s;
+    const uint32_t* T4[MAX_SHARDS];
+    int nb04[MAX_SHARDS], nb4[MAX_SHARDS];
+#pragma unroll
+    for (int i = 0; i < MAX_SHARDS; ++i) {
+        T4[i] = sa[i].T;
+        nb04[i] = sa[i].nb0;
+        nb4[i] = sa[i].nb;
+    }
+    const int an = a.n, aM = a.M, aSQ = a.SQ, aSR = a.SR, anorm = a.norm, afused = a.fused;
+    const int nthreads = (int)blockDim.x;
+    asm volatile("" ::"s"(T4[0]), "s"(T4[1]), "s"(T4[2]), "s"(T4[3]), "s"(nb04[0]), "s"(nb04[1]), "s"(nb04[2]),
+                 "s"(nb04[3]), "s"(nb4[0]), "s"(nb4[1]), "s"(nb4[2]), "s"(nb4[3]), "s"(an), "s"(aM), "s"(aSQ),
+                 "s"(aSR), "s"(anorm), "s"(afused), "s"(nthreads));
     int si = 0;
 #pragma unroll
     for (int i = 1; i < MAX_SHARDS; ++i)
-        if (i < a.n && nbg >= a.s[i].nb0) si = i;
-    const Shard S = a.s[si];
+        if (i < an && nbg >= nb04[i]) si = i;
+    // the copy's fields picked among the loaded ones; the rest of the shard read by index where first used
+    struct {
+        const uint32_t* T;
+        int nb0, nb;
+        const uint16_t *suh, *svh;
+        int col0;
+        float scale;
+    } S{T4[0], nb04[0], nb4[0], nullptr, nullptr, 0, 0.f};
+#pragma unroll
+    for (int i = 1; i < MAX_SHARDS; ++i)
+        if (si == i) {
+            S.T = T4[i];
+            S.nb0 = nb04[i];
+            S.nb = nb4[i];
+        }
+    S.suh = a.s[si].suh;
+    S.svh = a.s[si].svh;
+    S.col0 = a.s[si].col0;
+    S.scale = a.s[si].scale;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int c = lane & 15, G = lane >> 4;
     const int NTILES = S.nb * 8;
@@ -186,8 +221,8 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     // 0. the first stage of trellis copies, in flight while the input rows are rotated; the block's output scales.
     // With the norm in the launch and waves to spare, the copies come from the waves that do not normalise (4 a row
     // do), so the norm's loads are not queued behind them (vmcnt returns in order) and its barriers can leave them
-    // in flight.
-    const uint2 sv = *reinterpret_cast<const uint2*>(S.svh + cb_local * 128 + 4 * l32);
+    // in flight. The scales are loaded after the copies are issued: they need the shard's other fields, a later
+    // round of argument loads.
     const bool norm_apart = a.norm && 4 * M < NW;
     {
         const int steps = kr >> 5;
@@ -197,6 +232,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         else
             issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
     }
+    const uint2 sv = *reinterpret_cast<const uint2*>(S.svh + cb_local * 128 + 4 * l32);
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
     RowsA<MG, true> al;       // fused: the rotated rows in shared memory
