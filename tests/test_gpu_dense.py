@@ -228,3 +228,31 @@ def test_matmul_op_windows(dev, T):
     W = O.dequant_f32(m.trellis.cpu().numpy(), 2 * m.K, experts.KERNEL_CB[m.cb])
     ref = O.linear_ref(x.float().cpu().numpy(), W, bits(m.suh), bits(m.svh))
     assert O.rel_l2(y.float().cpu().numpy(), ref) < 2e-3
+
+
+@pytest.mark.parametrize("T", [33, 70])
+def test_prefill_gemm_mode(dev, monkeypatch, T):
+    """ESPALIER_PREFILL_MODE=gemm (ops.py): above 32 rows every matrix is decoded by the dequant kernel, rotated by the
+    had kernel on both sides and multiplied by torch's fp16 matmul. Within the 2e-2 bar of the dequantise-then-fp64
+    reference, per matrix (espalier::matmul) and for a layer of three matrices with padded output (espalier::dense);
+    not bit-identical to the windowed kernels (another summation order), so compared with the reference only."""
+    monkeypatch.setattr(ops, "PREFILL", "gemm")
+    mats = _mats([(512, 384, 4, "int6"), (512, 256, 3, "int5"), (512, 128, 2, "e2m1")], 18 + T, dev)
+    x = torch.randn((T, 512), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).to(dev)
+    refs = []
+    for m in mats:
+        W = O.dequant_f32(m.trellis.cpu().numpy(), 2 * m.K, experts.KERNEL_CB[m.cb])
+        refs.append(O.linear_ref(x.float().cpu().numpy(), W, bits(m.suh), bits(m.svh)))
+        y = torch.ops.espalier.matmul(x.half(), m.trellis, m.suh, m.svh, m.K, m.cb)
+        assert y.dtype == torch.float16 and y.shape == (T, m.out_features)
+        assert O.rel_l2(y.float().cpu().numpy(), refs[-1]) < 2e-2
+    d = D.Dense(mats, n_out=896)
+    key = next(ops.DENSE_KEYS)
+    ops.DENSE_LAYERS[key] = d
+    try:
+        y = torch.ops.espalier.dense(x, [m.trellis for m in mats], [m.suh for m in mats], [m.svh for m in mats], key)
+    finally:
+        ops.DENSE_LAYERS.pop(key)
+    assert y.dtype == x.dtype and y.shape == (T, 896)
+    assert O.rel_l2(y[:, :768].float().cpu().numpy(), np.concatenate(refs, axis=1)) < 2e-2
+    assert not y[:, 768:].any()
