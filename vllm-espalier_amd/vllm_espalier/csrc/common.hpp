@@ -210,18 +210,29 @@ __device__ __forceinline__ void store_dev(unsigned long long* p, unsigned long l
 __device__ __forceinline__ unsigned long long load_dev(const unsigned long long* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 4 floats (16-byte aligned) as two 64-bit device-scope accesses: half the instructions of four 32-bit ones
-__device__ __forceinline__ void store_dev4(float* p, const float4& v) {
-    auto q = reinterpret_cast<unsigned long long*>(p);
-    store_dev(q, (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)__float_as_uint(v.y) << 32));
-    store_dev(q + 1, (unsigned long long)__float_as_uint(v.z) | ((unsigned long long)__float_as_uint(v.w) << 32));
-}
-__device__ __forceinline__ float4 load_dev4(const float* p) {
-    auto q = reinterpret_cast<const unsigned long long*>(p);
-    const unsigned long long a = load_dev(q), b = load_dev(q + 1);
-    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
-                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
-}
+// Device-scope 16-byte accesses: one buffer_load / buffer_store_dwordx4 with cache policy sc1 (coherent across the
+// XCDs' L2s, as the agent-scope atomics above are), so a 32-lane half moves whole 128-byte lines. The buffer resource
+// covers 4 GiB from base, which every lane shares; each lane's address goes in as its byte offset from base.
+constexpr int CPOL_SC1 = 16;                    // the cache-policy operand's sc1 bit (gfx94x / gfx950)
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+struct DevBuf {
+    __amdgpu_buffer_rsrc_t r;
+    const char* b;
+    __device__ __forceinline__ explicit DevBuf(const void* base)
+        : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000)),
+          b(static_cast<const char*>(base)) {}
+    __device__ __forceinline__ uint32_t off(const float* p) const {
+        return (uint32_t)(reinterpret_cast<const char*>(p) - b);
+    }
+    __device__ __forceinline__ float4 load4(const float* p) const {
+        const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(r, off(p), 0, CPOL_SC1);
+        return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    }
+    __device__ __forceinline__ void store4(float* p, const float4& v) const {
+        const u32x4v u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+        __builtin_amdgcn_raw_buffer_store_b128(u, r, off(p), 0, CPOL_SC1);
+    }
+};
 
 constexpr int CNT_STRIDE = 32;   // ints between two arrival counters: one 128-byte line each, so workgroups arriving
                                  // on different counters never queue on one line's atomics

@@ -329,8 +329,9 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     }
     // 4. K splits: partials to Z, the last split of the block to arrive adds them in split order and finishes
     const size_t zrow = (size_t)a.NBT * 128;
+    const DevBuf zb(a.Z);
     for (int r = wave * 2 + half; r < M; r += 2 * NW)
-        store_dev4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
+        zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
     if (!arrive_last(a.counters + (size_t)nbg * CNT_STRIDE, a.SK, &last)) return;
     const size_t zsplit = (size_t)M * zrow;
     if (a.gather) {
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         const int idx = wave * 2 + half;
         if (idx < M * a.SK) {
             const int r = idx / a.SK, q = idx - r * a.SK;
-            zs[idx * 32 + l32] = load_dev4(a.Z + (size_t)q * zsplit + (size_t)r * zrow + nbg * 128 + 4 * l32);
+            zs[idx * 32 + l32] = zb.load4(a.Z + (size_t)q * zsplit + (size_t)r * zrow + nbg * 128 + 4 * l32);
         }
         __syncthreads();
         for (int r = wave * 2 + half; r < M; r += 2 * NW) {
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
             float4 u[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                if (q0 + i < a.SK) u[i] = load_dev4(zp + (q0 + i) * zsplit);
+                if (q0 + i < a.SK) u[i] = zb.load4(zp + (q0 + i) * zsplit);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (q0 + i == 0) {
@@ -477,6 +478,7 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
     a.n = (int)n_shards;
     ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= (int64_t)nbt * CNT_STRIDE),
                 "scratch too small: Z needs SK*M*N floats, counters 32 per 128 columns");
+    ESP_REQUIRE(SK * M * nbt * 128 <= (int64_t(1) << 30), "dense: the partials must fit in 4 GiB");
     const int64_t sq = (K / 32) / SK, sr = (K / 32) % SK;
     const int64_t steps_max = sq + (sr > 0);                  // the longest split
     const int64_t kr = steps_max * 32;

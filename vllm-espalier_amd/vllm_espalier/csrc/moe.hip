@@ -545,7 +545,7 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
         s4.x *= scale; s4.y *= scale; s4.z *= scale; s4.w *= scale;
         float* zp = Zm + (size_t)rows_sh[m] * a.N + nt0 * 16 + 4 * l32;
         if (dev)
-            store_dev4(zp, s4);
+            DevBuf(a.Z).store4(zp, s4);
         else
             *reinterpret_cast<float4*>(zp) = s4;
     }
@@ -559,13 +559,15 @@ __device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
 // sum over SK splits (stride apart) of the 4 floats at p, in split order, with up to 8 splits' loads in flight;
 // DEV: device-scope loads (partials another workgroup of the same launch stored)
 template <bool DEV = false>
-__device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t stride, int SK, float (&v)[4]) {
+__device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t stride, int SK, float (&v)[4],
+                                            const float* zbase = nullptr) {
+    const DevBuf zb(zbase);                              // DEV: the partials lie within 4 GiB above zbase
     for (int q0 = 0; q0 < SK; q0 += 8) {
         float4 u[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             if (q0 + i < SK)
-                u[i] = DEV ? load_dev4(p + (size_t)(q0 + i) * stride)
+                u[i] = DEV ? zb.load4(p + (size_t)(q0 + i) * stride)
                            : *reinterpret_cast<const float4*>(p + (size_t)(q0 + i) * stride);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -582,13 +584,14 @@ __device__ __forceinline__ void sum_splits4(const float* __restrict__ p, size_t 
 // in split order as sum_splits4 does
 template <bool DEV>
 __device__ __forceinline__ void sum_splits4x2(const float* __restrict__ pg, const float* __restrict__ pu, size_t stride,
-                                              int SK, float (&g)[4], float (&u)[4]) {
+                                              int SK, float (&g)[4], float (&u)[4], const float* zbase = nullptr) {
+    const DevBuf zb(zbase);                              // DEV: the partials lie within 4 GiB above zbase
     float4 a[8], b[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         if (i < SK) {
-            a[i] = DEV ? load_dev4(pg + (size_t)i * stride) : *reinterpret_cast<const float4*>(pg + (size_t)i * stride);
-            b[i] = DEV ? load_dev4(pu + (size_t)i * stride) : *reinterpret_cast<const float4*>(pu + (size_t)i * stride);
+            a[i] = DEV ? zb.load4(pg + (size_t)i * stride) : *reinterpret_cast<const float4*>(pg + (size_t)i * stride);
+            b[i] = DEV ? zb.load4(pu + (size_t)i * stride) : *reinterpret_cast<const float4*>(pu + (size_t)i * stride);
         }
     g[0] = a[0].x; g[1] = a[0].y; g[2] = a[0].z; g[3] = a[0].w;
     u[0] = b[0].x; u[1] = b[0].y; u[2] = b[0].z; u[3] = b[0].w;
@@ -851,10 +854,10 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
             float gv[4], uv[4], v[4];
             if (a.SK <= 8) {
                 sum_splits4x2<true>(a.Z + (size_t)p * a.N + n, a.Z + ((size_t)a.SK * a.P + p) * a.N + n,
-                                    (size_t)a.P * a.N, a.SK, gv, uv);
+                                    (size_t)a.P * a.N, a.SK, gv, uv, a.Z);
             } else {
-                sum_splits4<true>(a.Z + (size_t)p * a.N + n, (size_t)a.P * a.N, a.SK, gv);
-                sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv);
+                sum_splits4<true>(a.Z + (size_t)p * a.N + n, (size_t)a.P * a.N, a.SK, gv, a.Z);
+                sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv, a.Z);
             }
             gateup_unit(gv, uv, sc, a.limit, a.act_mode, l32, v);
             store4(a.xd, F16, (size_t)p * a.N + n, v);
@@ -1090,6 +1093,7 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
                 "moe_gateup: K must split into whole 128-blocks, N a multiple of 128");
     ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
     ESP_REQUIRE(z_numel >= 2 * SK * P * N, "Z too small");
+    ESP_REQUIRE(2 * SK * P * N <= (int64_t(1) << 30), "moe_gateup: the partials must fit in 4 GiB");
     ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
     ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
