@@ -281,8 +281,8 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         }
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
-            const int row = g * 16 + c;
-            al.set(g, row < M ? xs + (size_t)row * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
+            const int row = g * 16 + c;                     // a row past M reads row 0: its sums are never stored
+            al.set(g, xs + (size_t)(row < M ? row : 0) * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1));
         }
         al.kbase = c0 * 128;
     } else {
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
             const int row = g * 16 + c;
-            ag.set(g, row < M ? X + (size_t)row * a.K + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
+            ag.set(g, X + (size_t)(row < M ? row : 0) * a.K + 16 * (G >> 1) + 4 * (G & 1));
         }
         ag.kbase = 0;
     }

@@ -119,7 +119,7 @@ __device__ __forceinline__ void block_gemm(const uint32_t* __restrict__ T, int N
                                            bool prologue_issued) {
     constexpr int TW = 4 * K2;
     constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;   // scalar k loop
     const int pair = wave & 3, kw = wave >> 2;
     const int G = lane >> 4;
     const int steps = kr >> 5;
@@ -205,9 +205,11 @@ inline int host_stage_words(int k2, int kr) {
 }
 
 // A operand from fp16 rows in shared memory (LDS = true) or global memory: row group g's lane row, slots
-// [4(G&1) + 0..3, 8 + 4(G&1) + 0..3] of the lane's k tile (G >> 1), as trellis.hpp's B slots; a missing row reads as
-// zeros. Shared-memory rows carry their address space, so their loads are ds_read and never flat: a flat load counts
-// against vmcnt, which returns in order, so each step's A load would also wait for the trellis copies still in flight.
+// [4(G&1) + 0..3, 8 + 4(G&1) + 0..3] of the lane's k tile (G >> 1), as trellis.hpp's B slots. Every lane loads, with
+// no branch: a lane of a missing row (past the rows or members) is given a present row's address by its caller, and
+// since row i of an MFMA result depends on row i of A alone, those rows' sums are simply never stored. Shared-memory
+// rows carry their address space, so their loads are ds_read and never flat: a flat load counts against vmcnt, which
+// returns in order, so each step's A load would also wait for the trellis copies still in flight.
 template <int MG, bool LDS>
 struct RowsA;
 
@@ -216,20 +218,12 @@ struct RowsA<MG, true> {
     typedef __attribute__((address_space(3))) const uint16_t* ptr_t;
     typedef __attribute__((address_space(3))) const uint64_t* u64_t;
     ptr_t row[MG];
-    bool has[MG];
     int kbase;          // absolute k of row[g][0]
-    __device__ __forceinline__ void set(int g, const uint16_t* p) {
-        has[g] = p != nullptr;
-        row[g] = p != nullptr ? (ptr_t)p : ptr_t();
-    }
+    __device__ __forceinline__ void set(int g, const uint16_t* p) { row[g] = (ptr_t)p; }
     __device__ __forceinline__ void operator()(int g, int k, f16x8& av) const {
         typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-        uint64_t lo = 0, hi = 0;
-        if (has[g]) {
-            const ptr_t p = row[g] + (k - kbase);
-            lo = *(u64_t)(p);
-            hi = *(u64_t)(p + 8);
-        }
+        const ptr_t p = row[g] + (k - kbase);
+        const uint64_t lo = *(u64_t)(p), hi = *(u64_t)(p + 8);
         const u32x4_t t = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
         av = __builtin_bit_cast(f16x8, t);
     }
@@ -243,12 +237,8 @@ struct RowsA<MG, false> {
     __device__ __forceinline__ void set(int g, const uint16_t* p) { row[g] = p; }
     __device__ __forceinline__ void operator()(int g, int k, f16x8& av) const {
         typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-        uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
-        if (row[g] != nullptr) {
-            const uint16_t* p = row[g] + (k - kbase);
-            lo = *reinterpret_cast<const uint2*>(p);
-            hi = *reinterpret_cast<const uint2*>(p + 8);
-        }
+        const uint16_t* p = row[g] + (k - kbase);
+        const uint2 lo = *reinterpret_cast<const uint2*>(p), hi = *reinterpret_cast<const uint2*>(p + 8);
         const u32x4_t t = {lo.x, lo.y, hi.x, hi.y};
         av = __builtin_bit_cast(f16x8, t);
     }

@@ -525,7 +525,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
     for (int g = 0; g < MG; ++g) {
         const int m = g * 16 + c;
         const int p = rows_sh[m];
-        al.set(g, p >= 0 ? abase + (size_t)(by_member ? m : p) * astride + 16 * (G >> 1) + 4 * (G & 1) : nullptr);
+        // a missing member (p < 0) reads row 0: its sums are never stored
+        al.set(g, abase + (size_t)(p >= 0 ? (by_member ? m : p) : 0) * astride + 16 * (G >> 1) + 4 * (G & 1));
     }
     al.kbase = kbase;
     f32x4 acc[2][MG];

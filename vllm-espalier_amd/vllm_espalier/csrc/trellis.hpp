@@ -101,13 +101,16 @@ __device__ __forceinline__ void run_states(uint32_t w0, uint32_t w1, uint32_t w2
 __device__ __forceinline__ uint32_t mcg_hash(uint32_t s) { return (s * MCG_MUL & MCG_MASK) ^ MCG_XOR; }
 
 // mcg values of two states as packed fp16 (lo = s0): the two halves of each hash added in one RNE fp16 add
-// (experts_grouped.cuh:64-79)
+// (experts_grouped.cuh:64-79). Two v_add_f16 reading the halves through SDWA, the second writing the high half of the
+// result and keeping its low half: two instructions a pair, where gathering the halves for one packed add takes three.
 __device__ __forceinline__ uint32_t mcg_pair(uint32_t s0, uint32_t s1) {
     const uint32_t x0 = mcg_hash(s0), x1 = mcg_hash(s1);
-    const uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-    const uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-    const f16x2 r = __builtin_bit_cast(f16x2, lo) + __builtin_bit_cast(f16x2, hi);
-    return __builtin_bit_cast(uint32_t, r);
+    uint32_t d;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(d) : "v"(x0));
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "+v"(d) : "v"(x1));
+    return d;
 }
 
 // mcg value of one state: the two halves of its hash added in one RNE fp16 add (a v_add_f16 reading the high half
