@@ -142,8 +142,9 @@ __device__ __forceinline__ uint32_t decode_pair(uint32_t s0, uint32_t s1) {
         // more apart, relative). Back to fp16 through the same instruction pair, then * 0.75 (exact).
         const float k = E2M1_K;
         const float y0 = mul_mix(mcg_one(s0), k), y1 = mul_mix(mcg_one(s1), k);   // no packing of the two values
-        uint32_t code = 0u, h;
-        asm("v_cvt_scalef32_pk_fp4_f32 %0, %1, %2, %3" : "+v"(code) : "v"(y0), "v"(y1), "v"(1.0f));
+        // the conversion writes byte 0 of code and keeps the other three, which nothing reads: an output operand
+        uint32_t code, h;
+        asm("v_cvt_scalef32_pk_fp4_f32 %0, %1, %2, %3" : "=v"(code) : "v"(y0), "v"(y1), "v"(1.0f));
         asm("v_cvt_scalef32_pk_f16_fp4 %0, %1, %2" : "=v"(h) : "v"(code), "v"(1.0f));
         if constexpr (CB == 19) return h;                  // the unscaled grid: the GEMM scales its sums by 0.75
         const f16x2 q = __builtin_bit_cast(f16x2, h) * f16x2{(_Float16)0.75f, (_Float16)0.75f};
