@@ -760,7 +760,7 @@ __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, c
 }
 
 template <int OUT_DTYPE>
-__global__ __launch_bounds__(256) void down_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
+__global__ __launch_bounds__(1024) void down_combine_kernel(const float* __restrict__ Z, const int* __restrict__ pick,
                                                            const uint16_t* __restrict__ svh_d, float* __restrict__ y,
                                                            const float* __restrict__ wts, void* __restrict__ out,
                                                            void* __restrict__ out_shared, int P, int D, int SK, int E,
@@ -1189,16 +1189,18 @@ static int down_combine_any(const float* Z, const int32_t* pick, const void* svh
     ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
     if (rows <= 0) return esp_host::ok();
     dim3 grid((unsigned)rows, (unsigned)(D / 128));
+    // a 32-lane half a slot, so every slot's partials are loaded in one round (9 slots: 320 threads, not 256)
+    const unsigned nt = slots * 32 <= 256 ? 256u : (unsigned)((slots * 32 + 63) / 64 * 64);
     hipStream_t s = (hipStream_t)stream;
     auto svh = static_cast<const uint16_t*>(svh_d);
     if (out_dtype == ESP_BF16)
-        down_combine_kernel<BF16><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+        down_combine_kernel<BF16><<<grid, nt, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
                                                       (int)E, (int)slots, (int)n_routed);
     else if (out_dtype == ESP_F16)
-        down_combine_kernel<F16><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+        down_combine_kernel<F16><<<grid, nt, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
                                                      (int)E, (int)slots, (int)n_routed);
     else
-        down_combine_kernel<F32><<<grid, 256, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
+        down_combine_kernel<F32><<<grid, nt, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
                                                      (int)E, (int)slots, (int)n_routed);
     return esp_host::launch_check("down_combine");
 }
