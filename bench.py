@@ -33,9 +33,9 @@ sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
 # HBM bytes a qkv launch moves at batch 1, from the two rocprofv3 --pmc passes over `bench.py --traffic-probe` (the
-# summary under profiles/): FETCH_SIZE 2783.4 KiB x 2.000 + WRITE_SIZE 138.8 KiB x 1.000, the factors being what the
+# summary under profiles/): FETCH_SIZE 2788.4 KiB x 2.000 + WRITE_SIZE 138.8 KiB x 1.000, the factors being what the
 # counters read for a 256 MiB copy. Re-measured whenever the dense kernel changes.
-QKV_TRAFFIC_BYTES = 5841917
+QKV_TRAFFIC_BYTES = 5852147
 COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
 
 
