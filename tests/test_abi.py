@@ -55,18 +55,20 @@ def _dense(lib, **over):
     f.argtypes = [P, ctypes.c_int, I64, I64, I64, I64, ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(P),
                   ctypes.POINTER(I64), ctypes.POINTER(I64), P, ctypes.c_int, I64, I64, P, I64, P, I64, P, I64, I64,
                   I64, I64, I64, I64, I64, P]
-    a = dict(M=1, K=2048, n=1, ncols=2048, col0=0, y_cols=2048, k2=8, cb=7, SK=1, W=4)
+    a = dict(M=1, K=2048, n=1, ncols=2048, col0=0, y_cols=2048, k2=8, cb=7, SK=1, W=4, z_numel=1 << 30)
     a.update(over)
     one = (P * 1)(16)                                   # non-null, never dereferenced: the checks fail first
     nc, c0 = (I64 * 1)(a["ncols"]), (I64 * 1)(a["col0"])
     rc = f(16, 1, a["K"], a["M"], a["K"], a["n"], one, one, one, nc, c0, 16, 1, a["y_cols"], a["y_cols"], 16, 1 << 30,
-           16, 1 << 30, 16, 1 << 20, a["k2"], a["cb"], a["SK"], a["W"], 2, 0, None)
+           16, a["z_numel"], 16, 1 << 20, a["k2"], a["cb"], a["SK"], a["W"], 2, 0, None)
     return rc, lib.esp_last_error().decode()
 
 
 @pytest.mark.parametrize("over,needle", [
     (dict(M=0), "rows"), (dict(M=33), "rows"), (dict(n=5), "matrices"), (dict(K=2000), "K"),
     (dict(W=6), "W"), (dict(ncols=100), "shape"), (dict(col0=100), "past y"), (dict(SK=65), "SK"), (dict(SK=0), "SK"),
+    # the split-K partials are addressed by 32-bit byte offsets from Z (16-byte buffer accesses): at most 4 GiB
+    (dict(M=32, SK=64, ncols=4160 * 128, y_cols=4160 * 128, z_numel=1 << 40), "4 GiB"),
 ])
 def test_dense_argument_errors(lib, over, needle):
     rc, msg = _dense(lib, **over)
