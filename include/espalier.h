@@ -49,7 +49,8 @@ int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2
  * y[:, col0[s] : col0[s] + n_cols[s]] = H(H(x * suh_s) @ W_s) * svh_s, M <= 32 rows.
  * x [M][x_stride] (x_dtype), trellis[s] int16 [K/16][n_cols[s]/16][8*k2], suh[s] fp16 [K], svh[s] fp16 [n_cols[s]],
  * y [M][y_stride] (y_dtype) with y_cols columns. Scratch: xh fp16 (xh_numel halves; n_shards*M*K used when the input
- * rotation is not fused), Z fp32 (z_numel; SK*M*sum(n_cols) used when SK > 1), counters int32 (counters_numel;
+ * rotation is not fused), Z fp32 (z_numel; SK*M*sum(n_cols) used when SK > 1, at most 2^30 floats: the partials
+ * are addressed by 32-bit byte offsets), counters int32 (counters_numel;
  * 2 * sum(n_cols)/128 used, zero on entry and left zero). SK K splits; W, PF tile hints; the input rotation is fused
  * when M * (K / SK) * 2 <= rot_smem bytes. */
 int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
@@ -132,7 +133,7 @@ int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, fl
 /* rot_in + grouped (mats = 2) + gateup_epilogue in one launch: the member rows of each distinct expert are rotated
  * (x * suh, H) inside the launch, and the last of the 2 * SK programs of an (expert, 128-column block) to arrive runs the
  * gate/up epilogue of its rows into xd fp16 [P][N]. Arguments as esp_rot_in, esp_grouped and esp_gateup_epilogue;
- * (K / SK) % 128 == 0; counters >= nexp_max * (N / 128) * 32. */
+ * (K / SK) % 128 == 0; counters >= nexp_max * (N / 128) * 32; the 2 * SK * P * N partials at most 2^30 floats. */
 int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
                    const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1, const int32_t* C0,
                    const int32_t* C1, const int32_t* uids, int64_t nexp_max, const int32_t* ucount,
