@@ -279,6 +279,30 @@ def test_down_combine2_bit_exact(dev, ext, out_dtype):
     assert np.array_equal(oc.cpu().numpy(), wo_all)
 
 
+@pytest.mark.parametrize("slots", [4, 8, 13, 32])
+def test_down_combine2_slot_counts(dev, ext, slots):
+    """down_combine2 launches a 32-lane half a slot (at least 256 threads, up to 1024 at 32 slots): bit-exact against
+    the oracle at every width, the routed sum over all but the last slot and the last one gated apart."""
+    print(f"down_combine2 slots={slots}", flush=True)
+    gen = torch.Generator().manual_seed(50 + slots)
+    R, E, Dd, SK = 3, 40, 256, 3
+    P = R * slots
+    Z = torch.randn((SK, P, Dd), generator=gen)
+    pick = torch.randint(-1, E, (P,), generator=gen).to(torch.int32)
+    svh_d = torch.randn((E, Dd), generator=gen).half()
+    y0 = torch.randn((P, Dd), generator=gen)
+    wts = torch.rand((P,), generator=gen)
+    y = y0.clone().to(dev)
+    out = torch.zeros((R, Dd), dtype=torch.float32, device=dev)
+    osh = torch.zeros((R, Dd), dtype=torch.float32, device=dev)
+    ext.down_combine2(Z.to(dev), pick.to(dev), svh_d.to(dev), y, wts.to(dev), out, osh, R, P, Dd, SK, slots, E,
+                      slots - 1)
+    wo, ws, wy = O.down_combine2(Z.numpy(), pick.numpy(), bits(svh_d), y0.numpy(), wts.numpy(), R, P, Dd, SK, E,
+                                 slots, slots - 1)
+    assert np.array_equal(y.cpu().numpy(), wy)
+    assert np.array_equal(out.cpu().numpy(), wo) and np.array_equal(osh.cpu().numpy(), ws)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # the whole layer
 # ---------------------------------------------------------------------------------------------------------------
