@@ -475,3 +475,25 @@ def test_moe_fused_launches_equal_unfused(dev, layer16, R, invalid, monkeypatch)
     assert torch.equal(fo.view(torch.int16), uo.view(torch.int16))
     assert torch.equal(fs.view(torch.int16), us.view(torch.int16))
     assert int(s.counters.abs().sum()) == 0                 # every arrival counter left at zero
+
+
+def test_moe_fused_sixteen_splits(dev, layer16, monkeypatch):
+    """esp_moe_gateup at 16 K splits (past eight, the epilogue loads the gate and the up partials as two sets of
+    device-scope loads, not one) against the unfused launches at the same splits, bit for bit, counters left zero."""
+    monkeypatch.setenv("ESPALIER_GROUPED_TILE_PLAN", "4,16;4,4")
+    L, *_ = layer16
+    s = G.Scratch(L.E, L.D, L.I, 32, 9, dev)
+    assert s.cfg_gu[2] == 16
+    gen = torch.Generator().manual_seed(99)
+    R = 2
+    x = torch.randn((R, D), generator=gen).to(torch.bfloat16).to(dev)
+    pick = distinct_picks(R, 16, 8, gen).to(dev)
+    wts = torch.softmax(torch.randn((R, 8), generator=gen), -1).to(dev)
+    monkeypatch.setattr(G, "FUSED", False)
+    uo, us = (t.clone() for t in G.routed2(x, pick, wts, L, s))
+    monkeypatch.setattr(G, "FUSED", True)
+    fo, fs = (t.clone() for t in G.routed2(x, pick, wts, L, s))
+    torch.cuda.synchronize()
+    assert torch.equal(fo.view(torch.int16), uo.view(torch.int16))
+    assert torch.equal(fs.view(torch.int16), us.view(torch.int16))
+    assert int(s.counters.abs().sum()) == 0
