@@ -30,8 +30,20 @@ extern "C" {
 #define ESP_BF16 1
 #define ESP_F32 2
 
+/* Bits of the device status word (esp_status). */
+#define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
+#define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
+
 /* Message of the last failed call on this host thread ("" if none). */
 const char* esp_last_error(void);
+
+/* The device status word of the current GPU into *status, cleared afterwards when clear != 0. The grouped launches
+ * (esp_grouped, esp_moe_gateup) read each expert's width and codebook from device tables the host does not see;
+ * where an entry has no kernel (the reference traps: experts_grouped.cuh:288,293) or a width outside [lo, hi], the
+ * launch issues no copy for that expert, sets its K-split partials to NaN (so every output built from them is
+ * non-finite) and ORs ESP_STATUS_* bits into this word. No counterpart in the reference extension. Synchronises
+ * `stream` (a diagnostic call, not for the decode loop). */
+int esp_status(int32_t* status, int clear, void* stream);
 
 /* ABI version (incremented on any signature change). */
 int esp_abi_version(void);
@@ -50,9 +62,10 @@ int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2
  * x [M][x_stride] (x_dtype), trellis[s] int16 [K/16][n_cols[s]/16][8*k2], suh[s] fp16 [K], svh[s] fp16 [n_cols[s]],
  * y [M][y_stride] (y_dtype) with y_cols columns. Scratch: xh fp16 (xh_numel halves; n_shards*M*K used when the input
  * rotation is not fused), Z fp32 (z_numel; SK*M*sum(n_cols) used when SK > 1, at most 2^30 floats: the partials
- * are addressed by 32-bit byte offsets), counters int32 (counters_numel;
- * 2 * sum(n_cols)/128 used, zero on entry and left zero). SK K splits; W, PF tile hints; the input rotation is fused
- * when M * (K / SK) * 2 <= rot_smem bytes. */
+ * are addressed by 32-bit byte offsets), counters int32 (counters_numel >= 2 * sum(n_cols)/128 when SK > 1, the
+ * reference's size; one counter a 128-column block, min(32, counters_numel / (sum(n_cols)/128)) ints apart, so 32 a
+ * block keeps each on a 128-byte line of its own; zero on entry and left zero). SK K splits; W, PF tile hints; the
+ * input rotation is fused when M * (K / SK) * 2 <= rot_smem bytes. */
 int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
               const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
               const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh, int64_t xh_numel,
@@ -92,7 +105,8 @@ int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const int32_t* pick
 /* Replaces `grouped` (experts.cpp:44-66, experts_grouped.cuh:237-318, 360-377): Z fp32 [mats][SK][P][N] = the K-split
  * partial sums of X_mat[row] @ W_mat[e] for every member row of every distinct expert u < ucount. X0/X1 fp16 [P][K];
  * TP0/TP1 int64 [E] trellis device pointers; B0/B1 int32 [E] K2; C0/C1 int32 [E] codebook ids; uids [nexp_max];
- * members [nexp_max][maxm]. nt, warps, pf are tile hints; lo/hi bound the K2 of the launch's experts. */
+ * members [nexp_max][maxm]. nt, warps, pf are tile hints; lo/hi bound the K2 of the launch's experts (an expert
+ * outside them, or with no kernel, gets NaN partials and a status bit: esp_status). */
 int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
                 const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
                 const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int64_t mats,

@@ -220,6 +220,78 @@ def test_dequant_composition(cb, k2):
     assert np.array_equal(f32, O.f16(ref).astype(np.float32))
 
 
+# The reference's own unpack, emulated lane by lane: Fmt / LaneMap / fetch / decode_tile (experts_grouped.cuh:83-154)
+# and dequant_kernel's placement (:321-340). A 32-lane warp holds tile word l in lane l (and word 32 + l in its
+# second register, load_words :168-177); fetch(idx) is a shuffle from lane idx & 31. This is the warp's algorithm,
+# not the closed form, so it pins the oracle's reading of the format independently of test_state_unpack_bigint.
+def _ref_fmt(k2: int):
+    TW = 4 * k2
+    GV = 2 if k2 >= 13 else (4 if (k2 == 7 or 9 <= k2 <= 12 or k2 == 16) else 8)
+
+    def end(p):
+        return (p >> 1) * k2 + (k2 if p & 1 else k2 >> 1)
+    return TW, GV, 8 // GV, end
+
+
+def _ref_decode_tile_states(words: list[int], k2: int, lane: int) -> list[int]:
+    TW, GV, NG, end = _ref_fmt(k2)
+    M32 = 0xFFFFFFFF
+    if k2 == 8:
+        w0, p = words[lane], words[(lane + 31) & 31]
+        s = ((((p & M32) << 32) | w0) >> 20) & M32             # __funnelshift_r(w0, p, 20)
+        return [(s >> 8) & 0xFFFF, (s >> 4) & 0xFFFF, s & 0xFFFF, w0 >> 16, (w0 >> 12) & 0xFFFF,
+                (w0 >> 8) & 0xFFFF, (w0 >> 4) & 0xFFFF, w0 & 0xFFFF]
+    st = [0] * 8
+    for g in range(NG):
+        last_end = end(8 * lane + g * GV + GV - 1) + 128 * k2
+        hr = (last_end - 1) >> 5
+        hi, lo, sh = hr % TW, (hr + TW - 1) % TW, (hr + 1) * 32 - last_end
+        mm = ((words[lo] << 32) | words[hi]) >> sh
+        for j in range(GV):
+            st[g * GV + j] = (mm >> (end(GV - 1) - end(j))) & 0xFFFF
+    return st
+
+
+@pytest.mark.parametrize("k2", [2, 4, 6, 8, 10, 12, 14, 16])
+def test_state_unpack_matches_reference_lane_map(k2):
+    """Every lane's eight states from the emulated reference decode equal the oracle's eo_state, and the reference
+    dequant_kernel's placement of them equals eo_position, over random tiles."""
+    b = k2 // 2
+    for _ in range(20):
+        tile = RNG.integers(-32768, 32768, 16 * b).astype(np.int16)
+        words = _words(tile)
+        wa = np.array(words, dtype=np.uint32)
+        for lane in range(32):
+            st = _ref_decode_tile_states(words, k2, lane)
+            g, t = lane >> 2, lane & 3
+            for j in range(8):
+                p = 8 * lane + j
+                assert O.state(wa, k2, p) == st[j], (k2, lane, j)
+                q = j >> 1                                     # half2 v[q] = (st[2q], st[2q+1]), rows row, row + 1
+                assert O.position(p) == (2 * t + 8 * (q & 1) + (j & 1), g + 8 * (q >> 1)), (lane, j)
+
+
+@pytest.mark.parametrize("cb,k2", sorted(O.COMPILED))
+def test_dequant_matches_reference_kernel_emulation(cb, k2):
+    """O.dequant on a 2 x 3 tile matrix equals the emulated reference dequant_kernel: lane decode, codebook pairs,
+    out[row][col] / out[row + 1][col] stores."""
+    b = k2 // 2
+    tr = RNG.integers(-32768, 32768, (2, 3, 16 * b)).astype(np.int16)
+    table = O.codebook_table(cb)
+    ref = np.full((32, 48), 0xDEAD, dtype=np.uint16)
+    for kt in range(2):
+        for nt in range(3):
+            words = _words(tr[kt, nt])
+            for lane in range(32):
+                st = _ref_decode_tile_states(words, k2, lane)
+                g, t = lane >> 2, lane & 3
+                for q in range(4):
+                    col, row = nt * 16 + g + 8 * (q >> 1), kt * 16 + 2 * t + 8 * (q & 1)
+                    ref[row, col] = table[st[2 * q]]
+                    ref[row + 1, col] = table[st[2 * q + 1]]
+    assert np.array_equal(O.dequant(tr, k2, cb), ref)
+
+
 def test_dequant_rejects_unsupported():
     tr = np.zeros((1, 1, 16 * 5), dtype=np.int16)
     with pytest.raises(ValueError):

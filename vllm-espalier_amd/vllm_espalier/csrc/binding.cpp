@@ -445,6 +445,13 @@ void argmax(const at::Tensor& logits, at::Tensor ids, std::optional<at::Tensor> 
                     counters.has_value() ? counters->numel() : 0, cur_stream()));
 }
 
+// the device status word of the current GPU (esp_status; no reference counterpart), cleared after the read if asked
+int64_t status(bool clear) {
+    int32_t v = 0;
+    call(esp_status(&v, clear ? 1 : 0, cur_stream()));
+    return v;
+}
+
 PYBIND11_MODULE(espalier_ext, m) {
     m.def("had", &had);
     m.def("route_group", &route_group);
@@ -461,6 +468,7 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("down_combine", &down_combine);
     m.def("moe_gateup", &moe_gateup);
     m.def("dense_rmsnorm", &dense_rmsnorm);
+    m.def("status", &status, py::arg("clear") = false);
     m.def("route_group_rmsnorm", &route_group_rmsnorm);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);

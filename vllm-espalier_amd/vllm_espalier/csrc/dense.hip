@@ -43,6 +43,7 @@ struct DenseArgs {
     int* counters;
     int M, K, SK, NBT, fused, xs_stride, stage_bytes;
     int SQ, SR;              // K / 32 steps = SQ * SK + SR: split s has SQ + (s < SR) steps
+    int cnt_stride;          // ints between two column blocks' arrival counters (32: a 128-byte line each)
     int gather;              // the last workgroup loads the M * SK partials one a 32-lane half (shared memory holds them)
     // esp_dense_rmsnorm: the input rows are RMSNorm(h + d1 + d2) * nw (norm.hpp), made in the launch; workgroup (0, 0)
     // stores the residual h + d1 + d2 to nh_out. Rows of h, d1, d2 and nh_out are x_stride apart.
@@ -332,7 +333,8 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
     const DevBuf zb(a.Z);
     for (int r = wave * 2 + half; r < M; r += 2 * NW)
         zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
-    if (!arrive_last(a.counters + (size_t)nbg * CNT_STRIDE, a.SK, &last)) return;
+    int* const cnt_p = a.counters + (size_t)nbg * a.cnt_stride;
+    if (!arrive_last(cnt_p, a.SK, &last)) return;
     const size_t zsplit = (size_t)M * zrow;
     if (a.gather) {
         // every (row, split) partial in flight at once, one a 32-lane half, through shared memory (the k slots'
@@ -354,7 +356,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
             finish(v, l32, sv, S.scale);
             store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
         }
-        if (threadIdx.x == 0) store_dev(a.counters + (size_t)nbg * CNT_STRIDE, 0);
+        if (threadIdx.x == 0) store_dev(cnt_p, 0);
         return;
     }
     for (int r = wave * 2 + half; r < M; r += 2 * NW) {
@@ -378,7 +380,7 @@ __global__ __launch_bounds__(1024) void dense_kernel(DenseArgs a) {
         finish(v, l32, sv, S.scale);
         store4(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v);
     }
-    if (threadIdx.x == 0) store_dev(a.counters + (size_t)nbg * CNT_STRIDE, 0);  // every split of the block arrived
+    if (threadIdx.x == 0) store_dev(cnt_p, 0);  // every split of the block arrived
 }
 
 template <int KCB, int K2, int MG>
@@ -476,8 +478,11 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
         nbt += (int)(N / 128);
     }
     a.n = (int)n_shards;
-    ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= (int64_t)nbt * CNT_STRIDE),
-                "scratch too small: Z needs SK*M*N floats, counters 32 per 128 columns");
+    // the reference's contract (dense.cu:296): Z holds SK * M * N floats, counters at least 2 per 128 columns. The
+    // counters are spread as far apart as the buffer allows, up to one 128-byte line each (a caller sizing them
+    // 32 per 128 columns keeps arrivals on different counters off each other's line).
+    ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= 2 * (int64_t)nbt),
+                "scratch too small: Z needs SK*M*N floats, counters 2 per 128 columns");
     ESP_REQUIRE(SK * M * nbt * 128 <= (int64_t(1) << 30), "dense: the partials must fit in 4 GiB");
     const int64_t sq = (K / 32) / SK, sr = (K / 32) % SK;
     const int64_t steps_max = sq + (sr > 0);                  // the longest split
@@ -520,6 +525,7 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
     a.SQ = (int)sq;
     a.SR = (int)sr;
     a.NBT = nbt;
+    a.cnt_stride = SK == 1 ? 0 : (int)(counters_numel / nbt < CNT_STRIDE ? counters_numel / nbt : CNT_STRIDE);
     a.fused = fused;
     a.xs_stride = xs_stride;
     hipStream_t st = (hipStream_t)stream;

@@ -504,7 +504,16 @@ struct GroupedArgs {
     int act_mode;
     int* counters;                 // arrival counters CNT_STRIDE apart: zero on entry, left zero
     int stage_bytes, xs_stride;    // rotated rows in shared memory after the stages
+    int lo, hi;                    // the K2 range the launch's stages are sized for
 };
+
+// Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
+// they cannot run, which the host cannot check without reading the tables back. Read and cleared by esp_status.
+__device__ int g_status;
+
+__device__ __forceinline__ void raise_status(int bits) {
+    __hip_atomic_fetch_or(&g_status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The GEMM of one program. A rows: member m's row is abase + (by_member ? m : its slot row) * astride, holding k from
 // kbase, in shared memory (LDS) or global memory. dev: the partials go to Z with device-scope stores (another
@@ -804,10 +813,28 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     __syncthreads();
     if (nrows == 0) return;
     const int kr = a.K / a.SK, k0 = split * kr;
+    // An expert whose table entry has no kernel, or whose width lies outside the [lo, hi] the stages were sized for:
+    // no copy is issued (a wider expert would overrun the stage) and no GEMM runs; the program's partials become NaN,
+    // so every output that reads them is NaN, and the status word records why.
+    if (!supported(cb, k2) || k2 < a.lo || k2 > a.hi) {
+        if (threadIdx.x == 0) raise_status(supported(cb, k2) ? ESP_STATUS_WIDTH_RANGE : ESP_STATUS_NO_KERNEL);
+        float* Zm = a.Z + ((size_t)mat * a.SK + split) * a.P * a.N;
+        const float qn = __builtin_nanf("");
+        const float4 nan4 = make_float4(qn, qn, qn, qn);
+        for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+            float* zp = Zm + (size_t)rows_sh[m] * a.N + blockIdx.y * 128 + 4 * l32;
+            if (MODE == 1)
+                DevBuf(a.Z).store4(zp, nan4);
+            else
+                *reinterpret_cast<float4*>(zp) = nan4;
+        }
+        if constexpr (MODE == 0) return;
+    }
+    const bool runs = supported(cb, k2) && k2 >= a.lo && k2 <= a.hi;
     const uint16_t* abase = mat ? a.X1 : a.X0;
     int astride = a.K, kbase = 0;
     GateupScales sc{};
-    if constexpr (MODE == 1) {
+    if (MODE == 1 && runs) {
         // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory; the
         // epilogue's scales (the expert's, for this lane's 4 columns) ride along, for the workgroup that runs it
         issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), blockIdx.y * 8, stage);
@@ -825,9 +852,11 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
         abase = xs;
         astride = a.xs_stride;
         kbase = k0;
+    } else if (MODE == 1) {                                 // not run, but it may still be the last to arrive
+        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + blockIdx.y * 128 + 4 * l32);
     }
     const bool two = nrows > 16;
-    switch (cb * 32 + k2) {
+    switch (runs ? cb * 32 + k2 : -1) {
 #define ESP_GROUPED_CASE(CB_, K2_)                                                                            \
     case CB_ * 32 + K2_: {                                                                                    \
         constexpr int KCB = gemm_cb(CB_);                                                                     \
@@ -843,7 +872,7 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
         ESP_CASES(ESP_GROUPED_CASE)
 #undef ESP_GROUPED_CASE
         default:
-            break;                                          // no kernel: Z is left untouched (the host checks tables)
+            break;                                          // not run: the partials were set to NaN above
     }
     if constexpr (MODE == 1) {
         __shared__ int last;
@@ -1058,6 +1087,8 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.SK = (int)SK;
     a.maxm = (int)maxm;
     a.slots = (int)slots;
+    a.lo = (int)lo;
+    a.hi = (int)hi;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK));
     const size_t stage = (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;     // the widest expert's stages
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
@@ -1131,6 +1162,8 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
     a.limit = (float)limit;
     a.act_mode = (int)act_mode;
     a.counters = counters;
+    a.lo = (int)lo;
+    a.hi = (int)hi;
     const int64_t kr = K / SK;
     const size_t stage = (size_t)host_stage_words((int)hi, (int)kr) * 4;   // the widest expert's stages
     a.stage_bytes = (int)stage;
@@ -1216,4 +1249,22 @@ extern "C" int esp_down_combine2(const float* Z, const int32_t* pick, const void
                                  int64_t SK, int64_t slots, int64_t E, int64_t n_routed, void* stream) {
     return down_combine_any(Z, pick, svh_d, y, wts, out, out_dtype, out_shared, rows, P, D, SK, slots, E, n_routed,
                             stream);
+}
+
+extern "C" int esp_status(int32_t* status, int clear, void* stream) {
+    ESP_REQUIRE(status, "status: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    int v = 0;
+    if (hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(g_status), sizeof(int), 0, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "status: cannot read the device status word");
+    *status = v;
+    if (clear && v) {
+        const int zero = 0;
+        if (hipMemcpyToSymbolAsync(HIP_SYMBOL(g_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice, st) !=
+                hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return esp_host::fail(ESP_ERR_HIP, "status: cannot clear the device status word");
+    }
+    return esp_host::ok();
 }
