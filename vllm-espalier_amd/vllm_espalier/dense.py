@@ -1,25 +1,29 @@
-"""Dense trellis layers in one launch (csrc/dense.hip): every matrix of a vLLM layer, x in the model's dtype, output
-written into each matrix's columns, no casts or cat. Up to 32 rows (decode); above that ops.py windows them.
-(The surface of vllm_espalier/dense.py:1-103.)
+"""Dense trellis layers for decode: every matrix of one vLLM layer in as few esp_dense launches as the codes allow (the
+interface of vllm_espalier/dense.py: Dense, plan, scratch, MAX_ROWS).
 
-Each matrix keeps its own suh/svh. All matrices of one launch share K and codebook; a layer that mixes them runs one
-launch per group into the same output. The K split (`plan`) depends on the layer's shape alone, so a row's bits
-never depend on the batch.
+A vLLM layer fuses several checkpoint matrices (q/k/v, gate/up); each keeps its own suh/svh, so they are never
+concatenated into one trellis. A launch takes up to four of them that share the input width, the bit width and the
+codebook; it reads x once in the model's dtype and writes each matrix's columns of y in that dtype. Up to MAX_ROWS rows
+a launch; ops.py windows longer inputs.
+
+The K split of a launch (`plan`) is a function of the layer's shape alone, so the bits of a row never depend on the
+other rows of the batch.
 """
 from __future__ import annotations
 
+import itertools
 import os
+from dataclasses import dataclass
 
 import torch
 
-from .experts import KERNEL_CB, ext
 from ._env import env
+from .experts import KERNEL_CB, ext
 
 MAX_ROWS = 32
 COUNTER_STRIDE = 32          # ints between two 128-column blocks' arrival counters (one 128-byte line each)
+MAX_MATRICES = 4             # matrices one esp_dense launch takes
 ROT_SMEM = int(os.environ.get("ESPALIER_DENSE_ROTATION_SMEM", 64 * 1024))   # fuse the input rotation up to this much LDS
-_scratch: dict = {}
-_outgrown: list = []         # scratch a growth replaced: kept alive, since graphs captured before it still use it
 
 
 def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
@@ -46,24 +50,53 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
     return sk, w, 2
 
 
+class _SharedScratch:
+    """The split-K partials Z (fp32) and the unfused rotation's rows xh (fp16), one pair a device, shared by every
+    layer (layers run one after another). Sizes only grow, and only while layers are being built; a pair a growth
+    replaces stays allocated for good, because a graph captured before the growth still writes to it."""
+
+    def __init__(self):
+        self.current: dict = {}
+        self.retired: list = []
+
+    def reserve(self, device, z_floats: int, xh_halves: int):
+        have = self.current.get(device)
+        if have is not None and have[0].numel() >= z_floats and have[1].numel() >= xh_halves:
+            return have
+        if have is not None:
+            self.retired.append(have)
+            z_floats, xh_halves = max(z_floats, have[0].numel()), max(xh_halves, have[1].numel())
+        pair = (torch.empty(max(z_floats, 1), dtype=torch.float32, device=device),
+                torch.empty(max(xh_halves, 1), dtype=torch.float16, device=device))
+        self.current[device] = pair
+        return pair
+
+
+_SHARED = _SharedScratch()
+
+
 def scratch(device, z_floats: int, xh_halves: int):
-    """Shared scratch, grown while layers are prepared, never during a forward. A buffer that a growth replaces is
-    never freed: a graph captured before the growth keeps writing to the buffer it was captured with."""
-    s = _scratch.get(device)
-    if s is None or s[0].numel() < z_floats or s[1].numel() < xh_halves:
-        z = max(z_floats, s[0].numel() if s else 0, 1)
-        h = max(xh_halves, s[1].numel() if s else 0, 1)
-        if s is not None:
-            _outgrown.append(s)
-        s = (torch.empty(z, dtype=torch.float32, device=device), torch.empty(h, dtype=torch.half, device=device))
-        _scratch[device] = s
-    return s
+    """(Z, xh) of the device, grown to at least the given sizes."""
+    return _SHARED.reserve(device, z_floats, xh_halves)
 
 
-def _sms(dev) -> int:
-    if dev.type == "cuda" and torch.cuda.is_available():
-        return torch.cuda.get_device_properties(dev).multi_processor_count
+def _cu_count(device) -> int:
+    if device.type == "cuda" and torch.cuda.is_available():
+        return torch.cuda.get_device_properties(device).multi_processor_count
     return 256                                   # MI355X
+
+
+@dataclass(frozen=True)
+class Launch:
+    """One esp_dense launch: the matrices (indices into Dense.mats), their common half-bits and kernel codebook, the
+    columns they write, and the shape's plan."""
+    members: tuple
+    k2: int
+    cb: int
+    n: int
+    sk: int
+    w: int
+    pf: int
 
 
 class Dense:
@@ -71,70 +104,83 @@ class Dense:
 
     def __init__(self, mats, n_out: int | None = None):
         self.mats = list(mats)
-        m0 = self.mats[0]
-        self.K = m0.in_features
-        if any(m.in_features != self.K for m in self.mats):
-            raise ValueError("every matrix of a dense layer must share its input width")
-        self.groups = []                       # launches: (matrix indices, k2, kernel cb)
-        for i, m in enumerate(self.mats):
-            key = (2 * m.K, KERNEL_CB[m.cb])
-            if self.groups and (self.groups[-1][1], self.groups[-1][2]) == key and len(self.groups[-1][0]) < 4:
-                self.groups[-1][0].append(i)
-            else:
-                self.groups.append(([i], *key))
-        self.col0 = []
-        c = 0
-        for m in self.mats:
-            self.col0.append(c)
-            c += m.out_features
-        self.N = c
-        self.n_out = n_out or c
-        dev = m0.trellis.device
-        sms = _sms(dev)
-        self.plans, nbt_max, z = [], 0, 0
-        for idx, _, _ in self.groups:
-            n = sum(self.mats[i].out_features for i in idx)
-            p = plan(self.K, n, sms)
-            self.plans.append(p)
-            nbt_max = max(nbt_max, n // 128)
-            z = max(z, p[0] * MAX_ROWS * n)
-        self.counters = torch.zeros(COUNTER_STRIDE * nbt_max, dtype=torch.int32, device=dev)
-        scratch(dev, z, 4 * MAX_ROWS * self.K)
+        widths = {m.in_features for m in self.mats}
+        if len(widths) != 1:
+            raise ValueError(f"the matrices of a dense layer must share their input width, got {sorted(widths)}")
+        (self.K,) = widths
+        offsets = list(itertools.accumulate((m.out_features for m in self.mats), initial=0))
+        self.col0, self.N = offsets[:-1], offsets[-1]
+        self.n_out = n_out or self.N
+        device = self.mats[0].trellis.device
+        cus = _cu_count(device)
+        self.launches = []
+        for code, run in itertools.groupby(range(len(self.mats)), key=self._code):
+            run = list(run)
+            for i in range(0, len(run), MAX_MATRICES):
+                members = tuple(run[i:i + MAX_MATRICES])
+                n = sum(self.mats[j].out_features for j in members)
+                self.launches.append(Launch(members, *code, n, *plan(self.K, n, cus)))
+        blocks = max(l.n // 128 for l in self.launches)
+        self.counters = torch.zeros(COUNTER_STRIDE * blocks, dtype=torch.int32, device=device)
+        scratch(device, max(l.sk * MAX_ROWS * l.n for l in self.launches), 4 * MAX_ROWS * self.K)
+
+    def _code(self, i: int) -> tuple[int, int]:
+        m = self.mats[i]
+        return 2 * m.K, KERNEL_CB[m.cb]
+
+    @property
+    def groups(self) -> list:
+        """(matrix indices, k2, kernel codebook) of each launch."""
+        return [(list(l.members), l.k2, l.cb) for l in self.launches]
+
+    @property
+    def plans(self) -> list:
+        """(SK, W, PF) of each launch."""
+        return [(l.sk, l.w, l.pf) for l in self.launches]
+
+    @plans.setter
+    def plans(self, plans) -> None:
+        """Replace the launches' plans (the scratch must already be large enough for them)."""
+        if len(plans) != len(self.launches):
+            raise ValueError(f"{len(plans)} plans for {len(self.launches)} launches")
+        self.launches = [Launch(l.members, l.k2, l.cb, l.n, *p) for l, p in zip(self.launches, plans)]
 
     def forward(self, x, trellis=None, suh=None, svh=None, out=None):
-        """x [M, K] (M <= 32) -> [M, n_out] in x's dtype; trellis/suh/svh lists override the matrices' own tensors
-        (module buffers under torch.compile)."""
-        M = x.shape[0]
-        trellis = trellis or [m.trellis for m in self.mats]
-        suh = suh or [m.suh for m in self.mats]
-        svh = svh or [m.svh for m in self.mats]
-        y = out if out is not None else torch.empty((M, self.n_out), dtype=x.dtype, device=x.device)
+        """x [M, K] (M <= MAX_ROWS) -> [M, n_out] in x's dtype. trellis / suh / svh: lists that replace the matrices'
+        own tensors (the module buffers a compiled graph passes in)."""
+        codes = trellis or [m.trellis for m in self.mats]
+        pre = suh or [m.suh for m in self.mats]
+        post = svh or [m.svh for m in self.mats]
+        y = torch.empty((x.shape[0], self.n_out), dtype=x.dtype, device=x.device) if out is None else out
         if self.n_out > self.N:
-            y[:, self.N:].zero_()
-        z, xh = scratch(x.device, 0, 0)
+            y[:, self.N:].zero_()                     # padding columns (the LM head's vocabulary padding)
         if x.stride(-1) != 1:
             x = x.contiguous()
-        for (idx, k2, cb), (sk, w, pf) in zip(self.groups, self.plans):
-            ext().dense(x, [trellis[i] for i in idx], [suh[i] for i in idx], [svh[i] for i in idx],
-                        [self.col0[i] for i in idx], y, xh, z, self.counters, k2, cb, sk, w, pf, ROT_SMEM)
+        z, xh = scratch(x.device, 0, 0)
+        e = ext()
+        for l in self.launches:
+            pick = l.members
+            e.dense(x, [codes[i] for i in pick], [pre[i] for i in pick], [post[i] for i in pick],
+                    [self.col0[i] for i in pick], y, xh, z, self.counters, l.k2, l.cb, l.sk, l.w, l.pf, ROT_SMEM)
         return y
 
     def norm_fusable(self, M: int) -> bool:
-        """Whether forward_rmsnorm runs in one launch for M rows: one launch group, four waves a row, and the rotated
-        rows in the fused rotation's shared memory."""
-        if len(self.groups) != 1:
+        """Whether forward_rmsnorm runs in one launch for M rows: a single launch, four waves a row, and the rotated
+        rows within the fused rotation's shared memory."""
+        if len(self.launches) != 1:
             return False
-        sk, w, _ = self.plans[0]
-        steps = -(-(self.K // 32) // sk)
-        chunks = -(-(steps * 32 + 96) // 128)
-        return M <= w // 4 and self.K <= 8192 and M * chunks * 128 * 2 <= ROT_SMEM
+        l = self.launches[0]
+        steps = -(-(self.K // 32) // l.sk)
+        blocks = -(-(steps * 32 + 96) // 128)
+        return M <= l.w // 4 and self.K <= 8192 and M * blocks * 128 * 2 <= ROT_SMEM
 
     def forward_rmsnorm(self, h, d1, d2, norm_w, eps: float, h_out, out):
         """forward(RMSNorm(h + d1 + d2) * norm_w) with the residual h + d1 + d2 stored to h_out, the norm made inside
         the launch (bit-identical to add_rmsnorm then forward). h, d1, d2: [M, K] contiguous, the model's dtype."""
         z, _ = scratch(h.device, 0, 0)
-        (idx, k2, cb), (sk, w, pf) = self.groups[0], self.plans[0]
-        ext().dense_rmsnorm(h, d1, d2, norm_w, eps, h_out, [self.mats[i].trellis for i in idx],
-                            [self.mats[i].suh for i in idx], [self.mats[i].svh for i in idx],
-                            [self.col0[i] for i in idx], out, z, self.counters, k2, cb, sk, w, ROT_SMEM)
+        l = self.launches[0]
+        ms = [self.mats[i] for i in l.members]
+        ext().dense_rmsnorm(h, d1, d2, norm_w, eps, h_out, [m.trellis for m in ms], [m.suh for m in ms],
+                            [m.svh for m in ms], [self.col0[i] for i in l.members], out, z, self.counters, l.k2, l.cb,
+                            l.sk, l.w, ROT_SMEM)
         return out

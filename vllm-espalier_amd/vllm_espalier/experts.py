@@ -1,21 +1,23 @@
-"""Grouped routed experts: one MoE layer for up to ROWS tokens in six launches, whatever the experts' widths
-(the surface of vllm_espalier/experts.py:1-268, over the gfx950 kernels of csrc/):
+"""Routed and shared experts of one MoE layer through the grouped trellis kernels (the interface of
+vllm_espalier/experts.py: Layer, prepare, Scratch, scratch, route, routed, routed2, windows, dequant, ext).
 
-  group_shared / route_group   pick / weight tables with the shared expert as one more slot, then the grouping
-                               (distinct experts in id order, member rows in pick order), all on the device
-  rot_in                       H(x * suh) for gate and up of every slot, read straight from the model's bf16/fp16 x
-  grouped (mats=2)             gate and up of all distinct experts in one launch, W decoded in registers
-  gateup_epilogue              splits summed, H, * svh, SwiGLU in fp32, * suh_d, H -> the down input
-  grouped (mats=1)             down
-  down_combine2                splits summed, H, * svh_d, routing-weighted sum over the routed slots (slot order),
-                               and the gated shared slot, both written in the model's dtype
+One layer, up to Scratch.rows tokens, whatever the experts' widths, in six launches:
+  group_shared | route_group   the pick and weight tables with the shared expert as one more slot, then the grouping
+                               (distinct experts in id order, their member rows in pick order), all on the device
+  rot_in                       H(x * suh) of every slot for gate and up, from the model's bf16 / fp16 rows
+  grouped, 2 matrices          gate and up of every distinct expert in one launch, the weights decoded in registers
+  gateup_epilogue              splits summed, H, * svh, SwiGLU in fp32, * suh of down, H: the fp16 down input
+  grouped, 1 matrix            down
+  down_combine2                splits summed, H, * svh of down; the routing-weighted sum over the routed slots in slot
+                               order, and the gated shared slot, each in the model's dtype
+(Up to FUSED_ROWS tokens the rot_in / gate-up / epilogue trio is one launch, esp_moe_gateup, with the same bits.)
 
-Every sum runs in a fixed order, so a token's output never depends on the other tokens in the window, and nothing
-allocates, so HIP graphs capture it. The trellises are read in place through pointer tables; suh/svh are stacked per
-projection and each EspMatrix's suh/svh become views of the stacks.
+Sums run in a fixed order, so a token's output does not depend on the other tokens of its window, and nothing
+allocates, so a HIP graph can hold the whole layer. Trellises are read in place through device address tables; the
+matrices' suh / svh become rows of per-projection stacks.
 
-The extension (espalier_ext, csrc/binding.cpp over libespalier_hip.so) is built in-tree by csrc/build.py;
-ESPALIER_PREBUILT_EXTENSION points at a prebuilt espalier_ext .so instead.
+The extension (espalier_ext: csrc/binding.cpp over libespalier_hip.so) is built in-tree by csrc/build.py;
+ESPALIER_PREBUILT_EXTENSION names a prebuilt espalier_ext .so instead.
 """
 from __future__ import annotations
 
@@ -23,7 +25,7 @@ import importlib.machinery
 import importlib.util
 import math
 import os
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from functools import lru_cache
 from pathlib import Path
 
@@ -100,152 +102,214 @@ def tile_config(K: int, N: int, gateup: bool) -> tuple[int, int, int, int]:
     return 8, 4, sk, 2
 
 
-@dataclass
-class Layer:
-    """One layer's routed experts as the kernels read them."""
+_PROJECTIONS = ("gate", "up", "down")
 
-    ptr: tuple            # int64 [E] trellis pointers: gate, up, down
-    k2: tuple             # int32 [E] half-bits: gate, up, down
-    cb: tuple             # int32 [E] kernel codebook ids: gate, up, down
-    suh_g: torch.Tensor   # fp16 [E, D]
-    suh_u: torch.Tensor
-    svh_g: torch.Tensor   # fp16 [E, I]
-    svh_u: torch.Tensor
-    suh_d: torch.Tensor   # fp16 [E, I]
-    svh_d: torch.Tensor   # fp16 [E, D]
-    E: int                # matrices in the tables: routed experts, plus the shared expert at index E-1 if any
-    D: int
-    I: int
-    k2_gu: tuple          # (min, max) over gate and up
-    k2_d: tuple
-    shared_id: int = -1   # index of the shared expert in the tables, -1 without one
-    gate_w: torch.Tensor | None = None   # the shared expert's sigmoid-gate weight [D], the model's dtype
-    keep: list = field(default_factory=list, repr=False)
+
+@dataclass(frozen=True)
+class ExpertTable:
+    """One projection over a layer's expert matrices, as the grouped kernels read it: device tables indexed by
+    expert, and the range of half-bits the launch's shared-memory stages must hold."""
+    ptr: torch.Tensor        # int64 [E] trellis addresses
+    k2: torch.Tensor         # int32 [E] half-bits (2 * bits)
+    cb: torch.Tensor         # int32 [E] kernel codebook ids
+    k2_lo: int
+    k2_hi: int
+
+
+def _expert_table(mats, in_f: int, out_f: int, proj: str, device) -> ExpertTable:
+    addrs, half_bits, books = [], [], []
+    for e, m in enumerate(mats):
+        where = f"expert {e} {proj}"
+        if (m.in_features, m.out_features) != (in_f, out_f):
+            raise ValueError(f"{where}: {m.in_features}x{m.out_features}, expected {in_f}x{out_f}")
+        if m.cb not in KERNEL_CB:
+            raise NotImplementedError(f"{where}: grid code {m.cb} has no grouped kernel")
+        pair = (KERNEL_CB[m.cb], 2 * m.K)
+        if pair not in COMPILED:
+            raise NotImplementedError(f"{where}: no grouped kernel for codebook {pair[0]} at {m.K} bits")
+        if m.trellis.dtype != torch.int16 or not m.trellis.is_contiguous():
+            raise ValueError(f"{where}: the trellis must be contiguous int16")
+        addrs.append(m.trellis.data_ptr())
+        books.append(pair[0])
+        half_bits.append(pair[1])
+
+    def dev(values, dtype):
+        return torch.tensor(values, dtype=dtype, device=device)
+    return ExpertTable(dev(addrs, torch.int64), dev(half_bits, torch.int32), dev(books, torch.int32),
+                       min(half_bits), max(half_bits))
+
+
+def _stack_rows(mats, attr: str, width: int, device) -> torch.Tensor:
+    """fp16 [E, width] holding each matrix's `attr` (suh or svh) as a row; the matrix then refers to its row."""
+    stack = torch.empty((len(mats), width), dtype=torch.float16, device=device)
+    for row, m in zip(stack, mats):
+        row.copy_(getattr(m, attr).reshape(-1))
+        setattr(m, attr, row)
+    return stack
+
+
+class Layer:
+    """One layer's experts as the kernels read them: three ExpertTables (gate, up, down), the suh / svh stacks, and
+    the shared expert (if any) as the last entry, with its sigmoid-gate weight."""
+
+    def __init__(self, experts, shared=None, gate_w=None):
+        entries = [tuple(mats) for mats in experts]
+        if shared is not None:
+            entries.append(tuple(shared))
+        gate0 = entries[0][0]
+        self.E, self.D, self.I = len(entries), gate0.in_features, gate0.out_features
+        device = gate0.trellis.device
+        by_proj = list(zip(*entries))                        # [gate mats], [up mats], [down mats]
+        shapes = ((self.D, self.I), (self.D, self.I), (self.I, self.D))
+        self.tables = tuple(_expert_table(mats, k, n, name, device)
+                            for mats, (k, n), name in zip(by_proj, shapes, _PROJECTIONS))
+        gate_m, up_m, down_m = by_proj
+        self.suh_g = _stack_rows(gate_m, "suh", self.D, device)
+        self.suh_u = _stack_rows(up_m, "suh", self.D, device)
+        self.svh_g = _stack_rows(gate_m, "svh", self.I, device)
+        self.svh_u = _stack_rows(up_m, "svh", self.I, device)
+        self.suh_d = _stack_rows(down_m, "suh", self.I, device)
+        self.svh_d = _stack_rows(down_m, "svh", self.D, device)
+        self.shared_id = self.E - 1 if shared is not None else -1
+        self.gate_w = None if gate_w is None else gate_w.reshape(-1).contiguous()
+        self.keep = [m.trellis for mats in entries for m in mats]     # the tables hold raw addresses
+
+    @property
+    def ptr(self) -> tuple:
+        return tuple(t.ptr for t in self.tables)
+
+    @property
+    def k2(self) -> tuple:
+        return tuple(t.k2 for t in self.tables)
+
+    @property
+    def cb(self) -> tuple:
+        return tuple(t.cb for t in self.tables)
+
+    @property
+    def k2_gu(self) -> tuple:
+        """(lowest, highest) half-bits over gate and up: one launch runs both."""
+        g, u = self.tables[0], self.tables[1]
+        return min(g.k2_lo, u.k2_lo), max(g.k2_hi, u.k2_hi)
+
+    @property
+    def k2_d(self) -> tuple:
+        return self.tables[2].k2_lo, self.tables[2].k2_hi
 
 
 def prepare(experts, shared=None, gate_w=None) -> Layer:
     """experts: [(gate, up, down) EspMatrix] in expert order; shared: the shared expert's (gate, up, down), appended as
-    the last table entry, with gate_w its sigmoid-gate weight [D]. Rebinds each matrix's suh/svh to stack rows."""
-    if shared is not None:
-        experts = list(experts) + [tuple(shared)]
-    E = len(experts)
-    g0 = experts[0][0]
-    D, I = g0.in_features, g0.out_features
-    dev = g0.trellis.device
-
-    def tables(j, k, n):
-        ptrs, k2s, cbs = [], [], []
-        for e, mats in enumerate(experts):
-            m = mats[j]
-            if (m.in_features, m.out_features) != (k, n):
-                raise ValueError(f"expert {e} projection {j}: {m.in_features}x{m.out_features}, expected {k}x{n}")
-            if m.cb not in KERNEL_CB:
-                raise NotImplementedError(f"expert {e}: grid code {m.cb} has no grouped kernel")
-            k2, cb = 2 * m.K, KERNEL_CB[m.cb]
-            if (cb, k2) not in COMPILED:
-                raise NotImplementedError(f"expert {e}: no grouped instance for codebook {cb} at {m.K} bits")
-            if not (m.trellis.is_contiguous() and m.trellis.dtype == torch.int16):
-                raise ValueError(f"expert {e} projection {j}: trellis must be contiguous int16")
-            ptrs.append(m.trellis.data_ptr())
-            k2s.append(k2)
-            cbs.append(cb)
-        return (torch.tensor(ptrs, dtype=torch.int64, device=dev), torch.tensor(k2s, dtype=torch.int32, device=dev),
-                torch.tensor(cbs, dtype=torch.int32, device=dev), k2s)
-
-    gp, gk, gc, gks = tables(0, D, I)
-    up, uk, uc, uks = tables(1, D, I)
-    dp, dk, dc, dks = tables(2, I, D)
-
-    def stack(j, attr, n):
-        out = torch.empty((E, n), dtype=torch.float16, device=dev)
-        for e, mats in enumerate(experts):
-            out[e].copy_(getattr(mats[j], attr).reshape(-1))
-            setattr(mats[j], attr, out[e])
-        return out
-
-    return Layer((gp, up, dp), (gk, uk, dk), (gc, uc, dc), stack(0, "suh", D), stack(1, "suh", D),
-                 stack(0, "svh", I), stack(1, "svh", I), stack(2, "suh", I), stack(2, "svh", D), E, D, I,
-                 (min(gks + uks), max(gks + uks)), (min(dks), max(dks)),
-                 E - 1 if shared is not None else -1,
-                 None if gate_w is None else gate_w.reshape(-1).contiguous(),
-                 [m.trellis for mats in experts for m in mats])
+    the last table entry, with gate_w its sigmoid-gate weight [D]. Each matrix's suh / svh become rows of the layer's
+    stacks."""
+    return Layer(experts, shared, gate_w)
 
 
 class Scratch:
-    """Buffers for up to `rows` tokens of `slots` picks, shared by every layer of one shape (layers run in turn)."""
+    """Every buffer of the pipeline for up to `rows` tokens of `slots` picks each, shared by all layers of one shape
+    (layers run one after another, so no two use it at once)."""
 
     def __init__(self, E: int, D: int, I: int, rows: int, slots: int, device):
+        self.rows, self.slots, self.E = rows, slots, E
         self.cfg_gu = tile_config(D, I, True)
         self.cfg_d = tile_config(I, D, False)
         P = rows * slots
-        self.xg = torch.zeros((P, D), dtype=torch.float16, device=device)
-        self.xu = torch.zeros((P, D), dtype=torch.float16, device=device)
-        self.xd = torch.zeros((P, I), dtype=torch.float16, device=device)
-        self.z = torch.zeros((max(2 * self.cfg_gu[2] * I, self.cfg_d[2] * D) * P,), dtype=torch.float32,
-                             device=device)
-        self.y = torch.zeros((P, D), dtype=torch.float32, device=device)
-        self.route_counter = torch.zeros((1,), dtype=torch.int32, device=device)       # route_group's arrivals
-        self.logits = torch.zeros((rows * E,), dtype=torch.float32, device=device)     # route_group's logits
         maxu = min(P, E)
-        self.pick = torch.zeros((P,), dtype=torch.int32, device=device)      # with the shared slot
-        self.wts = torch.zeros((P,), dtype=torch.float32, device=device)
-        self.ids = torch.zeros((maxu,), dtype=torch.int32, device=device)
-        self.count = torch.zeros((1,), dtype=torch.int32, device=device)
-        self.members = torch.full((maxu * rows,), -1, dtype=torch.int32, device=device)
-        # arrival counters of the fused gate/up launch, one per (expert, 128 columns), 32 ints apart, zero between
-        # launches
-        self.counters = torch.zeros((maxu * (I // 128) * 32,), dtype=torch.int32, device=device)
-        self.rows, self.slots, self.E = rows, slots, E
+        partials = P * max(2 * self.cfg_gu[2] * I, self.cfg_d[2] * D)
+        f16, f32, i32 = torch.float16, torch.float32, torch.int32
+        layout = {
+            "xg": ((P, D), f16, 0), "xu": ((P, D), f16, 0),          # rotated gate / up inputs, a row a slot
+            "xd": ((P, I), f16, 0),                                   # the down input
+            "z": ((partials,), f32, 0),                               # K-split partial sums of either projection
+            "y": ((P, D), f32, 0),                                    # per-slot down outputs
+            "route_counter": ((1,), i32, 0),                          # route_group's arrival count
+            "logits": ((rows * E,), f32, 0),                          # route_group's logits
+            "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),            # with the shared slot
+            "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0),        # distinct experts, in id order
+            "members": ((maxu * rows,), i32, -1),                     # their member rows, -1 padded
+            # esp_moe_gateup's arrival counters, one a (expert, 128 columns) on its own 128-byte line
+            "counters": ((maxu * (I // 128) * 32,), i32, 0),
+        }
+        for name, (shape, dtype, fill) in layout.items():
+            setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
 
     def window(self, R: int):
+        """(ids, members [maxu, R]) views for a window of R tokens."""
         maxu = min(R * self.slots, self.E)
         return self.ids[:maxu], self.members[:maxu * R].view(maxu, R)
+
+    def fit(self, R: int, slots: int) -> None:
+        if R > self.rows or slots != self.slots:
+            raise ValueError(f"{R}x{slots} slots but the scratch holds {self.rows}x{self.slots}")
 
 
 _SCRATCH: dict = {}
 
 
 def scratch(layer: Layer, rows: int, slots: int, device) -> Scratch:
-    """slots counts the shared slot when the layer has one."""
+    """The Scratch shared by every layer of this layer's shape; slots counts the shared slot when there is one."""
     key = (layer.E, layer.D, layer.I, rows, slots, str(device))
-    if key not in _SCRATCH:
-        _SCRATCH[key] = Scratch(layer.E, layer.D, layer.I, rows, slots, device)
-    return _SCRATCH[key]
+    found = _SCRATCH.get(key)
+    if found is None:
+        found = _SCRATCH[key] = Scratch(layer.E, layer.D, layer.I, rows, slots, device)
+    return found
+
+
+def _gate_up(e, x, L: Layer, s: Scratch, R: int, P: int, slots: int, pick, ids, members) -> None:
+    """xd (the down input) of every valid slot: rot_in, the gate/up GEMM and its epilogue, fused into one launch for
+    up to FUSED_ROWS rows (the same arithmetic in the same order)."""
+    nt, w, sk, pf = s.cfg_gu
+    lo, hi = L.k2_gu
+    (tg, tu), (bg, bu), (cg, cu) = L.ptr[:2], L.k2[:2], L.cb[:2]
+    if FUSED and R <= FUSED_ROWS and (L.D // sk) % 128 == 0:
+        e.moe_gateup(x, x.stride(0), L.suh_g, L.suh_u, tg, tu, bg, bu, cg, cu, ids, s.count, members, s.z,
+                     s.counters, L.svh_g, L.svh_u, L.suh_d, s.xd, L.D, L.I, P, sk, slots, w, lo, hi, math.inf,
+                     ACT_F32)
+        return
+    e.rot_in(x, x.stride(0), pick, L.suh_g, L.suh_u, s.xg, s.xu, R, L.D, slots, L.E)
+    e.grouped(s.xg, s.xu, tg, tu, bg, bu, cg, cu, ids, s.count, members, s.z, 2, L.D, L.I, P, sk, slots, nt, w, pf,
+              lo, hi)
+    e.gateup_epilogue(s.z, pick, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
+
+
+def _down(e, L: Layer, s: Scratch, P: int, slots: int, ids, members) -> int:
+    """The down GEMM's partials into s.z; returns its K splits."""
+    nt, w, sk, pf = s.cfg_d
+    t, b, c = L.ptr[2], L.k2[2], L.cb[2]
+    e.grouped(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.z, 1, L.I, L.D, P, sk, slots, nt, w, pf,
+              *L.k2_d)
+    return sk
 
 
 def routed(x: torch.Tensor, pick: torch.Tensor, wts: torch.Tensor, L: Layer, s: Scratch,
            out: torch.Tensor | None = None) -> torch.Tensor:
-    """x [R, D] fp16/bf16, pick int32 [R, slots], wts fp32 [R, slots] -> fp32 [R, D], the weighted sum of the
-    routed experts' outputs (picks outside [0, E) are skipped)."""
+    """x [R, D] fp16/bf16, pick int32 [R, slots] (every slot a routed expert; picks outside [0, E) skipped), wts fp32
+    [R, slots] -> fp32 [R, D], the weighted sum of the experts' outputs (the legacy fp32 pipeline: group, rot_in,
+    grouped, gateup_epilogue, grouped, down_combine)."""
     e = ext()
     R, slots = pick.shape
-    D, I, E = L.D, L.I, L.E
+    s.fit(R, slots)
     P = R * slots
-    if R > s.rows or slots != s.slots:
-        raise ValueError(f"{R}x{slots} picks but the scratch holds {s.rows}x{s.slots}")
     ids, members = s.window(R)
-    e.group(pick, ids, s.count, members, R, slots, E)
-    e.rot_in(x, x.stride(0), pick, L.suh_g, L.suh_u, s.xg, s.xu, R, D, slots, E)
+    e.group(pick, ids, s.count, members, R, slots, L.E)
     nt, w, sk, pf = s.cfg_gu
+    e.rot_in(x, x.stride(0), pick, L.suh_g, L.suh_u, s.xg, s.xu, R, L.D, slots, L.E)
     e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
-              D, I, P, sk, slots, nt, w, pf, L.k2_gu[0], L.k2_gu[1])
-    e.gateup_epilogue(s.z, pick, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, I, sk, slots, E, math.inf, ACT_F32)
-    nt, w, sk, pf = s.cfg_d
-    e.grouped(s.xd, s.xd, L.ptr[2], L.ptr[2], L.k2[2], L.k2[2], L.cb[2], L.cb[2], ids, s.count, members, s.z, 1,
-              I, D, P, sk, slots, nt, w, pf, L.k2_d[0], L.k2_d[1])
-    if out is None:
-        out = torch.empty((R, D), dtype=torch.float32, device=x.device)
-    e.down_combine(s.z, pick, L.svh_d, s.y, wts, out, R, P, D, sk, slots, E)
+              L.D, L.I, P, sk, slots, nt, w, pf, *L.k2_gu)
+    e.gateup_epilogue(s.z, pick, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
+    sk_d = _down(e, L, s, P, slots, ids, members)
+    out = torch.empty((R, L.D), dtype=torch.float32, device=x.device) if out is None else out
+    e.down_combine(s.z, pick, L.svh_d, s.y, wts, out, R, P, L.D, sk_d, slots, L.E)
     return out
 
 
 def route(x: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
-    """Router logits (x @ gate.T, plus the shared gate), softmax / top-k / renormalisation and grouping in one launch
-    (csrc/moe.hip route_group), into the scratch's pick / wts / ids / count / members; then routed2(..., pick=None)."""
+    """The router GEMV (plus the shared gate), softmax / top-k / renormalisation and the grouping in one launch
+    (route_group) into the scratch's tables; routed2(..., pick=None) then runs the experts."""
     R = x.shape[0]
     ids, members = s.window(R)
-    ext().route_group(x, gate, L.gate_w, k, L.shared_id, s.logits, s.route_counter, s.pick[:R * s.slots],
-                      s.wts[:R * s.slots], ids, s.count, members)
+    P = R * s.slots
+    ext().route_group(x, gate, L.gate_w, k, L.shared_id, s.logits, s.route_counter, s.pick[:P], s.wts[:P], ids,
+                      s.count, members)
 
 
 def route_rmsnorm(h: torch.Tensor, d1: torch.Tensor | None, norm_w: torch.Tensor, eps: float, h_out: torch.Tensor,
@@ -254,67 +318,56 @@ def route_rmsnorm(h: torch.Tensor, d1: torch.Tensor | None, norm_w: torch.Tensor
     add_rmsnorm then route); stores a_out and the residual h + d1 to h_out. At most 4 rows."""
     R = h.shape[0]
     ids, members = s.window(R)
+    P = R * s.slots
     ext().route_group_rmsnorm(h, d1, norm_w, eps, h_out, a_out, gate, L.gate_w, k, L.shared_id, s.logits,
-                              s.route_counter, s.pick[:R * s.slots], s.wts[:R * s.slots], ids, s.count, members)
-
-
-def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: Scratch,
-            k: int | None = None, gate: torch.Tensor | None = None):
-    """routed2 over windows of s.rows tokens (prefill), each window as in decode; with gate (and pick=None) route()
-    first in each window. Returns (routed sum, shared expert output or None)."""
-    R = x.shape[0]
-    out = torch.empty_like(x)
-    sh = torch.empty_like(x) if L.shared_id >= 0 else None
-    for r in range(0, R, s.rows):
-        w = slice(r, r + s.rows)
-        if gate is not None:
-            route(x[w], gate, k, L, s)
-        routed2(x[w], None if pick is None else pick[w], None if wts is None else wts[w], L, s, out=out[w],
-                out_shared=None if sh is None else sh[w], k=k)
-    return out, sh
+                              s.route_counter, s.pick[:P], s.wts[:P], ids, s.count, members)
 
 
 def routed2(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: Scratch,
             out: torch.Tensor | None = None, out_shared: torch.Tensor | None = None, k: int | None = None):
-    """x [R, D] in the model's dtype, pick int32 [R, k] (vLLM's routed ids), wts fp32 [R, k]. Returns (routed sum,
-    shared expert output or None), both [R, D] in x's dtype; the shared output is gated by sigmoid(x . gate_w).
-    pick=None: the scratch already holds the grouping (route()), for k routed slots a row."""
+    """x [R, D] in the model's dtype; pick int32 [R, k] (vLLM's routed ids) and wts fp32 [R, k], or pick=None when
+    route() has already filled the scratch's tables for k routed slots a row. Returns (routed sum, the shared expert's
+    gated output or None), [R, D] in x's dtype."""
     e = ext()
-    R, k = (x.shape[0], k) if pick is None else pick.shape
-    D, I, E = L.D, L.I, L.E
-    slots = k + (L.shared_id >= 0)
+    R = x.shape[0]
+    k = k if pick is None else pick.shape[1]
+    has_shared = L.shared_id >= 0
+    slots = k + has_shared
+    s.fit(R, slots)
     P = R * slots
-    if R > s.rows or slots != s.slots:
-        raise ValueError(f"{R}x{slots} slots but the scratch holds {s.rows}x{s.slots}")
     ids, members = s.window(R)
-    pk, wt = s.pick[:P], s.wts[:P]
+    pick_p, wts_p = s.pick[:P], s.wts[:P]
     if pick is not None:
-        e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pk, wt, ids, s.count, members, R, k, E)
-    if out is None:
-        out = torch.empty((R, D), dtype=x.dtype, device=x.device)
-    if L.shared_id >= 0 and out_shared is None:
-        out_shared = torch.empty((R, D), dtype=x.dtype, device=x.device)
-    osh = out_shared if L.shared_id >= 0 else None
-    nt, w, sk, pf = s.cfg_gu
-    if FUSED and R <= FUSED_ROWS and (D // sk) % 128 == 0:
-        # rot_in + gate/up + its epilogue in one launch (the same arithmetic in the same order: the same bits)
-        e.moe_gateup(x, x.stride(0), L.suh_g, L.suh_u, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids,
-                     s.count, members, s.z, s.counters, L.svh_g, L.svh_u, L.suh_d, s.xd, D, I, P, sk, slots, w,
-                     L.k2_gu[0], L.k2_gu[1], math.inf, ACT_F32)
-    else:
-        e.rot_in(x, x.stride(0), pk, L.suh_g, L.suh_u, s.xg, s.xu, R, D, slots, E)
-        e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
-                  D, I, P, sk, slots, nt, w, pf, L.k2_gu[0], L.k2_gu[1])
-        e.gateup_epilogue(s.z, pk, L.svh_g, L.svh_u, L.suh_d, s.xd, R, P, I, sk, slots, E, math.inf, ACT_F32)
-    nt, w, sk, pf = s.cfg_d
-    e.grouped(s.xd, s.xd, L.ptr[2], L.ptr[2], L.k2[2], L.k2[2], L.cb[2], L.cb[2], ids, s.count, members, s.z, 1,
-              I, D, P, sk, slots, nt, w, pf, L.k2_d[0], L.k2_d[1])
-    e.down_combine2(s.z, pk, L.svh_d, s.y, wt, out, osh, R, P, D, sk, slots, E, k)
-    return out, osh
+        e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, R, k,
+                       L.E)
+    _gate_up(e, x, L, s, R, P, slots, pick_p, ids, members)
+    sk_d = _down(e, L, s, P, slots, ids, members)
+    out = torch.empty((R, L.D), dtype=x.dtype, device=x.device) if out is None else out
+    if has_shared and out_shared is None:
+        out_shared = torch.empty((R, L.D), dtype=x.dtype, device=x.device)
+    shared_out = out_shared if has_shared else None
+    e.down_combine2(s.z, pick_p, L.svh_d, s.y, wts_p, out, shared_out, R, P, L.D, sk_d, slots, L.E, k)
+    return out, shared_out
+
+
+def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: Scratch,
+            k: int | None = None, gate: torch.Tensor | None = None):
+    """routed2 over consecutive windows of s.rows tokens (prefill), each exactly as in decode; with gate (and
+    pick=None), route() first in each window. Returns (routed sum, shared output or None)."""
+    out = torch.empty_like(x)
+    shared_out = torch.empty_like(x) if L.shared_id >= 0 else None
+    for r0 in range(0, x.shape[0], s.rows):
+        rows = slice(r0, r0 + s.rows)
+        if gate is not None:
+            route(x[rows], gate, k, L, s)
+        routed2(x[rows], None if pick is None else pick[rows], None if wts is None else wts[rows], L, s,
+                out=out[rows], out_shared=None if shared_out is None else shared_out[rows], k=k)
+    return out, shared_out
 
 
 def dequant(trellis: torch.Tensor, K: int, grid: int) -> torch.Tensor:
-    """W [in, out] fp16 through the kernels' lane decode (bit-exact with the reference dequantisation)."""
-    out = torch.empty((trellis.shape[0] * 16, trellis.shape[1] * 16), dtype=torch.float16, device=trellis.device)
-    ext().dequant(trellis.contiguous(), out, 2 * K, KERNEL_CB[grid])
-    return out
+    """W [in, out] fp16 decoded by the kernels' lane decode (bit-exact with the reference dequantisation). K is the
+    bit width, grid the checkpoint grid code."""
+    w = torch.empty((16 * trellis.shape[0], 16 * trellis.shape[1]), dtype=torch.float16, device=trellis.device)
+    ext().dequant(trellis.contiguous(), w, 2 * K, KERNEL_CB[grid])
+    return w

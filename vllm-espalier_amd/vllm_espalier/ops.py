@@ -1,17 +1,17 @@
-"""torch custom ops around the extension, so torch.compile and HIP-graph capture see opaque calls
-(the surface of vllm_espalier/ops.py:1-87).
+"""The plugin's torch custom ops (the interface of vllm_espalier/ops.py): opaque to torch.compile and safe under
+HIP-graph capture, since nothing in them allocates from the host's point of view beyond the output.
 
-espalier::matmul(x, trellis, suh, svh, K, cb) = H(H(x * suh) @ W) * svh for one trellis matrix, x fp16 [m, in]
-contiguous -> fp16 [m, out]: the dense kernel for the one matrix, 32 rows a launch. The fake implementation only gives
-the shape.
+espalier::matmul(x, trellis, suh, svh, K, cb) -> fp16 [m, out]
+    one trellis matrix, x fp16 [m, in] contiguous; K is the bit width, cb the checkpoint grid code.
+espalier::dense(x, trellis[], suh[], svh[], key) -> [m, n_out] in x's dtype
+    every matrix of one vLLM layer, the Dense registered under `key` in DENSE_LAYERS.
 
-espalier::dense(x, trellis[], suh[], svh[], key) = every matrix of one vLLM layer, [m, in] in the model's dtype ->
-[m, out] in the same dtype: one dense launch (dense.Dense, registered under `key`) per 32 rows.
-
-Above 32 rows (prefill) the kernels run in 32-row windows (ESPALIER_PREFILL_MODE=chunk, default), so a row gets the
-bits it gets in decode. ESPALIER_PREFILL_MODE=gemm instead decodes each matrix's weight (dequant kernel), applies the
-Hadamards with the had kernel and multiplies with torch fp16 matmul (hipBLASLt), per matrix (the head always runs in
-windows: its weight would need ~1 GB).
+Rows beyond one launch (prefill) follow ESPALIER_PREFILL_MODE:
+    chunk  (default) the decode kernels over windows of MAX_ROWS rows, so a row gets exactly its decode bits;
+    gemm   each matrix decoded once (dequant kernel), both Hadamards by the had kernel, and an fp16 matmul
+           (hipBLASLt) between them. A layer of HUGE weights or more (the LM head) stays windowed: its decoded weight
+           would not fit beside the model.
+The fake implementations give only the output shapes.
 """
 from __future__ import annotations
 
@@ -21,71 +21,88 @@ import torch
 
 from ._env import env
 
+PREFILL_MODES = ("chunk", "gemm")
 PREFILL = env("ESPALIER_PREFILL_MODE", "chunk")
-if PREFILL not in ("chunk", "gemm"):
-    raise ValueError(f"ESPALIER_PREFILL_MODE={PREFILL}: chunk or gemm")
-_SINGLE: dict = {}           # trellis data_ptr -> dense.Dense for one matrix (<= 32 rows)
+if PREFILL not in PREFILL_MODES:
+    raise ValueError(f"ESPALIER_PREFILL_MODE={PREFILL}: expected one of {PREFILL_MODES}")
+
+DENSE_LAYERS: dict = {}       # key -> dense.Dense, filled by the linear method
+DENSE_KEYS = itertools.count()
+HUGE = 1 << 28                 # K * N at or above which a layer is never decoded whole
+_SINGLE: dict = {}             # trellis address -> a one-matrix dense.Dense for espalier::matmul
 
 
-def _windows(d, x, *args):
-    """d.forward over 32-row windows of x into one output."""
-    if x.shape[0] <= d.MAX_ROWS:
-        return d.forward(x, *args)
-    y = x.new_empty((x.shape[0], d.n_out))
-    for r in range(0, x.shape[0], d.MAX_ROWS):
-        d.forward(x[r:r + d.MAX_ROWS], *args, out=y[r:r + d.MAX_ROWS])
+class _Single:
+    """The fields dense.Dense reads from a matrix, for a matrix that reaches matmul as bare tensors."""
+
+    def __init__(self, trellis, suh, svh, bits: int, grid: int):
+        self.trellis, self.suh, self.svh = trellis, suh, svh
+        self.K, self.cb = bits, grid
+        self.in_features, self.out_features = suh.numel(), svh.numel()
+
+
+def windowed(layer, x: torch.Tensor, *tensors) -> torch.Tensor:
+    """layer.forward over consecutive windows of layer.MAX_ROWS rows of x, into one output."""
+    step = layer.MAX_ROWS
+    if x.shape[0] <= step:
+        return layer.forward(x, *tensors)
+    y = x.new_empty((x.shape[0], layer.n_out))
+    for r0 in range(0, x.shape[0], step):
+        rows = slice(r0, r0 + step)
+        layer.forward(x[rows], *tensors, out=y[rows])
     return y
 
 
-def _matmul(x, trellis, suh, svh, K: int, cb: int):
-    from . import dense, experts
-    if x.shape[0] <= dense.MAX_ROWS or PREFILL == "chunk":
-        d = _SINGLE.get(trellis.data_ptr())
-        if d is None:
-            from types import SimpleNamespace
-            m = SimpleNamespace(trellis=trellis, suh=suh, svh=svh, K=K, cb=cb, in_features=suh.numel(),
-                                out_features=svh.numel())
-            d = _SINGLE[trellis.data_ptr()] = dense.Dense([m])
-        return _windows(d, x)
+def _decoded_matmul(x: torch.Tensor, trellis, suh, svh, bits: int, grid: int) -> torch.Tensor:
+    """The gemm prefill path of one matrix: W decoded, x rotated by H(x * suh), the fp16 product, then H(.) * svh."""
+    from . import experts
     e = experts.ext()
-    w = experts.dequant(trellis, K, cb)
-    xh = torch.empty_like(x)
-    e.had(x, suh, None, xh)
-    y = xh @ w
+    w = experts.dequant(trellis, bits, grid)
+    rotated = torch.empty_like(x)
+    e.had(x, suh, None, rotated)
+    y = rotated @ w
     e.had(y, None, svh, y)
     return y
+
+
+def _single(trellis, suh, svh, bits: int, grid: int):
+    from . import dense
+    layer = _SINGLE.get(trellis.data_ptr())
+    if layer is None:
+        layer = _SINGLE[trellis.data_ptr()] = dense.Dense([_Single(trellis, suh, svh, bits, grid)])
+    return layer
 
 
 @torch.library.custom_op("espalier::matmul", mutates_args=())
 def matmul(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
            K: int, cb: int) -> torch.Tensor:
-    return _matmul(x, trellis, suh, svh, K, cb)
-
-
-DENSE_LAYERS: dict = {}       # key -> dense.Dense
-DENSE_KEYS = itertools.count()
-HUGE = 1 << 28                 # weights above which a layer never reconstructs (K * N; the head)
+    from .dense import MAX_ROWS
+    if PREFILL == "gemm" and x.shape[0] > MAX_ROWS:
+        return _decoded_matmul(x, trellis, suh, svh, K, cb)
+    return windowed(_single(trellis, suh, svh, K, cb), x)
 
 
 @torch.library.custom_op("espalier::dense", mutates_args=())
 def dense(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
           key: int) -> torch.Tensor:
-    d = DENSE_LAYERS[key]
-    if x.shape[0] <= d.MAX_ROWS or PREFILL == "chunk" or d.K * d.N >= HUGE:
-        return _windows(d, x.contiguous(), trellis, suh, svh)
-    xh = x.half().contiguous()
-    ys = [matmul(xh, t, s, v, m.K, m.cb) for t, s, v, m in zip(trellis, suh, svh, d.mats)]
-    y = (ys[0] if len(ys) == 1 else torch.cat(ys, dim=-1)).to(x.dtype)
-    if d.n_out > d.N:
-        y = torch.nn.functional.pad(y, (0, d.n_out - d.N))
+    layer = DENSE_LAYERS[key]
+    decode_whole = PREFILL == "gemm" and x.shape[0] > layer.MAX_ROWS and layer.K * layer.N < HUGE
+    if not decode_whole:
+        return windowed(layer, x.contiguous(), trellis, suh, svh)
+    x16 = x.to(torch.float16).contiguous()
+    parts = [matmul(x16, t, s, v, m.K, m.cb) for t, s, v, m in zip(trellis, suh, svh, layer.mats)]
+    y = torch.cat(parts, dim=-1) if len(parts) > 1 else parts[0]
+    y = y.to(x.dtype)
+    if layer.n_out > layer.N:
+        y = torch.nn.functional.pad(y, (0, layer.n_out - layer.N))
     return y
 
 
-@dense.register_fake
-def _(x, trellis, suh, svh, key):
-    return x.new_empty((x.shape[0], DENSE_LAYERS[key].n_out))
-
-
 @matmul.register_fake
-def _(x, trellis, suh, svh, K, cb):
-    return x.new_empty((x.shape[0], svh.shape[0]), dtype=torch.half)
+def _matmul_shape(x, trellis, suh, svh, K, cb):
+    return x.new_empty((x.shape[0], svh.shape[0]), dtype=torch.float16)
+
+
+@dense.register_fake
+def _dense_shape(x, trellis, suh, svh, key):
+    return x.new_empty((x.shape[0], DENSE_LAYERS[key].n_out))
