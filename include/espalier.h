@@ -176,6 +176,20 @@ int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, d
                             int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu,
                             int32_t* ucount, int32_t* members, int64_t maxm, void* stream);
 
+/* esp_dense without caller scratch, for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference. Arguments and results as esp_dense (the
+ * same kernels, the same bits); the arrival counters, the split-K partials Z and the unfused rotation's rows live in a
+ * 16 MiB device array of the library, one per GPU, held until the process ends. A launch needing more than that
+ * (64 KiB of counters, then SK * M * sum(n_cols) * 4 bytes of partials rounded to 256, then n_shards * M * K * 2 bytes
+ * when the rotation is not fused) fails with ESP_ERR_ARG. Nothing is allocated: the array's address is looked up,
+ * and its counters cleared by a kernel on `stream`, on a device's first call. Calls on one GPU share the array, so
+ * calls that overlap in time (on different streams, or from different threads) race. */
+int esp_dense_noalloc(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                      const void* const* trellis, const void* const* suh, const void* const* svh,
+                      const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                      int64_t y_cols, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF, int64_t rot_smem,
+                      void* stream);
+
 /* ---- Decode-step glue (csrc/step.hip). No counterpart in the reference extension: in a served model vLLM does
  * these (VocabParallelEmbedding, fused_add_rms_norm, the greedy sampler). They let the synthetic decoder step run as
  * one HIP graph whose next token stays on the device. ---- */

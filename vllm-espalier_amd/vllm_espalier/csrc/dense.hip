@@ -19,6 +19,8 @@
 #include "norm.hpp"
 #include "../../../include/espalier.h"
 
+#include <mutex>
+
 namespace esp {
 
 constexpr int MAX_SHARDS = 4;
@@ -584,4 +586,97 @@ extern "C" int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, 
     const DenseNorm nrm{h, d1, d2, norm_w, h_out, eps};
     return dense_impl(h, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
                       y_cols, nullptr, 0, Z, z_numel, counters, counters_numel, k2, cb, SK, W, rot_smem, &nrm, stream);
+}
+
+// ======================================================================================================================
+// esp_dense_noalloc: esp_dense with its scratch (arrival counters, split-K partials, unfused rotation rows) in a
+// file-scope device array instead of caller buffers, for callers that cannot allocate. Layout of the array:
+//   [0, NOALLOC_COUNTER_BYTES)       arrival counters, one a 128-column block, as far apart as fit (up to 32 ints)
+//   [NOALLOC_COUNTER_BYTES, ...)     Z, SK * M * sum(n_cols) floats, then xh (n_shards * M * K halves) if unfused
+// The counters start zero (cleared once per device when the array is first used) and every launch leaves the ones
+// it used zero, so no call needs to clear them. Calls overlapping on one GPU share the array and race.
+// ======================================================================================================================
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
+constexpr size_t NOALLOC_COUNTER_BYTES = size_t(64) << 10;
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];     // the array's device address, per device
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The array's address on the current device: looked up (and its counter region cleared, by a kernel on `stream`)
+// the first time the device uses it.
+int noalloc_scratch(hipStream_t stream, unsigned char** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return esp_host::fail(ESP_ERR_HIP, "dense_noalloc: no current device");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return esp_host::fail(ESP_ERR_HIP, "dense_noalloc: cannot resolve the scratch array: %s",
+                                  hipGetErrorString(e));
+        const int words = (int)(NOALLOC_COUNTER_BYTES / 4);
+        zero_words_kernel<<<(unsigned)((words + 255) / 256), 256, 0, stream>>>(static_cast<uint32_t*>(p), words);
+        const int rc = esp_host::launch_check("dense_noalloc: counter clear");
+        if (rc) return rc;
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = static_cast<unsigned char*>(g_noalloc_ptr[dev]);
+    return ESP_OK;
+}
+}  // namespace
+
+extern "C" int esp_dense_noalloc(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K,
+                                 int64_t n_shards, const void* const* trellis, const void* const* suh,
+                                 const void* const* svh, const int64_t* n_cols, const int64_t* col0, void* y,
+                                 int y_dtype, int64_t y_stride, int64_t y_cols, int64_t k2, int64_t cb, int64_t SK,
+                                 int64_t W, int64_t PF, int64_t rot_smem, void* stream) {
+    (void)PF;
+    ESP_REQUIRE(x && n_cols, "dense_noalloc: null x / n_cols");
+    ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "1 to 4 matrices a launch");
+    ESP_REQUIRE(M >= 1 && M <= 32 && K > 0 && K % 128 == 0 && SK >= 1 && SK <= K / 32, "dense_noalloc: shape");
+    int64_t nbt = 0;
+    for (int64_t s = 0; s < n_shards; ++s) {
+        ESP_REQUIRE(n_cols[s] > 0 && n_cols[s] % 128 == 0, "matrix shape");
+        nbt += n_cols[s] / 128;
+    }
+    // what the launch needs of the array: the counters (at least 2 ints a block, the esp_dense minimum), Z, and xh
+    // for the unfused rotation (esp_dense's fusion test, repeated here to size it)
+    const int64_t counters_numel = (int64_t)(NOALLOC_COUNTER_BYTES / 4);
+    ESP_REQUIRE(SK == 1 || 2 * nbt <= counters_numel,
+                "dense_noalloc: %lld column blocks need more arrival counters than the scratch array holds (%lld)",
+                (long long)nbt, (long long)counters_numel);
+    const int64_t z_numel = SK > 1 ? SK * M * nbt * 128 : 0;
+    const int64_t sq = (K / 32) / SK, sr = (K / 32) % SK;
+    const int64_t steps_max = sq + (sr > 0);
+    const bool aligned = sr == 0 && sq % 4 == 0;
+    const int64_t chunks_max = aligned ? steps_max / 4 : (steps_max * 32 + 96 + 127) / 128;
+    const bool fused = M * chunks_max * 128 * 2 <= rot_smem;
+    const int64_t xh_numel = fused ? 0 : n_shards * M * K;
+    const size_t z_bytes = ((size_t)z_numel * 4 + 255) / 256 * 256;
+    const size_t need = NOALLOC_COUNTER_BYTES + z_bytes + (size_t)xh_numel * 2;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return esp_host::fail(ESP_ERR_ARG,
+                              "dense_noalloc: this launch needs %zu bytes of scratch, the array holds %zu "
+                              "(use esp_dense with caller buffers)",
+                              need, NOALLOC_SCRATCH_BYTES);
+    hipStream_t st = (hipStream_t)stream;
+    unsigned char* base = nullptr;
+    const int rc = noalloc_scratch(st, &base);
+    if (rc) return rc;
+    int32_t* counters = reinterpret_cast<int32_t*>(base);
+    float* Z = reinterpret_cast<float*>(base + NOALLOC_COUNTER_BYTES);
+    void* xh = base + NOALLOC_COUNTER_BYTES + z_bytes;
+    return dense_impl(x, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
+                      y_cols, fused ? nullptr : xh, xh_numel, SK > 1 ? Z : nullptr, z_numel, counters,
+                      counters_numel, k2, cb, SK, W, rot_smem, nullptr, stream);
 }
