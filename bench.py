@@ -32,11 +32,34 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
-# HBM bytes a qkv launch moves at batch 1, from the two rocprofv3 --pmc passes over `bench.py --traffic-probe` (the
-# summary under profiles/): FETCH_SIZE 2788.4 KiB x 2.000 + WRITE_SIZE 138.8 KiB x 1.000, the factors being what the
-# counters read for a 256 MiB copy. Re-measured whenever the dense kernel changes.
-QKV_TRAFFIC_BYTES = 5852147
 COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
+CSRC = REPO / "vllm-espalier_amd" / "vllm_espalier" / "csrc"
+# HBM bytes a qkv launch moves at batch 1, written by `bench.py --traffic-record` from the two rocprofv3 --pmc passes
+# (FETCH_SIZE, then WRITE_SIZE) over `bench.py --traffic-probe`, each scaled by what the counter reads for a plain
+# copy of known size. The record names the hash of the kernel sources it was measured on; the bench reports its
+# traffic only while the sources still hash the same, and null otherwise.
+TRAFFIC_RECORD = REPO / "profiles" / "dense_qkv_batch1_traffic.json"
+ROOFLINE_KERNEL = "dense_kernel<23, 8, 1>"
+
+
+def kernel_sources_sha() -> str:
+    """sha256 of the sources the dense kernel is compiled from."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in ("dense.hip", "common.hpp", "trellis.hpp", "gemm.hpp", "norm.hpp"):
+        h.update(name.encode())
+        h.update((CSRC / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def recorded_traffic():
+    """(bytes per qkv launch, note): the record's traffic if it was measured on these kernel sources, else None."""
+    if not TRAFFIC_RECORD.exists():
+        return None, "no traffic record"
+    rec = json.loads(TRAFFIC_RECORD.read_text())
+    if rec.get("sources_sha") != kernel_sources_sha():
+        return None, f"record measured on other kernel sources ({rec.get('sources_sha')}); unmeasured for this build"
+    return rec["bytes"], f"rocprofv3 FETCH_SIZE x {rec['fetch_factor']:.3f} + WRITE_SIZE x {rec['write_factor']:.3f}"
 
 
 def log(msg: str) -> None:
@@ -129,39 +152,47 @@ def moe_layer(gen, dev, E=256, D=2048, I=512):
     return L, experts, shared, router
 
 
-def bench_moe(dev, steps: int, layers: int, rows=(1, 4, 32)):
+def bench_moe(dev, steps: int, layers: int = 8, passes: int = 16, rows=(1, 4, 32)):
+    """Config 4 (route_group + the six-launch MoE layer) and config 3 (route_group alone). A replay runs `passes`
+    passes over `layers` distinct 256-expert layers (1.6 GB of expert weights), each (pass, layer) with its own input
+    rows, so the experts picked change from one call to the next and a replay reads well over 1 GiB of picked-expert
+    bytes at one token (the 256 MB MALL cannot serve them from one replay to the next). Algorithmic bytes: trellis +
+    suh + svh of every distinct expert a call picks, plus the shared expert, summed over the calls."""
     import torch
     from vllm_espalier import experts as G, workloads as WL
     gen = torch.Generator(device=dev).manual_seed(4)
     stack = [moe_layer(gen, dev) for _ in range(layers)]
+    calls = [(p, l) for p in range(passes) for l in range(layers)]
     res = {}
     for T in rows:
         xg = torch.Generator(device=dev).manual_seed(40 + T)
-        xs = [torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16) for _ in stack]
+        xs = {c: torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16) for c in calls}
         s = G.scratch(stack[0][0], 32, 9, dev)
-        outs = [(torch.empty((T, 2048), dtype=torch.bfloat16, device=dev),
-                 torch.empty((T, 2048), dtype=torch.bfloat16, device=dev)) for _ in stack]
-        # the experts each layer picks, for its algorithmic bytes
+        outs = (torch.empty((T, 2048), dtype=torch.bfloat16, device=dev),
+                torch.empty((T, 2048), dtype=torch.bfloat16, device=dev))
         nbytes = 0
-        for (L, experts, shared, router), x in zip(stack, xs):
-            G.route(x, router, 8, L, s)
+        for c in calls:                       # the experts each call picks, for its algorithmic bytes
+            L, experts, shared, router = stack[c[1]]
+            G.route(xs[c], router, 8, L, s)
             torch.cuda.synchronize()
-            cnt = int(s.count.item())
-            ids = s.ids[:cnt].tolist()
+            ids = s.ids[:int(s.count.item())].tolist()
             nbytes += sum(WL.nbytes(experts[e]) if e < 256 else WL.nbytes(shared) for e in ids)
 
         def fn():
-            for (L, experts, shared, router), x, (o, sh) in zip(stack, xs, outs):
-                G.route(x, router, 8, L, s)
-                G.routed2(x, None, None, L, s, out=o, out_shared=sh, k=8)
+            for c in calls:
+                L, experts, shared, router = stack[c[1]]
+                G.route(xs[c], router, 8, L, s)
+                G.routed2(xs[c], None, None, L, s, out=outs[0], out_shared=outs[1], k=8)
         g = graph_of(fn)
         ms = time_graph(g, steps)
-        us = ms * 1000 / len(stack)
-        gbs = nbytes / len(stack) / (us * 1e-6) / 1e9
-        res[str(T)] = {"us_per_layer": round(us, 2), "bytes_per_layer": nbytes // len(stack), "GBps": round(gbs, 1),
-                       "pct_peak": round(100 * gbs / PEAK_GBS, 1)}
-        log(f"moe T={T}: {us:.2f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak)")
-    # the router alone (config 3)
+        del g
+        us = ms * 1000 / len(calls)
+        gbs = nbytes / len(calls) / (us * 1e-6) / 1e9
+        res[str(T)] = {"us_per_layer": round(us, 2), "bytes_per_layer": nbytes // len(calls), "GBps": round(gbs, 1),
+                       "pct_peak": round(100 * gbs / PEAK_GBS, 1), "picked_bytes_per_replay": nbytes}
+        log(f"moe T={T}: {us:.2f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak), "
+            f"{nbytes / 2**30:.2f} GiB of picked experts a replay")
+    # the router alone (config 3): its 1 MiB bf16 weight a layer stays in the MALL (8 layers), so this is warm
     rt = {}
     for T in (1, 32):
         xg = torch.Generator(device=dev).manual_seed(70 + T)
@@ -172,7 +203,7 @@ def bench_moe(dev, steps: int, layers: int, rows=(1, 4, 32)):
             for (L, experts, shared, router), x in zip(stack, xs):
                 G.route(x, router, 8, L, s)
         ms = time_graph(graph_of(fr), steps)
-        rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2)}
+        rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2), "weights": "MALL-warm"}
         log(f"route_group T={T}: {ms * 1000 / len(stack):.2f} us")
     del stack
     torch.cuda.empty_cache()
@@ -232,13 +263,26 @@ def bench_decoder(dev, steps: int, warmup: int, layers: int = 40, prefill_tokens
 # ---------------------------------------------------------------------------------------------------------------
 # CPU baseline: the reference's CPU path (dequantisation + torch matmul) on this host
 # ---------------------------------------------------------------------------------------------------------------
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(block, reps: int):
     import numpy as np
     import torch
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle as O            # the C restatement of the reference dequantisation (cpu_baseline leg only)
     from vllm_espalier import experts as G
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    affinity = len(os.sched_getaffinity(0))
+    # the job's CPU share: OMP_NUM_THREADS where the host sets it (16 for one GPU on the MI355X boxes), else every
+    # core of the affinity mask
+    cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
     torch.set_num_threads(cores)
     H = torch.from_numpy(O.sylvester() / np.sqrt(128.0)).float()
     mats = [[(m.trellis.cpu().numpy(), 2 * m.K, G.KERNEL_CB[m.cb], m.suh.float().cpu(), m.svh.float().cpu())
@@ -261,7 +305,7 @@ def cpu_baseline(block, reps: int):
         layer()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    return med, cores
+    return med, cores, affinity
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -292,6 +336,117 @@ def traffic_probe(dev) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f"traffic probe: {copies} qkv launches x 2 at 1 row, x 1 at 32 rows, copy of {CALIB_BYTES} B x 2")
+
+
+def _counter_avgs(d: str, counter: str) -> dict:
+    """Average per-dispatch value of `counter` by (kernel name with template arguments, grid size) in a rocprofv3
+    csv directory."""
+    import csv
+    from collections import defaultdict
+    f = next(Path(d).rglob("*counter_collection.csv"))
+    acc = defaultdict(list)
+    for r in csv.DictReader(open(f)):
+        if r["Counter_Name"] == counter:
+            grid = r.get("Grid_Size") or r.get("Grid_Size_X", "?")
+            acc[(r["Kernel_Name"].replace("void ", "").split("(")[0], grid)].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def traffic_record(fetch_dir: str, write_dir: str) -> dict:
+    """The traffic record from the FETCH_SIZE and WRITE_SIZE passes over --traffic-probe: the qkv launch's KiB a
+    dispatch, each scaled by what the counter reads for the probe's copy of CALIB_BYTES (it reads and writes them;
+    the copy is the copy kernel dispatch of the largest grid)."""
+    fetch, write = _counter_avgs(fetch_dir, "FETCH_SIZE"), _counter_avgs(write_dir, "WRITE_SIZE")
+    kern = next(k for k in fetch if k[0].endswith(ROOFLINE_KERNEL))
+    copy = max((k for k in fetch if "copyBuffer" in k[0]), key=lambda k: int(k[1]) if k[1].isdigit() else 0)
+    kib = CALIB_BYTES / 1024
+    ff, wf = kib / fetch[copy], kib / write[copy]
+    rec = {"kernel": kern[0], "grid": kern[1], "copy_grid": copy[1], "fetch_kib": round(fetch[kern], 1), "write_kib": round(write[kern], 1),
+           "copy_fetch_kib": round(fetch[copy], 1), "copy_write_kib": round(write[copy], 1),
+           "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
+           "bytes": int(round((fetch[kern] * ff + write[kern] * wf) * 1024)), "sources_sha": kernel_sources_sha()}
+    return rec
+
+
+def counter_probe(dev) -> None:
+    """The workload of the shader-counter passes over the expert kernels and the LM head: 8 cold 256-expert layers
+    at 1 token (route_group, the fused gate/up launch, the grouped down launch, down_combine2) and at 32 tokens
+    (route_group, rot_in, the grouped gate/up launch, its epilogue, the grouped down launch, down_combine2), one
+    replay each, then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row."""
+    import torch
+    from vllm_espalier import dense as D, experts as G, workloads as WL
+    gen = torch.Generator(device=dev).manual_seed(4)
+    stack = [moe_layer(gen, dev) for _ in range(8)]
+    for T in (1, 32):
+        xs = [torch.randn((T, 2048), device=dev).to(torch.bfloat16) for _ in stack]
+        s = G.scratch(stack[0][0], 32, 9, dev)
+        o = (torch.empty((T, 2048), dtype=torch.bfloat16, device=dev), torch.empty((T, 2048), dtype=torch.bfloat16,
+                                                                                   device=dev))
+
+        def fn():
+            for (L, experts, shared, router), x in zip(stack, xs):
+                G.route(x, router, 8, L, s)
+                G.routed2(x, None, None, L, s, out=o[0], out_shared=o[1], k=8)
+        graph_of(fn).replay()
+    del stack
+    heads = [D.Dense([WL.matrix(2048, 151936, 6, "mcg", gen, dev)]) for _ in range(2)]
+    x = torch.randn((1, 2048), device=dev).to(torch.bfloat16)
+    y = torch.empty((1, 151936), dtype=torch.bfloat16, device=dev)
+    graph_of(lambda: [h.forward(x, out=y) for h in heads]).replay()
+    torch.cuda.synchronize()
+    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# ceilings (--probes): launch floor, streaming read rate, VALU issue rates, from libespalier_probe.so
+# ---------------------------------------------------------------------------------------------------------------
+VALU_OPS = ["v_add_u32", "v_mul_lo_u32", "v_bfe_u32", "v_perm_b32", "v_fma_mix_f32", "v_pk_add_f16",
+            "v_add_f16 (SDWA)"]
+
+
+def probes(dev) -> dict:
+    """The device ceilings DESIGN.md's kernel notes refer to, measured here: (1) the launch floor, an empty kernel of
+    256 workgroups, as us a launch in a graph of 1000; (2) the streaming read rate of a 2 GiB buffer (16-byte
+    nontemporal loads, 8 workgroups of 256 threads a CU); (3) each decode instruction's issue rate, 8 independent
+    chains a lane, one and four waves a SIMD, as lane operations a CU a clock (at the reported peak clock)."""
+    import ctypes
+    import torch
+    L = ctypes.CDLL(str(REPO / "vllm-espalier_amd" / "vllm_espalier" / "libespalier_probe.so"))
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    L.esp_probe_empty.argtypes = [I64, P]
+    L.esp_probe_read.argtypes = [P, I64, P, I64, P]
+    L.esp_probe_valu.argtypes = [ctypes.c_int, ctypes.c_int, I64, ctypes.c_int, P, P]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    khz = L.esp_probe_clock_khz()
+    out = {"cus": cus, "clock_mhz": khz / 1000}
+
+    def stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    n = 1000
+    g = graph_of(lambda: [L.esp_probe_empty(256, stream()) for _ in range(n)])
+    out["launch_floor_us"] = round(time_graph(g, 5) * 1000 / n, 3)
+    del g
+    nbytes = 2 << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    g = graph_of(lambda: L.esp_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), 8 * cus, stream()))
+    ms = time_graph(g, 10)
+    out["read_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del g, buf
+    rates = {}
+    iters = 20000
+    for op, name in enumerate(VALU_OPS):
+        for waves_per_simd in (1, 4):
+            g = graph_of(lambda: L.esp_probe_valu(op, iters, cus, 4 * waves_per_simd, sink.data_ptr(), stream()))
+            ms = time_graph(g, 5)
+            lane_ops = cus * 4 * waves_per_simd * 64 * 8 * iters
+            rates[f"{name} @{waves_per_simd}w"] = round(lane_ops / (ms * 1e-3) / (cus * khz * 1e3), 1)
+            del g
+    out["valu_lane_ops_per_cu_clk"] = rates
+    for k, v in out.items():
+        log(f"probe {k}: {v}")
+    return out
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -339,13 +494,15 @@ def rocprof_summary(d: str, top: int = 30) -> str:
     if pmc is not None:
         groups = defaultdict(list)
         for r in csv.DictReader(open(pmc)):
+            if "esp::" not in r["Kernel_Name"] and "copyBuffer" not in r["Kernel_Name"]:
+                continue
             n = r["Kernel_Name"].replace("void ", "").split("(")[0]
             shape = r.get("Grid_Size") or f"{r.get('Grid_Size_X', '?')}x{r.get('Grid_Size_Y', '?')}x{r.get('Grid_Size_Z', '?')}"
             groups[(n[:80], shape, r["Counter_Name"])].append(float(r["Counter_Value"]))
-        items = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
+        items = sorted(groups.items(), key=lambda kv: (kv[0][0], kv[0][1], kv[0][2]))
         out += ["Counters (counter_collection.csv), per dispatch, grouped by kernel, grid size (threads) and counter:", "",
                 "| kernel | grid | counter | dispatches | average | min | max |", "|---|---|---|---:|---:|---:|---:|"]
-        for (n, shape, c), v in items[:top]:
+        for (n, shape, c), v in items[:8 * top]:
             out.append(f"| `{n}` | {shape} | {c} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
         out.append("")
     return "\n".join(out)
@@ -365,9 +522,20 @@ def main() -> int:
                     "directory and exit (no GPU work)")
     ap.add_argument("--traffic-probe", action="store_true", help="run only the workload of the FETCH_SIZE / "
                     "WRITE_SIZE counter passes (the roofline graph and a calibration copy) and exit")
+    ap.add_argument("--traffic-record", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), help="write the traffic record "
+                    f"({TRAFFIC_RECORD.relative_to(REPO)}) from the two rocprofv3 csv directories and exit")
+    ap.add_argument("--counter-probe", action="store_true", help="run only the workload of the shader-counter "
+                    "passes over the expert kernels and the LM head, and exit")
+    ap.add_argument("--probes", action="store_true", help="measure the ceilings the kernels are held to (graph "
+                    "launch floor, streaming read bandwidth, VALU issue rates) and exit")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
+        return 0
+    if a.traffic_record:
+        rec = traffic_record(*a.traffic_record)
+        TRAFFIC_RECORD.write_text(json.dumps(rec, indent=1) + "\n")
+        print(json.dumps(rec))
         return 0
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the reference path is single-GPU, TP=1); --gpus {a.gpus} is "
@@ -384,6 +552,12 @@ def main() -> int:
     log(f"device {name}")
     if a.traffic_probe:
         traffic_probe(dev)
+        return 0
+    if a.counter_probe:
+        counter_probe(dev)
+        return 0
+    if a.probes:
+        print(json.dumps({"probes": probes(dev), "device": name}), flush=True)
         return 0
 
     # ---- config 2 dense block, cold stack
@@ -458,20 +632,21 @@ def main() -> int:
 
     moe = route = None
     if not a.no_moe:
-        moe, route = bench_moe(dev, max(5, a.steps // 2), 6)
+        moe, route = bench_moe(dev, max(5, a.steps // 2))
     decoder = None
     if not a.no_decoder:
         decoder = bench_decoder(dev, max(5, a.steps // 2), a.warmup)
 
     cpu = None
     if not a.no_cpu:
-        med, cores = cpu_baseline(cpu_block, a.cpu_reps)
+        med, cores, affinity = cpu_baseline(cpu_block, a.cpu_reps)
         cpu = {"value": round(bpl / med / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-               "us_per_layer": round(med * 1e6, 1),
+               "us_per_layer": round(med * 1e6, 1), "affinity_cores": affinity, "cpu_model": cpu_model(),
                "sample": f"median of {a.cpu_reps} forwards of one config-2 block at batch 1: C dequantisation "
                          f"(oracle/, {cores} threads) + fp32 Hadamards + torch.matmul"}
         log(f"cpu baseline: {med * 1e3:.1f} ms/layer on {cores} cores")
 
+    traffic, traffic_note = recorded_traffic()
     out = {
         "metric": "compressed-weight HBM GB/s, config-2 dense block at batch 1 (us/layer at batch 1/8/32 and the MoE "
                   "layer alongside)",
@@ -497,8 +672,8 @@ def main() -> int:
         "route_group": route,
         "decoder": decoder,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": QKV_TRAFFIC_BYTES,
-                     "kernel": "dense_kernel (qkv launch, 5,269,504 B a launch)"},
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_note,
+                     "kernel": f"{ROOFLINE_KERNEL} (qkv launch, {qkv_bytes:,} B a launch)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -2,6 +2,7 @@
 
   libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, moe.hip, step.hip, abi.cpp)
   espalier_ext*.so     the torch extension module (binding.cpp, host code only), linked to libespalier_hip.so
+  libespalier_probe.so bench.py --probes' measurement kernels (probe.hip), apart from the kernel layer
 
 Both land in the vllm_espalier package directory. Usage: python build.py [--jobs N] [--only lib|ext]
 """
@@ -69,6 +70,15 @@ def build_lib(jobs: int) -> Path:
     return LIB
 
 
+def build_probe() -> Path:
+    BUILD.mkdir(exist_ok=True)
+    cc = hipcc()
+    out = PKG / "libespalier_probe.so"
+    run([cc, *HIP_FLAGS, "-x", "hip", "-shared", str(CSRC / "probe.hip"), "-o", str(out) + ".tmp"])
+    os.replace(str(out) + ".tmp", out)
+    return out
+
+
 def build_ext() -> Path:
     import torch.utils.cpp_extension as ce
     import torch
@@ -92,11 +102,13 @@ def build(jobs: int = 4, only: str | None = None) -> None:
         build_lib(jobs)
     if only in (None, "ext"):
         build_ext()
+    if only in (None, "probe"):
+        build_probe()
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
-    ap.add_argument("--only", choices=["lib", "ext"])
+    ap.add_argument("--only", choices=["lib", "ext", "probe"])
     a = ap.parse_args()
     build(a.jobs, a.only)
