@@ -136,6 +136,32 @@ def run_dense(stack, M: int, dev, which=None):
     return graph_of(fn)
 
 
+def run_dense_multi(stack, M: int, dev, chain: bool):
+    """A graph over every copy of the block as ONE esp_dense_multi launch a copy (W = 16 for every group): the four
+    groups side by side on their own inputs ("in one launch per layer"), or chained, each group
+    reading the previous group's output (o reads q, gate/up reads o's output, down reads the gate half), every
+    consumer waiting for its producer inside the launch."""
+    import torch
+    from vllm_espalier import dense as D
+    gen = torch.Generator(device=dev).manual_seed(2000 + M)
+    xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for K in (512, 2048, 4096)}
+    multis, ios = [], []
+    for block in stack:
+        m = D.DenseMulti(block, after=[False, chain, chain, chain], W=16)
+        outs = [torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev) for d in block]
+        if chain:
+            ins = [xs[2048], outs[0][:, :4096], outs[1], outs[2][:, :512]]
+        else:
+            ins = [xs[d.K] for d in block]
+        multis.append(m)
+        ios.append((ins, outs))
+
+    def fn():
+        for m, (ins, outs) in zip(multis, ios):
+            m.forward(ins, outs)
+    return graph_of(fn)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # MoE (config 4)
 # ---------------------------------------------------------------------------------------------------------------
@@ -580,6 +606,17 @@ def main() -> int:
             g1 = g
         else:
             del g
+    # the same block as one esp_dense_multi launch a layer: side by side, and chained
+    multi = {}
+    for chain in (False, True):
+        key = "chain" if chain else "independent"
+        multi[key] = {}
+        for M in (1, 8, 32):
+            g = run_dense_multi(stack, M, dev, chain)
+            us = time_graph(g, a.steps if M == 1 else max(5, a.steps // 2), a.warmup) * 1000 / copies
+            del g
+            multi[key][str(M)] = {"us_per_layer": round(us, 3), "GBps": round(bpl / (us * 1e-6) / 1e9, 1)}
+            log(f"dense block, one multi launch ({key}) M={M}: {us:.3f} us/layer, {bpl / (us * 1e-6) / 1e9:.0f} GB/s")
     # the timed steps of the headline: a step = one replay over the cold stack at batch 1
     for _ in range(a.warmup):
         g1.replay()
@@ -665,6 +702,7 @@ def main() -> int:
                                f"{copies} cold copies a step",
                    "bytes_per_layer": bpl, "layers_per_step": copies, "device": name},
         "dense_block": per_m,
+        "dense_block_one_launch": multi,
         "dense_launch_us_batch1": per_launch,
         "config1_us": round(c1_us, 3),
         "config1_GBps": round(c1_gbs, 1),

@@ -33,6 +33,7 @@ extern "C" {
 /* Bits of the device status word (esp_status). */
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
+#define ESP_STATUS_WAIT_TIMEOUT 4 /* a dense_multi group gave up waiting for its producer group (~20 ms) */
 
 /* Message of the last failed call on this host thread ("" if none). */
 const char* esp_last_error(void);
@@ -175,6 +176,42 @@ int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, d
                             const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
                             int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu,
                             int32_t* ucount, int32_t* members, int64_t maxm, void* stream);
+
+/* One group of esp_dense_multi: the arguments of one esp_dense launch (x, the matrices, y, k2 / cb / SK), plus
+ * after_previous: x is (a view of) the previous group's y, read once every column block of that group is finished;
+ * and an optional RMSNorm of the input as esp_dense_rmsnorm has it (norm_h non-NULL; not with after_previous). */
+typedef struct esp_dense_group {
+    const void* x;
+    int x_dtype;
+    int64_t x_stride, K, n_shards;
+    const void* trellis[4];
+    const void* suh[4];
+    const void* svh[4];
+    int64_t n_cols[4], col0[4];
+    void* y;
+    int y_dtype;
+    int64_t y_stride, y_cols, k2, cb, SK;
+    int after_previous;
+    const void* norm_h;
+    const void* norm_d1;
+    const void* norm_d2;
+    const void* norm_w;
+    void* norm_h_out;
+    double norm_eps;
+} esp_dense_group;
+
+/* Up to 4 dense launches (esp_dense's arithmetic and bits, group by group) in one launch, with M <= 32 rows and W waves
+ * a workgroup for every group. No counterpart in the reference, which launches each vLLM layer on its own: this runs a
+ * layer's dense launches -- independent ones side by side, or a chain such as qkv then o (after_previous) -- as one
+ * grid, so one launch gap and one weight-landing latency serve them all. A consumer group's workgroups issue their
+ * first trellis copies, then wait for the producer's column blocks (its finishers store y device-coherently and count
+ * the block done); workgroups are dispatched in id order and producers come first, so the wait ends, and a wait past
+ * ~20 ms sets ESP_STATUS_WAIT_TIMEOUT (esp_status) instead of hanging. Every group's input rotation must be the fused
+ * one (M * (K / SK) * 2 <= rot_smem). Scratch: Z (z_numel >= sum over groups of SK * M * sum(n_cols), each rounded up
+ * to 64 floats; at most 2^30 floats a group), counters (counters_numel >= 32 * sum over groups of sum(n_cols)/128 +
+ * 64 * n_groups; zero on entry and left zero). */
+int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, int64_t M, int64_t W, float* Z, int64_t z_numel,
+                    int32_t* counters, int64_t counters_numel, int64_t rot_smem, void* stream);
 
 /* esp_dense without caller scratch, for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the reference. Arguments and results as esp_dense (the

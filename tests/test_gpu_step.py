@@ -198,3 +198,21 @@ def test_decoder_fused_norms_equal_separate(small_decoder, T, monkeypatch):
     for x, y in zip(res[False], res[True]):
         assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x,
                            y.view(torch.int16) if y.dtype == torch.bfloat16 else y)
+
+
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_decoder_multi_attention_equals_apart(small_decoder, T, monkeypatch):
+    """qkv and o as one chained launch (DenseMulti) against the two launches apart: logits and residuals bit for bit."""
+    dec = small_decoder
+    ids = [(7 + 613 * i) % 5120 for i in range(T)]
+    res = {}
+    for multi in (False, True):
+        monkeypatch.setattr(S, "MULTI_ATTN", multi)
+        b = dec.buffers(T)
+        b.ids_in.copy_(torch.tensor(ids, dtype=torch.int32))
+        dec.forward(T)
+        torch.cuda.synchronize()
+        res[multi] = (b.logits.cpu().clone(), b.h.cpu().clone(), b.h2.cpu().clone(), b.ids_out.cpu().clone())
+    for x, y in zip(res[False], res[True]):
+        assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x,
+                           y.view(torch.int16) if y.dtype == torch.bfloat16 else y)

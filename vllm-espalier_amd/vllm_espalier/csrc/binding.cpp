@@ -445,6 +445,86 @@ void argmax(const at::Tensor& logits, at::Tensor ids, std::optional<at::Tensor> 
                     counters.has_value() ? counters->numel() : 0, cur_stream()));
 }
 
+// several dense launches as one (esp_dense_multi; no reference counterpart): per group its input rows, matrices,
+// output columns and plan; after[g] != 0 when group g's x is a view of group g - 1's y. The optional norm (h, d1, d2,
+// w, h_out, eps) makes group 0's input RMSNorm(h + d1 + d2) * w, as dense_rmsnorm does.
+void dense_multi(const std::vector<at::Tensor>& xs, const std::vector<std::vector<at::Tensor>>& T,
+                 const std::vector<std::vector<at::Tensor>>& suh, const std::vector<std::vector<at::Tensor>>& svh,
+                 const std::vector<std::vector<int64_t>>& col0, const std::vector<at::Tensor>& ys,
+                 const std::vector<int64_t>& k2, const std::vector<int64_t>& cb, const std::vector<int64_t>& SK,
+                 const std::vector<int64_t>& after, at::Tensor Z, at::Tensor counters, int64_t W, int64_t rot_smem,
+                 const c10::optional<at::Tensor>& norm_h, const c10::optional<at::Tensor>& norm_d1,
+                 const c10::optional<at::Tensor>& norm_d2, const c10::optional<at::Tensor>& norm_w,
+                 const c10::optional<at::Tensor>& norm_h_out, double eps) {
+    const size_t n = xs.size();
+    TORCH_CHECK(n >= 1 && n <= 4, "dense_multi: 1 to 4 groups");
+    TORCH_CHECK(T.size() == n && suh.size() == n && svh.size() == n && col0.size() == n && ys.size() == n &&
+                    k2.size() == n && cb.size() == n && SK.size() == n && after.size() == n,
+                "dense_multi: one entry a group in every list");
+    check(Z, at::kFloat, "Z");
+    check(counters, at::kInt, "counters");
+    std::vector<esp_dense_group> g(n);
+    const int64_t M = xs[0].size(0);
+    for (size_t i = 0; i < n; ++i) {
+        const at::Tensor& x = xs[i];
+        const at::Tensor& y = ys[i];
+        TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1 && x.size(0) == M, "x: CUDA [M, K], unit column stride");
+        TORCH_CHECK(y.is_cuda() && y.dim() == 2 && y.stride(1) == 1 && y.size(0) == M, "y: CUDA [M, N], unit column stride");
+        TORCH_CHECK(T[i].size() >= 1 && T[i].size() <= 4 && suh[i].size() == T[i].size() && svh[i].size() == T[i].size() &&
+                        col0[i].size() == T[i].size(),
+                    "dense_multi: 1 to 4 matrices a group, one entry a matrix");
+        esp_dense_group& G = g[i];
+        G = esp_dense_group{};
+        G.x = x.data_ptr();
+        G.x_dtype = dtype_code(x);
+        G.x_stride = x.stride(0);
+        G.K = x.size(1);
+        G.n_shards = (int64_t)T[i].size();
+        for (size_t s = 0; s < T[i].size(); ++s) {
+            TORCH_CHECK(T[i][s].is_cuda() && T[i][s].scalar_type() == at::kShort && T[i][s].is_contiguous() &&
+                            T[i][s].dim() == 3 && T[i][s].size(0) * 16 == G.K && T[i][s].size(1) * 16 == svh[i][s].numel() &&
+                            T[i][s].size(2) == 8 * k2[i],
+                        "trellis: contiguous int16 [K/16, N/16, 16K] matching x and svh");
+            check(suh[i][s], at::kHalf, "suh");
+            check(svh[i][s], at::kHalf, "svh");
+            TORCH_CHECK(suh[i][s].numel() == G.K, "suh must have K elements");
+            G.trellis[s] = T[i][s].data_ptr();
+            G.suh[s] = suh[i][s].data_ptr();
+            G.svh[s] = svh[i][s].data_ptr();
+            G.n_cols[s] = svh[i][s].numel();
+            G.col0[s] = col0[i][s];
+        }
+        G.y = y.data_ptr();
+        G.y_dtype = dtype_code(y);
+        G.y_stride = y.stride(0);
+        G.y_cols = y.size(1);
+        G.k2 = k2[i];
+        G.cb = cb[i];
+        G.SK = SK[i];
+        G.after_previous = after[i] ? 1 : 0;
+    }
+    if (norm_h.has_value()) {
+        const auto t = norm_h->scalar_type();
+        TORCH_CHECK(norm_h->is_contiguous() && norm_w.has_value() && norm_h_out.has_value() && norm_w->scalar_type() == t &&
+                        norm_h_out->scalar_type() == t && norm_h->sizes() == xs[0].sizes(),
+                    "dense_multi: the norm's h, w, h_out in x's shape and dtype");
+        for (const auto* d : {&norm_d1, &norm_d2})
+            if (d->has_value()) TORCH_CHECK((*d)->is_contiguous() && (*d)->scalar_type() == t && (*d)->sizes() == norm_h->sizes(),
+                                            "deltas: h's dtype and shape, contiguous");
+        g[0].x = norm_h->data_ptr();
+        g[0].x_stride = norm_h->stride(0);
+        g[0].norm_h = norm_h->data_ptr();
+        g[0].norm_d1 = norm_d1.has_value() ? norm_d1->data_ptr() : nullptr;
+        g[0].norm_d2 = norm_d2.has_value() ? norm_d2->data_ptr() : nullptr;
+        g[0].norm_w = norm_w->data_ptr();
+        g[0].norm_h_out = norm_h_out->data_ptr();
+        g[0].norm_eps = eps;
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(xs[0].device());
+    call(esp_dense_multi((int64_t)n, g.data(), M, W, mptr<float>(Z), Z.numel(), mptr<int32_t>(counters),
+                         counters.numel(), rot_smem, cur_stream()));
+}
+
 // the device status word of the current GPU (esp_status; no reference counterpart), cleared after the read if asked
 int64_t status(bool clear) {
     int32_t v = 0;
@@ -469,6 +549,11 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("moe_gateup", &moe_gateup);
     m.def("dense_rmsnorm", &dense_rmsnorm);
     m.def("status", &status, py::arg("clear") = false);
+    m.def("dense_multi", &dense_multi, py::arg("xs"), py::arg("T"), py::arg("suh"), py::arg("svh"), py::arg("col0"),
+          py::arg("ys"), py::arg("k2"), py::arg("cb"), py::arg("SK"), py::arg("after"), py::arg("Z"),
+          py::arg("counters"), py::arg("W"), py::arg("rot_smem"), py::arg("norm_h") = py::none(),
+          py::arg("norm_d1") = py::none(), py::arg("norm_d2") = py::none(), py::arg("norm_w") = py::none(),
+          py::arg("norm_h_out") = py::none(), py::arg("eps") = 0.0);
     m.def("route_group_rmsnorm", &route_group_rmsnorm);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);

@@ -256,6 +256,7 @@ const char* last_error();
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();
 int launch_check(const char* what);
+int dense_status(int clear, hipStream_t st, int* out);     // dense.hip: the dense launches' status word
 }  // namespace esp_host
 
 #define ESP_REQUIRE(cond, ...)                                                                  \

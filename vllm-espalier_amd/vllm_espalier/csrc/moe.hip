@@ -1255,10 +1255,12 @@ extern "C" int esp_status(int32_t* status, int clear, void* stream) {
     ESP_REQUIRE(status, "status: null pointer");
     hipStream_t st = (hipStream_t)stream;
     int v = 0;
+    *status = 0;
     if (hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(g_status), sizeof(int), 0, hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "status: cannot read the device status word");
-    *status = v;
+    if (esp_host::dense_status(clear, st, status)) return ESP_ERR_HIP;
+    *status |= v;
     if (clear && v) {
         const int zero = 0;
         if (hipMemcpyToSymbolAsync(HIP_SYMBOL(g_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice, st) !=

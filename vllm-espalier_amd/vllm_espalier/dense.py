@@ -184,3 +184,40 @@ class Dense:
                             [m.svh for m in ms], [self.col0[i] for i in l.members], out, z, self.counters, l.k2, l.cb,
                             l.sk, l.w, ROT_SMEM)
         return out
+
+
+class DenseMulti:
+    """Several one-launch Dense layers as a single esp_dense_multi launch: independent layers side by side, or a chain
+    in which layer i reads layer i-1's output (after[i]): one launch gap and one weight-landing latency for all of
+    them. Every layer keeps its own plan's K splits; the waves a workgroup are the same for all (W), so a layer's bits
+    equal its own launch at that W."""
+
+    def __init__(self, layers, after=None, W: int = 16):
+        self.layers = list(layers)
+        self.after = list(after) if after is not None else [False] * len(self.layers)
+        if not 1 <= len(self.layers) <= 4 or len(self.after) != len(self.layers) or self.after[0]:
+            raise ValueError("1 to 4 layers; only a layer after the first may read the previous one's output")
+        if any(len(d.launches) != 1 for d in self.layers):
+            raise ValueError("every layer of a multi launch must be a single launch group")
+        self.W = W
+        device = self.layers[0].mats[0].trellis.device
+        blocks = sum(d.launches[0].n // 128 for d in self.layers)
+        self.counters = torch.zeros(COUNTER_STRIDE * (blocks + 2 * len(self.layers)), dtype=torch.int32, device=device)
+        z = sum(-(-(d.launches[0].sk * MAX_ROWS * d.launches[0].n) // 64) * 64 for d in self.layers)
+        scratch(device, z, 0)
+
+    def forward(self, xs, outs, norm=None):
+        """xs[i] [M, K_i] rows of layer i (for a layer after its predecessor, a view of that layer's output); outs[i]
+        [M, n_out_i] in the model's dtype. norm = (h, d1, d2, w, eps, h_out): layer 0's rows are RMSNorm(h + d1 + d2)
+        * w, made in the launch, with the residual stored to h_out (xs[0] is then unused)."""
+        z, _ = scratch(outs[0].device, 0, 0)
+        launches = [d.launches[0] for d in self.layers]
+        h, d1, d2, w, eps, h_out = norm if norm is not None else (None, None, None, None, 0.0, None)
+        x0 = h if norm is not None else xs[0]
+        ext().dense_multi([x0] + list(xs[1:]), [[d.mats[i].trellis for i in l.members] for d, l in zip(self.layers, launches)],
+                          [[d.mats[i].suh for i in l.members] for d, l in zip(self.layers, launches)],
+                          [[d.mats[i].svh for i in l.members] for d, l in zip(self.layers, launches)],
+                          [[d.col0[i] for i in l.members] for d, l in zip(self.layers, launches)], list(outs),
+                          [l.k2 for l in launches], [l.cb for l in launches], [l.sk for l in launches],
+                          [int(a) for a in self.after], z, self.counters, self.W, ROT_SMEM, h, d1, d2, w, h_out, eps)
+        return outs

@@ -14,7 +14,9 @@ package, nothing allocates after construction, so a HIP graph holds a whole step
 
 For up to 4 rows (decode) each norm runs inside its consumer's launch instead (dense_rmsnorm for qkv and the head,
 route_group_rmsnorm for the router), with the same arithmetic in the same order, so the bits do not change: the qkv
-launch stores the residual to a second buffer, which the routing launch reads and adds o to, back into h.
+launch stores the residual to a second buffer, which the routing launch reads and adds o to, back into h. qkv and o
+run as one chained launch (dense.DenseMulti: o's workgroups issue their weight copies, then wait for qkv's column
+blocks), with the bits of the two launches apart (MULTI_ATTN = False runs them apart).
 
 Rows never interact (the dense and grouped kernels keep rows apart, norms are per row), so a window of T rows
 gives each row the bits it gets alone.
@@ -37,6 +39,7 @@ VOCAB = 151936
 TOPK = 8
 EPS = 1e-6
 FUSE_NORMS = True            # the norms inside their consumers' launches for up to 4 rows (same bits)
+MULTI_ATTN = True            # qkv and o as one chained launch (same bits)
 
 
 @dataclass
@@ -44,6 +47,7 @@ class DecoderLayer:
     norm1: torch.Tensor          # bf16 [D]
     qkv: Dn.Dense
     o: Dn.Dense
+    attn: Dn.DenseMulti          # qkv then o (reading q) in one launch
     norm2: torch.Tensor
     router: torch.Tensor         # bf16 [E, D]
     moe: G.Layer
@@ -68,7 +72,10 @@ def build_layer(gen: torch.Generator, dev, E: int = 256, D: int = D_MODEL, I: in
     gate_w = (torch.randn((D,), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
     router = (torch.randn((E, D), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
     moe = G.prepare(experts, shared, gate_w)
-    return DecoderLayer(_norm_weight(gen, dev, D), qkv, o, _norm_weight(gen, dev, D), router, moe, experts, shared)
+    # both launches at 16 waves (their plans' own width at these shapes), so the chained launch keeps their bits
+    attn = Dn.DenseMulti([qkv, o], after=[False, True], W=16)
+    return DecoderLayer(_norm_weight(gen, dev, D), qkv, o, attn, _norm_weight(gen, dev, D), router, moe, experts,
+                        shared)
 
 
 class Buffers:
@@ -123,13 +130,19 @@ class SyntheticDecoder:
         q = b.qkv[:, :Q_OUT]
         d1, d2 = (None, None) if first else (b.moe, b.moe_shared)
         if self.fused_norms(b.T):
-            L.qkv.forward_rmsnorm(b.h, d1, d2, L.norm1, EPS, b.h2, out=b.qkv)
-            L.o.forward(q, out=b.o)
+            if MULTI_ATTN:
+                L.attn.forward([None, q], [b.qkv, b.o], norm=(b.h, d1, d2, L.norm1, EPS, b.h2))
+            else:
+                L.qkv.forward_rmsnorm(b.h, d1, d2, L.norm1, EPS, b.h2, out=b.qkv)
+                L.o.forward(q, out=b.o)
             G.route_rmsnorm(b.h2, b.o, L.norm2, EPS, b.h, b.a, L.router, TOPK, L.moe, self.scratch)
         else:
             e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
-            L.qkv.forward(b.a, out=b.qkv)
-            L.o.forward(q, out=b.o)
+            if MULTI_ATTN:
+                L.attn.forward([b.a, q], [b.qkv, b.o])
+            else:
+                L.qkv.forward(b.a, out=b.qkv)
+                L.o.forward(q, out=b.o)
             e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
             G.route(b.a, L.router, TOPK, L.moe, self.scratch)
         if picks is not None:                     # eager runs only: the distinct experts this layer reads
