@@ -281,6 +281,19 @@ def bench_decoder(dev, steps: int, warmup: int, layers: int = 40, prefill_tokens
     del g
     res["prefill"] = {"tokens": nwin * W, "window": W, "ms": round(ms, 3), "tok_per_s": round(nwin * W / (ms * 1e-3), 1)}
     log(f"prefill: {nwin * W} tokens in {ms:.2f} ms, {nwin * W / (ms * 1e-3):.0f} tok/s")
+    # the tile prefill: the same prompt with every layer's experts grouped over the whole prompt
+    T = nwin * W
+    bp = dec.prefill_buffers(T)
+    bp.ids_in.copy_(ids_all[:T])
+
+    def prefill_tile():
+        dec.prefill(T)
+    g = graph_of(prefill_tile)
+    ms = time_graph(g, max(3, steps // 4), 1)
+    del g
+    res["prefill_tile"] = {"tokens": T, "ms": round(ms, 3), "tok_per_s": round(T / (ms * 1e-3), 1),
+                           "mode": "dense layers in 32-row windows, each layer's MoE grouped over the whole prompt"}
+    log(f"prefill (tile): {T} tokens in {ms:.2f} ms, {T / (ms * 1e-3):.0f} tok/s")
     del dec
     torch.cuda.empty_cache()
     return res

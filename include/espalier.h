@@ -86,14 +86,17 @@ int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int
 
 /* Replaces `group_shared` (experts.cpp:154-172, experts.cu:247-330, 518-539): pick/weight tables with the shared
  * expert as slot slots_in (weight sigmoid(x . gate_w), fp32), then the grouping. pick_in int32 / wts_in fp32
- * [R][slots_in]; x [R][x_stride] with H columns; gate_w [H] (x's dtype) or NULL; pick_out / wts_out [R * slots]. */
+ * [R][slots_in]; x [R][x_stride] with H columns; gate_w [H] (x's dtype) or NULL; pick_out / wts_out [R * slots].
+ * Windows of more than 1056 picks (a whole prompt) are grouped by a workgroup an expert id, with the same tables
+ * (maxm <= 16384). */
 int esp_group_shared(const int32_t* pick_in, const float* wts_in, const void* x, int x_dtype, int64_t x_stride,
                      int64_t H, const void* gate_w, int64_t shared_id, int32_t* pick_out, float* wts_out,
                      int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm, int64_t R,
                      int64_t slots_in, int64_t E, void* stream);
 
 /* Replaces `group` (experts.cpp:79-90, experts.cu:23-76, 435-455): distinct picks in [0, E) in id order (uids,
- * ucount) and their members row * 32 + slot in pick order, -1 padded to maxm. */
+ * ucount) and their members row * 32 + slot in pick order, -1 padded to maxm (any window: beyond 1056 picks a
+ * workgroup an expert id, maxm <= 16384). */
 int esp_group(const int32_t* pick, int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm,
               int64_t R, int64_t slots, int64_t E, void* stream);
 
@@ -106,8 +109,10 @@ int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const int32_t* pick
 /* Replaces `grouped` (experts.cpp:44-66, experts_grouped.cuh:237-318, 360-377): Z fp32 [mats][SK][P][N] = the K-split
  * partial sums of X_mat[row] @ W_mat[e] for every member row of every distinct expert u < ucount. X0/X1 fp16 [P][K];
  * TP0/TP1 int64 [E] trellis device pointers; B0/B1 int32 [E] K2; C0/C1 int32 [E] codebook ids; uids [nexp_max];
- * members [nexp_max][maxm]. nt, warps, pf are tile hints; lo/hi bound the K2 of the launch's experts (an expert
- * outside them, or with no kernel, gets NaN partials and a status bit: esp_status). */
+ * members [nexp_max][maxm], maxm any size: an expert's members run in tiles of 32 (the reference's are 16,
+ * experts_grouped.cuh:244), each tile decoding the expert's weights once. nt, warps, pf are tile hints; lo/hi bound
+ * the K2 of the launch's experts (an expert outside them, or with no kernel, gets NaN partials and a status bit:
+ * esp_status). */
 int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
                 const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
                 const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int64_t mats,
@@ -208,8 +213,10 @@ typedef struct esp_dense_group {
  * the block done); workgroups are dispatched in id order and producers come first, so the wait ends, and a wait past
  * ~20 ms sets ESP_STATUS_WAIT_TIMEOUT (esp_status) instead of hanging. Every group's input rotation must be the fused
  * one (M * (K / SK) * 2 <= rot_smem). Scratch: Z (z_numel >= sum over groups of SK * M * sum(n_cols), each rounded up
- * to 64 floats; at most 2^30 floats a group), counters (counters_numel >= 32 * sum over groups of sum(n_cols)/128 +
- * 64 * n_groups; zero on entry and left zero). */
+ * to 64 floats; at most 2^30 floats a group), counters (8-byte aligned, counters_numel >= 32 * sum over groups of
+ * sum(n_cols)/128 + 64 * n_groups; zero before a buffer's first launch. The split-K counters are left zero; the last
+ * 64 ints a group hold 64-bit running counts of the chain's hand-offs, which only grow, so one buffer serves one chain
+ * of groups for the life of the process). */
 int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, int64_t M, int64_t W, float* Z, int64_t z_numel,
                     int32_t* counters, int64_t counters_numel, int64_t rot_smem, void* stream);
 

@@ -2,7 +2,8 @@
 independent groups side by side (BASELINE config 2's block: qkv, o, shared gate/up, shared down), and chains in which
 a group reads the previous group's output (qkv then o on q, as the synthetic decoder runs them), with and without the
 RMSNorm of the first group's input made in the launch. Counters are left zero and no wait times out (status 0); graph
-replays equal eager launches.
+replays equal eager launches. A chain's hand-off counts only grow, so a multi launch replayed many times (graph
+replays, eager calls) keeps waiting for the right launch's producer.
 """
 import numpy as np
 import pytest
@@ -33,7 +34,7 @@ def _layers(specs, seed, dev):
 
 def _clean(ext, multi):
     torch.cuda.synchronize()
-    assert int(multi.counters.abs().sum()) == 0, "counters left non-zero"
+    assert int(multi.counters[:multi.split_counters].abs().sum()) == 0, "split-K counters left non-zero"
     assert int(ext.status(True)) == 0, "a wait timed out"
 
 

@@ -52,14 +52,18 @@ def ext_suffix() -> str:
     return sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 
 
-def build_lib(jobs: int) -> Path:
+def build_lib(jobs: int, incremental: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
     srcs = [CSRC / "dense.hip", CSRC / "dense_multi.hip", CSRC / "moe.hip", CSRC / "step.hip", CSRC / "abi.cpp"]
     objs = [BUILD / (s.stem + ".o") for s in srcs]
+    headers = [*CSRC.glob("*.hpp"), REPO / "include" / "espalier.h"]
+    newest_header = max(h.stat().st_mtime for h in headers)
 
     def compile_one(pair):
         s, o = pair
+        if incremental and o.exists() and o.stat().st_mtime > max(s.stat().st_mtime, newest_header):
+            return                                       # object newer than its source and every header
         lang = ["-x", "hip"] if s.suffix == ".hip" else []
         run([cc, *HIP_FLAGS, *lang, "-c", str(s), "-o", str(o)])
 
@@ -98,9 +102,9 @@ def build_ext() -> Path:
     return out
 
 
-def build(jobs: int = 4, only: str | None = None) -> None:
+def build(jobs: int = 4, only: str | None = None, incremental: bool = False) -> None:
     if only in (None, "lib"):
-        build_lib(jobs)
+        build_lib(jobs, incremental)
     if only in (None, "ext"):
         build_ext()
     if only in (None, "probe"):
@@ -111,5 +115,6 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("--only", choices=["lib", "ext", "probe"])
+    ap.add_argument("--incremental", action="store_true", help="skip objects newer than their source and every header")
     a = ap.parse_args()
-    build(a.jobs, a.only)
+    build(a.jobs, a.only, a.incremental)

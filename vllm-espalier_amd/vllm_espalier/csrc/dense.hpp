@@ -44,12 +44,14 @@ struct DenseArgs {
     uint16_t* nh_out;
     float neps;
     int norm;
-    // a group of a multi launch (esp_dense_multi); all null / zero in a plain launch
-    int* done;               // this group's finished column blocks (counted by each block's finisher), or null
-    const int* wait_done;    // the producer group's counter: x is its output, read once it reaches wait_total
-    int wait_total;
-    int* pass;               // this group's workgroups past the wait; the last resets *wait_done and *pass
-    int pass_total;
+    // a group of a multi launch (esp_dense_multi); all null / zero in a plain launch. The counters only grow: in the
+    // n-th launch (from 0) a producer's finishers take done from n * blocks to (n + 1) * blocks, and a consumer
+    // workgroup's ticket (its pass count, taken when it starts) tells it n.
+    unsigned long long* done;        // this group's finished column blocks, or null
+    const unsigned long long* wait_done;   // the producer group's done: x is its output
+    unsigned long long* pass;        // this group's workgroups started (tickets)
+    int wait_total;                  // the producer's column blocks
+    int pass_total;                  // this group's workgroups
     int case_id;             // cb * 32 + k2 of the group (the multi kernel's instance)
 };
 
@@ -97,15 +99,15 @@ __device__ __forceinline__ RotIn rot128_load_dev(const void* x, int x_dtype, siz
 // A consumer workgroup of a multi launch waits for its producer group: nothing outside a multi launch; the multi
 // launch's wait is defined in dense_multi.hip, before its kernel
 template <bool MULTI>
-__device__ __forceinline__ void dense_wait_producer(const DenseArgs& a);
+__device__ __forceinline__ void dense_wait_producer(const DenseArgs& a, unsigned long long ticket);
 template <>
-__device__ __forceinline__ void dense_wait_producer<false>(const DenseArgs&) {}
+__device__ __forceinline__ void dense_wait_producer<false>(const DenseArgs&, unsigned long long) {}
 
 // After a finisher's y stores: drain them, then count the column block done for the consumer group
 __device__ __forceinline__ void signal_done(const DenseArgs& a) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(a.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(a.done, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // the finished outputs of one row's 128 columns from their fp32 sums, 4 a lane: H / sqrt(128), * c, * svh
 // (dense.cu:120-128); sv holds the lane's 4 svh values (fp16 bits), loaded when the workgroup starts
@@ -125,6 +127,10 @@ __device__ __forceinline__ void finish(float (&v)[4], int l32, uint2 sv, float s
 template <int CB, int K2, int MG, bool MULTI>
 __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg, const int split, unsigned char* smem,
                                               int& last, float* npart, float* ninv) {
+    // a consumer group's ticket, taken first so its round trip overlaps the producer's work
+    unsigned long long ticket = 0;
+    if (MULTI && a.wait_done && threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(a.pass, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // What the first copy needs -- every shard's trellis pointer, first block and width, the split and the launch
     // shape -- in one round of kernel-argument loads, consumed together by one empty asm: an indexed load of the
     // workgroup's shard would wait for the shard's selection, and each later first use for its own round trip.
@@ -230,7 +236,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             }
         } else if (MULTI && a.wait_done) {
             // x is the output of the producer group of this launch: wait for it, then read it device-coherently
-            dense_wait_producer<MULTI>(a);
+            dense_wait_producer<MULTI>(a, ticket);
             for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
                 const int r = idx / chunks, ch = idx % chunks;
                 const int kb = (c0 + ch) * 128;

@@ -7,24 +7,21 @@ namespace esp {
 // Device status of the dense launches (read and cleared by esp_status through dense_status)
 __device__ int g_dense_status;
 
-// Thread 0 waits until *done reaches total (the producer group has finished every column block), for at most ~20 ms
-// of device time: past that it records ESP_STATUS_WAIT_TIMEOUT and goes on, so a launch can never hang. Then it counts
-// this workgroup past the wait; the last of the group's workgroups to pass resets both counters for the next launch.
+// Thread 0 waits until the producer's done count reaches this launch's target, (n + 1) * blocks with n = ticket /
+// the group's workgroups, for at most ~20 ms of device time: past that it records ESP_STATUS_WAIT_TIMEOUT and goes on,
+// so a launch can never hang. Nothing is reset (the counters are 64-bit).
 template <>
-__device__ __forceinline__ void dense_wait_producer<true>(const DenseArgs& a) {
+__device__ __forceinline__ void dense_wait_producer<true>(const DenseArgs& a, unsigned long long ticket) {
     if (threadIdx.x == 0) {
+        const unsigned long long target = (ticket / (unsigned)a.pass_total + 1ull) * (unsigned)a.wait_total;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();        // 100 MHz
-        while (load_dev(a.wait_done) < a.wait_total) {
-            __builtin_amdgcn_s_sleep(2);
+        while (load_dev(a.wait_done) < target) {
+            __builtin_amdgcn_s_sleep(4);
             if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
                 __hip_atomic_fetch_or(&g_dense_status, ESP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-        }
-        if (__hip_atomic_fetch_add(a.pass, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.pass_total - 1) {
-            store_dev(const_cast<int*>(a.wait_done), 0);
-            store_dev(a.pass, 0);
         }
     }
     __syncthreads();
@@ -45,18 +42,24 @@ struct MultiArgs {
     int nbt[MAX_GROUPS];
 };
 
+// The arguments are read where the launch put them, in the kernel-argument segment (constant address space), never
+// through the by-value parameter: indexing that with the run-time group would copy the whole block (~1.4 KiB) into
+// every lane's private memory.
+typedef __attribute__((address_space(4))) const MultiArgs* MultiArgsPtr;
+
 template <int MG>
-__global__ __launch_bounds__(1024) void dense_multi_kernel(MultiArgs m) {
+__global__ __launch_bounds__(1024) void dense_multi_kernel(MultiArgs) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int last;
     __shared__ float npart[16], ninv[4];
+    const MultiArgsPtr m = (MultiArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
     const int id = blockIdx.x;
     int gi = 0;
 #pragma unroll
     for (int i = 1; i < MAX_GROUPS; ++i)
-        if (i < m.ng && id >= m.start[i]) gi = i;
-    const DenseArgs& a = m.g[gi];
-    const int local = id - m.start[gi], nb = m.nbt[gi];
+        if (i < m->ng && id >= m->start[i]) gi = i;
+    const DenseArgs& a = *(const DenseArgs*)&m->g[gi];
+    const int local = id - m->start[gi], nb = m->nbt[gi];
     const int nbg = local % nb, split = local / nb;
     switch (a.case_id) {
 #define ESP_MULTI_CASE(CB_, K2_)                                                                      \
@@ -87,6 +90,7 @@ extern "C" int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, 
                                void* stream) {
     ESP_REQUIRE(groups && n_groups >= 1 && n_groups <= MAX_GROUPS, "dense_multi: 1 to 4 groups");
     ESP_REQUIRE(Z && counters, "dense_multi: null scratch");
+    ESP_REQUIRE(((uintptr_t)counters & 7) == 0, "dense_multi: counters must be 8-byte aligned");
     MultiArgs m{};
     m.ng = (int)n_groups;
     int64_t z_off = 0, c_off = 0;
@@ -131,11 +135,11 @@ extern "C" int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, 
     }
     for (int g = 1; g < n_groups; ++g) {
         if (!groups[g].after_previous) continue;
-        int* link = counters + link_base;
-        m.g[g - 1].done = link + (2 * (g - 1)) * CNT_STRIDE;
+        unsigned long long* link = reinterpret_cast<unsigned long long*>(counters + link_base);
+        m.g[g - 1].done = link + (2 * (g - 1)) * (CNT_STRIDE / 2);
         m.g[g].wait_done = m.g[g - 1].done;
         m.g[g].wait_total = m.nbt[g - 1];
-        m.g[g].pass = link + (2 * g + 1) * CNT_STRIDE;
+        m.g[g].pass = link + (2 * g + 1) * (CNT_STRIDE / 2);
         m.g[g].pass_total = m.start[g + 1] - m.start[g];
     }
     hipStream_t st = (hipStream_t)stream;

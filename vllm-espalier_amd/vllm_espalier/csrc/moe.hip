@@ -450,6 +450,95 @@ __global__ __launch_bounds__(GT) void group_shared_kernel(const int* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// Grouping of windows larger than one workgroup's shared memory holds (more than MAX_PICKS picks: prefill over a
+// whole prompt): one workgroup per expert id. Every workgroup scans all the picks, chunk by chunk in pick order,
+// setting the ids it sees in a bitmask (an expert's place is then the number of used ids below it) and ranking its own
+// id's picks by ballots and a scan over its waves; the tables are group_block's, entry for entry.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int GW = 256;
+constexpr int GW_MAX_M = 16384;           // members an expert (its list is kept in shared memory)
+
+__global__ __launch_bounds__(GW) void group_wide_kernel(const int* __restrict__ pick, int n, int slots, int nid,
+                                                        int maxm, int* __restrict__ uids, int* __restrict__ ucount,
+                                                        int* __restrict__ members) {
+    extern __shared__ int mem_sh[];                      // this id's member codes, in pick order
+    __shared__ unsigned used[MAX_GROUP_IDS / 32];
+    __shared__ int wave_cnt[GW / 64];
+    __shared__ int place_sh;
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int words = (nid + 31) >> 5;
+    for (int w = tid; w < words; w += GW) used[w] = 0u;
+    __syncthreads();
+    int count = 0;                                       // this id's picks so far (the same in every thread)
+    for (int base = 0; base < n; base += GW) {
+        const int i = base + tid;
+        const int v = i < n ? pick[i] : -1;
+        const bool valid = v >= 0 && v < nid;
+        if (valid) atomicOr(&used[v >> 5], 1u << (v & 31));
+        const bool mine = valid && v == e;
+        const uint64_t bal = __ballot(mine);
+        if (lane == 0) wave_cnt[wave] = __builtin_popcountll(bal);
+        __syncthreads();
+        int before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < GW / 64; ++w) {
+            const int c = wave_cnt[w];
+            before += w < wave ? c : 0;
+            total += c;
+        }
+        if (mine) {
+            const int rank = count + before + __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+            if (rank < maxm) mem_sh[rank] = (i / slots) * 32 + (i % slots);
+        }
+        count += total;
+        __syncthreads();                                 // wave_cnt is rewritten by the next chunk
+    }
+    if (e == 0 && tid == 0) {
+        int u = 0;
+        for (int w = 0; w < words; ++w) u += __builtin_popcount(used[w]);
+        *ucount = u;
+    }
+    if (count == 0) return;                              // the same in every thread
+    if (tid == 0) {
+        int p = __builtin_popcount(used[e >> 5] & ((1u << (e & 31)) - 1u));
+        for (int w = 0; w < (e >> 5); ++w) p += __builtin_popcount(used[w]);
+        place_sh = p;
+        uids[p] = e;
+    }
+    __syncthreads();
+    const size_t at = (size_t)place_sh * maxm;
+    for (int m = tid; m < maxm; m += GW) members[at + m] = m < count ? mem_sh[m] : -1;
+}
+
+// group_shared's pick / weight tables for any number of rows, a wave a row: the routed slots copied, the shared slot
+// added with weight sigmoid(x . gate_w) computed exactly as group_shared_kernel does (the same bits)
+__global__ __launch_bounds__(256) void shared_slots_kernel(const int* __restrict__ pick_in, const float* __restrict__ wts_in,
+                                                           const uint16_t* __restrict__ x, int x_stride, int bf16,
+                                                           const uint16_t* __restrict__ gate_w, int H, int shared_id,
+                                                           int* __restrict__ pick_out, float* __restrict__ wts_out,
+                                                           int R, int slots_in) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= R) return;
+    const int has = shared_id >= 0, slots = slots_in + has;
+    for (int k = lane; k < slots_in; k += 64) {
+        pick_out[r * slots + k] = pick_in[r * slots_in + k];
+        wts_out[r * slots + k] = wts_in[r * slots_in + k];
+    }
+    if (!has) return;
+    if (lane == 0) pick_out[r * slots + slots_in] = shared_id;
+    double acc = 0.0;
+    for (int h = 4 * lane; h < H; h += 256) {
+        double xv[4], wv[4];
+        load4_16(x + (size_t)r * x_stride + h, bf16, xv);
+        load4_16(gate_w + h, bf16, wv);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = __builtin_fma(xv[q], wv[q], acc);
+    }
+    const double sum = wave_sum_f64_dpp(acc);
+    if (lane == 0) wts_out[r * slots + slots_in] = 1.f / (1.f + expf(-(float)sum));
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // rot_in (experts.cu:97-115): one wave per (slot row, 128-block); lanes 0-31 the gate input, 32-63 the up input
 // ------------------------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rot_in_kernel(const uint16_t* __restrict__ x, int x_dtype, int x_stride,
@@ -505,6 +594,7 @@ struct GroupedArgs {
     int* counters;                 // arrival counters CNT_STRIDE apart: zero on entry, left zero
     int stage_bytes, xs_stride;    // rotated rows in shared memory after the stages
     int lo, hi;                    // the K2 range the launch's stages are sized for
+    int mt;                        // member tiles of 32 an expert (MODE 0: ceil(maxm / 32); MODE 1: 1)
 };
 
 // Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
@@ -789,7 +879,9 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
     const int u = blockIdx.x;
-    const int split = blockIdx.z % a.SK, mat = blockIdx.z / a.SK;
+    // program: member tile (32 members of the expert's list), K split, matrix
+    const int mtile = blockIdx.z % a.mt, zz = blockIdx.z / a.mt;
+    const int split = zz % a.SK, mat = zz / a.SK;
     const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
     const int NW = (int)(blockDim.x >> 6);
     __shared__ int rows_sh[32];
@@ -799,8 +891,8 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     const int cnt = a.ucount[0];
     const int e = a.uids[u];
     if (threadIdx.x < 64) {
-        const int m = threadIdx.x;
-        const int code = m < a.maxm && m < 32 ? a.members[(size_t)u * a.maxm + m] : -1;
+        const int m = threadIdx.x, mm = mtile * 32 + m;
+        const int code = m < 32 && mm < a.maxm ? a.members[(size_t)u * a.maxm + mm] : -1;
         const int rp = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
         if (m < 32) rows_sh[m] = rp;
         const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
@@ -910,9 +1002,15 @@ extern "C" int esp_group(const int32_t* pick, int32_t* uids, int64_t maxu, int32
     ESP_REQUIRE(pick && uids && ucount && members, "group: null pointer");
     ESP_REQUIRE(E >= 1 && E <= MAX_GROUP_IDS, "too many experts for the grouping kernel");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
-    ESP_REQUIRE(R >= 1 && R * slots <= MAX_PICKS, "grouping window too large");
+    ESP_REQUIRE(R >= 1 && R * slots <= (int64_t(1) << 24), "grouping window too large");
     ESP_REQUIRE(maxu >= (R * slots < E ? R * slots : E), "uids too small");
     ESP_REQUIRE(maxm >= 1, "members too small");
+    if (R * slots > MAX_PICKS) {                     // past one workgroup's shared memory: a workgroup an id
+        ESP_REQUIRE(maxm <= GW_MAX_M, "group: at most 16384 members an expert");
+        group_wide_kernel<<<(unsigned)E, GW, (size_t)maxm * 4, (hipStream_t)stream>>>(
+            pick, (int)(R * slots), (int)slots, (int)E, (int)maxm, uids, ucount, members);
+        return esp_host::launch_check("group (wide)");
+    }
     group_kernel<<<1, GT, 0, (hipStream_t)stream>>>(pick, uids, ucount, members, (int)R, (int)slots, (int)E,
                                                      (int)maxm);
     return esp_host::launch_check("group");
@@ -1022,12 +1120,24 @@ extern "C" int esp_group_shared(const int32_t* pick_in, const float* wts_in, con
     ESP_REQUIRE(pick_in && wts_in && pick_out && wts_out && uids && ucount && members, "group_shared: null pointer");
     ESP_REQUIRE(E >= 1 && E <= MAX_GROUP_IDS, "too many experts for the grouping kernel");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
-    ESP_REQUIRE(R >= 1 && R * slots <= MAX_PICKS, "grouping window too large");
+    ESP_REQUIRE(R >= 1 && R * slots <= (int64_t(1) << 24), "grouping window too large");
     ESP_REQUIRE(!has || (gate_w && x), "a shared slot needs its gate weight");
     ESP_REQUIRE(!has || (x_dtype == ESP_BF16 || x_dtype == ESP_F16), "x: bf16/fp16");
     ESP_REQUIRE(!has || (H % 256 == 0 && x_stride % 4 == 0), "group_shared: H must be a multiple of 256");
     ESP_REQUIRE(maxu >= (R * slots < E ? R * slots : E), "uids too small");
     ESP_REQUIRE(maxm >= 1, "members too small");
+    if (R * slots > MAX_PICKS) {                     // past one workgroup's shared memory: the tables, then the grouping
+        ESP_REQUIRE(maxm <= GW_MAX_M, "group_shared: at most 16384 members an expert");
+        hipStream_t st = (hipStream_t)stream;
+        shared_slots_kernel<<<(unsigned)((R + 3) / 4), 256, 0, st>>>(
+            pick_in, wts_in, static_cast<const uint16_t*>(x), (int)x_stride, x_dtype == ESP_BF16,
+            static_cast<const uint16_t*>(gate_w), (int)H, (int)shared_id, pick_out, wts_out, (int)R, (int)slots_in);
+        const int rc = esp_host::launch_check("group_shared (slots)");
+        if (rc) return rc;
+        group_wide_kernel<<<(unsigned)E, GW, (size_t)maxm * 4, st>>>(pick_out, (int)(R * slots), (int)slots, (int)E,
+                                                                      (int)maxm, uids, ucount, members);
+        return esp_host::launch_check("group_shared (wide)");
+    }
     group_shared_kernel<<<1, GT, 0, (hipStream_t)stream>>>(
         pick_in, wts_in, static_cast<const uint16_t*>(x), (int)x_stride, x_dtype == ESP_BF16,
         static_cast<const uint16_t*>(gate_w), (int)H, (int)shared_id, pick_out, wts_out, uids, ucount, members,
@@ -1063,12 +1173,15 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     ESP_REQUIRE(mats == 1 || mats == 2, "mats must be 1 or 2");
     ESP_REQUIRE(SK >= 1 && K > 0 && N > 0 && K % (32 * SK) == 0 && N % 128 == 0, "K and N must split evenly");
     ESP_REQUIRE(z_numel >= mats * SK * P * N, "Z too small");
-    ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
+    ESP_REQUIRE(maxm >= 1 && maxm <= 65536, "members a row of the table: 1 to 65536");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
     ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
     ESP_REQUIRE(warps == 4 || warps == 8 || warps == 16, "warps (waves a workgroup) must be 4, 8 or 16");
+    const int64_t mt = (maxm + 31) / 32;                 // an expert's members in tiles of 32 (experts_grouped.cuh:244)
+    ESP_REQUIRE(mats * SK * mt <= 65535, "grouped: too many member tiles, splits and matrices for one launch");
     if (nexp_max <= 0) return esp_host::ok();
     GroupedArgs a{};
+    a.mt = (int)mt;
     a.X0 = static_cast<const uint16_t*>(X0);
     a.X1 = static_cast<const uint16_t*>(X1);
     a.TP0 = TP0;
@@ -1089,7 +1202,7 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.slots = (int)slots;
     a.lo = (int)lo;
     a.hi = (int)hi;
-    dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK));
+    dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK * mt));
     const size_t stage = (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;     // the widest expert's stages
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
     const size_t smem = stage > red ? stage : red;
@@ -1133,6 +1246,7 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
     ESP_REQUIRE(counters_numel >= nexp_max * (N / 128) * CNT_STRIDE, "counters: 32 ints per (expert, 128 columns)");
     if (nexp_max <= 0) return esp_host::ok();
     GroupedArgs a{};
+    a.mt = 1;
     a.X0 = a.X1 = nullptr;
     a.TP0 = TP0;
     a.TP1 = TP1;

@@ -45,6 +45,7 @@ ACT_F32 = 1
 # ESPALIER_MOE_FUSED=0 turns it off.
 FUSED = env("ESPALIER_MOE_FUSED", "1") != "0"
 FUSED_ROWS = 4
+PREFILL_WAVES = 4          # waves a workgroup of the whole-prompt (prefill) grouped launches
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 
@@ -362,6 +363,91 @@ def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
             route(x[rows], gate, k, L, s)
         routed2(x[rows], None if pick is None else pick[rows], None if wts is None else wts[rows], L, s,
                 out=out[rows], out_shared=None if shared_out is None else shared_out[rows], k=k)
+    return out, shared_out
+
+
+class PrefillScratch:
+    """The buffers of one whole-prompt MoE pass (prefill) for up to `rows` tokens of `slots` picks: the pipeline's
+    tables and activations for P = rows * slots slot rows, the grouping over the whole prompt (members [maxu][rows]),
+    and the window tables route_group writes (its window grouping is not used)."""
+
+    def __init__(self, E: int, D: int, I: int, rows: int, slots: int, device, window: int = 32):
+        self.rows, self.slots, self.E, self.window = rows, slots, E, window
+        P = rows * slots
+        maxu = min(P, E)
+        wmax = min(window * slots, E)
+        f16, f32, i32 = torch.float16, torch.float32, torch.int32
+        layout = {
+            "xg": ((P, D), f16, 0), "xu": ((P, D), f16, 0), "xd": ((P, I), f16, 0),
+            "z": ((P * max(2 * I, D),), f32, 0),                     # one K split: the partials are the sums
+            "y": ((P, D), f32, 0),
+            "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
+            "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
+            "route_counter": ((1,), i32, 0), "logits": ((window * E,), f32, 0),
+            "win_ids": ((wmax,), i32, 0), "win_count": ((1,), i32, 0), "win_members": ((wmax * window,), i32, -1),
+        }
+        for name, (shape, dtype, fill) in layout.items():
+            setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
+
+    def grouping(self, T: int):
+        maxu = min(T * self.slots, self.E)
+        return self.ids[:maxu], self.members[:maxu * T].view(maxu, T)
+
+
+_PREFILL: dict = {}
+
+
+def prefill_scratch(layer: Layer, rows: int, slots: int, device) -> PrefillScratch:
+    """The PrefillScratch shared by every layer of this layer's shape, for prompts of up to `rows` tokens."""
+    key = (layer.E, layer.D, layer.I, slots, str(device))
+    found = _PREFILL.get(key)
+    if found is None or found.rows < rows:
+        found = _PREFILL[key] = PrefillScratch(layer.E, layer.D, layer.I, rows, slots, device)
+    return found
+
+
+def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: PrefillScratch,
+            k: int, gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            out_shared: torch.Tensor | None = None):
+    """The MoE layer over a whole prompt (ESPALIER_PREFILL_MODE=tile): the picks of every token (vLLM's, or route_group
+    over windows of s.window tokens, the bits decode gives them), ONE grouping of all of them, and the expert GEMMs
+    over that grouping with one K split, so each picked expert's weights are decoded once for all its member rows
+    (in tiles of 32) instead of once a 32-token window. Returns (routed sum, shared output or None), [T, D] in x's
+    dtype; a token's output depends on its own picks and rows only (the K split is fixed), not on the other tokens."""
+    e = ext()
+    T = x.shape[0]
+    has_shared = L.shared_id >= 0
+    slots = k + has_shared
+    if T > s.rows or slots != s.slots:
+        raise ValueError(f"{T}x{slots} slots but the prefill scratch holds {s.rows}x{s.slots}")
+    P = T * slots
+    ids, members = s.grouping(T)
+    pick_p, wts_p = s.pick[:P], s.wts[:P]
+    if pick is None:
+        if gate is None:
+            raise ValueError("prefill needs the picks or the router weight")
+        for r0 in range(0, T, s.window):
+            R = min(s.window, T - r0)
+            wmax = min(R * slots, L.E)
+            e.route_group(x[r0:r0 + R], gate, L.gate_w, k, L.shared_id, s.logits, s.route_counter,
+                          s.pick[r0 * slots:(r0 + R) * slots], s.wts[r0 * slots:(r0 + R) * slots], s.win_ids[:wmax],
+                          s.win_count, s.win_members[:wmax * R].view(wmax, R))
+        e.group(pick_p, ids, s.count, members, T, slots, L.E)
+    else:
+        e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, T, k,
+                       L.E)
+    e.rot_in(x, x.stride(0), pick_p, L.suh_g, L.suh_u, s.xg, s.xu, T, L.D, slots, L.E)
+    e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
+              L.D, L.I, P, 1, slots, 8, PREFILL_WAVES, 2, *L.k2_gu)
+    e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, 1, slots, L.E, math.inf, ACT_F32)
+    t, b, c = L.ptr[2], L.k2[2], L.cb[2]
+    e.grouped(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.z, 1, L.I, L.D, P, 1, slots, 8, PREFILL_WAVES,
+              2, *L.k2_d)
+    out = torch.empty((T, L.D), dtype=x.dtype, device=x.device) if out is None else out
+    if has_shared and out_shared is None:
+        out_shared = torch.empty((T, L.D), dtype=x.dtype, device=x.device)
+    shared_out = out_shared if has_shared else None
+    e.down_combine2(s.z, pick_p, L.svh_d, s.y, wts_p, out, shared_out, T, P, L.D, 1, slots, L.E, k)
     return out, shared_out
 
 

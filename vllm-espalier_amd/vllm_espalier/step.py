@@ -166,6 +166,38 @@ class SyntheticDecoder:
             e.argmax(b.logits, b.ids_out, b.argmax_part, b.argmax_cnt)
         return b
 
+    def prefill_buffers(self, T: int) -> Buffers:
+        key = ("prefill", T)
+        if key not in self._bufs:
+            self._bufs[key] = Buffers(T, self.vocab, self.dev)
+        return self._bufs[key]
+
+    def prefill(self, T: int, head_rows: int = 1) -> Buffers:
+        """A whole prompt of T tokens (prefill_buffers(T).ids_in) in the tile mode: the dense layers in windows of
+        MAX_ROWS rows (qkv then o as one chained launch), every layer's MoE over the whole prompt (experts.prefill:
+        routing in windows, one grouping, each picked expert decoded once), then the head and argmax on the last
+        head_rows tokens. Rows still never interact, but a row's bits are those of the tile mode, not of decode."""
+        b = self.prefill_buffers(T)
+        e = ext()
+        W = Dn.MAX_ROWS
+        e.embed(b.ids_in, self.embedding, b.h)
+        L0 = self.layers[0]
+        ps = G.prefill_scratch(L0.moe, T, TOPK + 1, self.dev)
+        q = b.qkv[:, :Q_OUT]
+        for i, L in enumerate(self.layers):
+            d1, d2 = (None, None) if i == 0 else (b.moe, b.moe_shared)
+            e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
+            for r0 in range(0, T, W):
+                rows = slice(r0, r0 + W)
+                L.attn.forward([b.a[rows], q[rows]], [b.qkv[rows], b.o[rows]])
+            e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
+            G.prefill(b.a, None, None, L.moe, ps, TOPK, gate=L.router, out=b.moe, out_shared=b.moe_shared)
+        e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
+        tail = slice(T - head_rows, T)
+        self.head.forward(b.a[tail], out=b.logits[tail])
+        e.argmax(b.logits[tail], b.ids_out[tail])
+        return b
+
     def algorithmic_bytes(self, picks: list[torch.Tensor], tokens: int, head: bool = True) -> int:
         """Weight bytes a pass over `tokens` rows reads: trellis + suh + svh of q/k/v/o, of the shared expert and of
         every distinct routed expert picked (picks from an eager forward), the bf16 router, the RMSNorm weights, one
