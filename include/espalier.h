@@ -208,15 +208,17 @@ typedef struct esp_dense_group {
 /* Up to 4 dense launches (esp_dense's arithmetic and bits, group by group) in one launch, with M <= 32 rows and W waves
  * a workgroup for every group. No counterpart in the reference, which launches each vLLM layer on its own: this runs a
  * layer's dense launches -- independent ones side by side, or a chain such as qkv then o (after_previous) -- as one
- * grid, so one launch gap and one weight-landing latency serve them all. A consumer group's workgroups issue their
- * first trellis copies, then wait for the producer's column blocks (its finishers store y device-coherently and count
- * the block done); workgroups are dispatched in id order and producers come first, so the wait ends, and a wait past
- * ~20 ms sets ESP_STATUS_WAIT_TIMEOUT (esp_status) instead of hanging. Every group's input rotation must be the fused
- * one (M * (K / SK) * 2 <= rot_smem). Scratch: Z (z_numel >= sum over groups of SK * M * sum(n_cols), each rounded up
- * to 64 floats; at most 2^30 floats a group), counters (8-byte aligned, counters_numel >= 32 * sum over groups of
- * sum(n_cols)/128 + 64 * n_groups; zero before a buffer's first launch. The split-K counters are left zero; the last
- * 64 ints a group hold 64-bit running counts of the chain's hand-offs, which only grow, so one buffer serves one chain
- * of groups for the life of the process). */
+ * grid, so one launch gap and one weight-landing latency serve them all. A consumer group's x must be whole 128-column
+ * blocks of the producer's y (same dtype and row stride, x - y a multiple of 128 elements, every column an output of
+ * the producer). Its workgroups issue their first trellis copies, then wait for just the producer column blocks that
+ * hold their K range (the producer's finishers store y device-coherently and count their block done); workgroups are
+ * dispatched in id order and producers come first, so the waits end, and a wait past ~20 ms sets
+ * ESP_STATUS_WAIT_TIMEOUT (esp_status) instead of hanging. Every group's input rotation must be the fused one
+ * (M * (K / SK) * 2 <= rot_smem). Scratch: Z (z_numel >= sum over groups of SK * M * sum(n_cols), each rounded up to
+ * 64 floats; at most 2^30 floats a group), counters (8-byte aligned, counters_numel >= 96 * B with B = sum over groups
+ * of sum(n_cols)/128; zero before a buffer's first launch. The first 32 * B ints, split-K arrivals, are left zero; the
+ * rest hold 64-bit running counts of the chain's hand-offs, two a column block, which only grow, so one buffer serves
+ * one chain of groups for the life of the process). */
 int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, int64_t M, int64_t W, float* Z, int64_t z_numel,
                     int32_t* counters, int64_t counters_numel, int64_t rot_smem, void* stream);
 

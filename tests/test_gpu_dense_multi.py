@@ -54,26 +54,28 @@ def test_multi_independent_block_equals_separate(dev, ext, M):
             assert torch.equal(o.view(torch.int16), w.view(torch.int16)), f"group {i}"
 
 
+@pytest.mark.parametrize("off", [0, 1024])
 @pytest.mark.parametrize("M", [1, 4, 32])
-def test_multi_chain_qkv_then_o(dev, ext, M):
-    """o reads q (the first 4096 columns of qkv's output) inside the launch, waiting for qkv's column blocks."""
-    print(f"dense_multi chain qkv -> o M={M}", flush=True)
+def test_multi_chain_qkv_then_o(dev, ext, M, off):
+    """o reads 4096 columns of qkv's output from column `off` inside the launch, each workgroup waiting for the qkv
+    column blocks that hold its x (at off 1024 those span all three of qkv's matrices)."""
+    print(f"dense_multi chain qkv -> o M={M} off={off}", flush=True)
     qkv, o = _layers(BLOCK[:2], 80 + M, dev)
     x = torch.randn((M, 2048), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
     y1 = qkv.forward(x).clone()
-    y2 = o.forward(y1[:, :4096]).clone()
+    y2 = o.forward(y1[:, off:off + 4096]).clone()
     multi = Dn.DenseMulti([qkv, o], after=[False, True], W=W)
     for _ in range(3):
         a = torch.full((M, 5120), float("nan"), dtype=torch.bfloat16, device=dev)
         b = torch.full((M, 2048), float("nan"), dtype=torch.bfloat16, device=dev)
-        multi.forward([x, a[:, :4096]], [a, b])
+        multi.forward([x, a[:, off:off + 4096]], [a, b])
         _clean(ext, multi)
         assert torch.equal(a.view(torch.int16), y1.view(torch.int16))
         assert torch.equal(b.view(torch.int16), y2.view(torch.int16))
     # and the chain's o meets the parity bar against the oracle (fed the GPU's q)
     m = o.mats[0]
     Wt = O.dequant_f32(m.trellis.cpu().numpy(), 2 * m.K, G.KERNEL_CB[m.cb])
-    ref = O.linear_ref(O.bf16_to_f32(bits(y1[:, :4096])), Wt, bits(m.suh), bits(m.svh))
+    ref = O.linear_ref(O.bf16_to_f32(bits(y1[:, off:off + 4096])), Wt, bits(m.suh), bits(m.svh))
     assert O.rel_l2(b.float().cpu().numpy(), ref) < 2e-2
 
 
@@ -139,3 +141,10 @@ def test_multi_rejects_bad_groups(dev, ext):
                          torch.empty((1, 2048), dtype=torch.bfloat16, device=dev)],
                         [8, 8], [7, 7], [qkv.plans[0][0], o.plans[0][0]], [0, 0], Dn.scratch(dev, 0, 0)[0],
                         multi.counters[:10], W, Dn.ROT_SMEM)
+    a = torch.empty((1, 5120), dtype=torch.bfloat16, device=dev)
+    b = torch.empty((1, 2048), dtype=torch.bfloat16, device=dev)
+    chain = Dn.DenseMulti([qkv, o], after=[False, True], W=W)
+    for xo_bad in (xo, a[:, 64:4160]):                         # not the producer's output; not on a block edge
+        with pytest.raises(RuntimeError, match="previous group"):
+            chain.forward([x, xo_bad], [a, b])
+    _clean(ext, chain)

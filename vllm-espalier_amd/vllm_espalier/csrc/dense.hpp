@@ -44,14 +44,15 @@ struct DenseArgs {
     uint16_t* nh_out;
     float neps;
     int norm;
-    // a group of a multi launch (esp_dense_multi); all null / zero in a plain launch. The counters only grow: in the
-    // n-th launch (from 0) a producer's finishers take done from n * blocks to (n + 1) * blocks, and a consumer
-    // workgroup's ticket (its pass count, taken when it starts) tells it n.
-    unsigned long long* done;        // this group's finished column blocks, or null
-    const unsigned long long* wait_done;   // the producer group's done: x is its output
-    unsigned long long* pass;        // this group's workgroups started (tickets)
-    int wait_total;                  // the producer's column blocks
-    int pass_total;                  // this group's workgroups
+    // a group of a multi launch (esp_dense_multi); all null / zero in a plain launch. Counters are 64-bit, one a
+    // column block, DONE_STRIDE apart, and only grow: in the n-th launch (from 0) a producer block's finisher takes its
+    // done count to n + 1, and a consumer workgroup's ticket (its block's pass count, taken when it starts) / SK is n.
+    unsigned long long* done;              // producer: done counts of its column blocks, or null
+    const unsigned long long* wait_done;   // consumer: the producer's done counts (x is the producer's y)
+    unsigned long long* pass;              // consumer: its column blocks' ticket counts
+    int wait_off;                          // consumer: x's first column in the producer's y, in 128-column blocks
+    int wp_n;                              // consumer: the producer's shards, as y column blocks [wp_c0, + wp_nb)
+    int wp_c0[4], wp_nb0[4], wp_nb[4];     //   holding the producer's column blocks wp_nb0 ...
     int case_id;             // cb * 32 + k2 of the group (the multi kernel's instance)
 };
 
@@ -98,16 +99,19 @@ __device__ __forceinline__ RotIn rot128_load_dev(const void* x, int x_dtype, siz
 
 // A consumer workgroup of a multi launch waits for its producer group: nothing outside a multi launch; the multi
 // launch's wait is defined in dense_multi.hip, before its kernel
-template <bool MULTI>
-__device__ __forceinline__ void dense_wait_producer(const DenseArgs& a, unsigned long long ticket);
-template <>
-__device__ __forceinline__ void dense_wait_producer<false>(const DenseArgs&, unsigned long long) {}
+constexpr int DONE_STRIDE = 16;            // 64-bit counters between two column blocks' (one 128-byte line each)
 
-// After a finisher's y stores: drain them, then count the column block done for the consumer group
-__device__ __forceinline__ void signal_done(const DenseArgs& a) {
+template <bool MULTI>
+__device__ __forceinline__ void dense_wait_producer(const DenseArgs& a, unsigned long long ticket, int c0, int chunks);
+template <>
+__device__ __forceinline__ void dense_wait_producer<false>(const DenseArgs&, unsigned long long, int, int) {}
+
+// After a finisher's y stores: drain them, then count column block nbg done for the consumer group
+__device__ __forceinline__ void signal_done(const DenseArgs& a, int nbg) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(a.done, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(a.done + (size_t)nbg * DONE_STRIDE, 1ull, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
 }
 // the finished outputs of one row's 128 columns from their fp32 sums, 4 a lane: H / sqrt(128), * c, * svh
 // (dense.cu:120-128); sv holds the lane's 4 svh values (fp16 bits), loaded when the workgroup starts
@@ -130,7 +134,8 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     // a consumer group's ticket, taken first so its round trip overlaps the producer's work
     unsigned long long ticket = 0;
     if (MULTI && a.wait_done && threadIdx.x == 0)
-        ticket = __hip_atomic_fetch_add(a.pass, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket = __hip_atomic_fetch_add(a.pass + (size_t)nbg * DONE_STRIDE, 1ull, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
     // What the first copy needs -- every shard's trellis pointer, first block and width, the split and the launch
     // shape -- in one round of kernel-argument loads, consumed together by one empty asm: an indexed load of the
     // workgroup's shard would wait for the shard's selection, and each later first use for its own round trip.
@@ -236,7 +241,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             }
         } else if (MULTI && a.wait_done) {
             // x is the output of the producer group of this launch: wait for it, then read it device-coherently
-            dense_wait_producer<MULTI>(a, ticket);
+            dense_wait_producer<MULTI>(a, ticket, c0, chunks);
             for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
                 const int r = idx / chunks, ch = idx % chunks;
                 const int kb = (c0 + ch) * 128;
@@ -299,7 +304,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             finish(v, l32, sv, S.scale);
             store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
         }
-        if (coherent) signal_done(a);
+        if (coherent) signal_done(a, nbg);
         return;
     }
     // 4. K splits: partials to Z, the last split of the block to arrive adds them in split order and finishes
@@ -331,7 +336,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
         }
         if (threadIdx.x == 0) store_dev(cnt_p, 0);
-        if (coherent) signal_done(a);
+        if (coherent) signal_done(a, nbg);
         return;
     }
     for (int r = wave * 2 + half; r < M; r += 2 * NW) {
@@ -356,7 +361,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
         store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
     }
     if (threadIdx.x == 0) store_dev(cnt_p, 0);  // every split of the block arrived
-    if (coherent) signal_done(a);
+    if (coherent) signal_done(a, nbg);
 }
 
 }  // namespace esp

@@ -7,22 +7,37 @@ namespace esp {
 // Device status of the dense launches (read and cleared by esp_status through dense_status)
 __device__ int g_dense_status;
 
-// Thread 0 waits until the producer's done count reaches this launch's target, (n + 1) * blocks with n = ticket /
-// the group's workgroups, for at most ~20 ms of device time: past that it records ESP_STATUS_WAIT_TIMEOUT and goes on,
-// so a launch can never hang. Nothing is reset (the counters are 64-bit).
+// Wave 0 waits for the producer's column blocks that hold the workgroup's x chunks [c0, c0 + chunks), a lane a block:
+// in the n-th launch (n = ticket / SK) each must be counted done n + 1 times. A wait runs for at most ~20 ms of device
+// time: past that it records ESP_STATUS_WAIT_TIMEOUT and goes on, so a launch can never hang. Nothing is reset (the
+// counts are 64-bit).
 template <>
-__device__ __forceinline__ void dense_wait_producer<true>(const DenseArgs& a, unsigned long long ticket) {
-    if (threadIdx.x == 0) {
-        const unsigned long long target = (ticket / (unsigned)a.pass_total + 1ull) * (unsigned)a.wait_total;
+__device__ __forceinline__ void dense_wait_producer<true>(const DenseArgs& a, unsigned long long ticket, int c0,
+                                                          int chunks) {
+    if (threadIdx.x < 64) {
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)ticket);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(ticket >> 32));
+        const unsigned long long target = (((unsigned long long)hi << 32) | lo) / (unsigned)a.SK + 1ull;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();        // 100 MHz
-        while (load_dev(a.wait_done) < target) {
-            __builtin_amdgcn_s_sleep(4);
-            if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
-                __hip_atomic_fetch_or(&g_dense_status, ESP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-                break;
+        bool late = false;
+        for (int i = (int)threadIdx.x; i < chunks && !late; i += 64) {
+            const int yb = a.wait_off + c0 + i;                       // the x chunk's column block in the producer's y
+            int pb = 0;
+#pragma unroll
+            for (int s = 0; s < MAX_SHARDS; ++s)
+                if (s < a.wp_n && yb >= a.wp_c0[s] && yb < a.wp_c0[s] + a.wp_nb[s]) pb = a.wp_nb0[s] + yb - a.wp_c0[s];
+            const unsigned long long* p = a.wait_done + (size_t)pb * DONE_STRIDE;
+            while (load_dev(p) < target) {
+                __builtin_amdgcn_s_sleep(2);
+                if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
+                    late = true;
+                    break;
+                }
             }
         }
+        if (late)
+            __hip_atomic_fetch_or(&g_dense_status, ESP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
 }
@@ -96,17 +111,17 @@ extern "C" int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, 
     int64_t z_off = 0, c_off = 0;
     size_t smem = 0;
     int mg = 1;
-    // the group's own counters first (split-K arrivals, 32 ints a column block), then two lines a group: its done
-    // count and its pass count
-    int64_t lines = 0;
+    // the groups' split-K arrival counters first (32 ints a column block), then two 128-byte lines a column block of
+    // every group: its done count (a producer's) and its ticket count (a consumer's)
+    int64_t blocks = 0;
+    int64_t nbs[MAX_GROUPS] = {};
     for (int g = 0; g < n_groups; ++g) {
-        int64_t nb = 0;
-        for (int s = 0; s < groups[g].n_shards && s < MAX_SHARDS; ++s) nb += groups[g].n_cols[s] / 128;
-        lines += nb;
+        for (int s = 0; s < groups[g].n_shards && s < MAX_SHARDS; ++s) nbs[g] += groups[g].n_cols[s] / 128;
+        blocks += nbs[g];
     }
-    const int64_t link_base = lines * CNT_STRIDE;
-    ESP_REQUIRE(counters_numel >= link_base + 2 * n_groups * CNT_STRIDE,
-                "dense_multi: counters need 32 ints a column block of every group, and 64 a group");
+    const int64_t link_base = blocks * CNT_STRIDE;
+    ESP_REQUIRE(counters_numel >= 3 * link_base,
+                "dense_multi: counters need 96 ints a column block of every group");
     for (int g = 0; g < n_groups; ++g) {
         const esp_dense_group& G = groups[g];
         ESP_REQUIRE(G.n_shards >= 1 && G.n_shards <= MAX_SHARDS, "dense_multi: 1 to 4 matrices a group");
@@ -133,14 +148,36 @@ extern "C" int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, 
         z_off += zg;
         c_off += nb * CNT_STRIDE;
     }
-    for (int g = 1; g < n_groups; ++g) {
+    unsigned long long* link = reinterpret_cast<unsigned long long*>(counters + link_base);
+    for (int g = 0, lb = 0; g < n_groups; lb += 2 * (int)nbs[g], ++g) {
+        if (g + 1 < n_groups && groups[g + 1].after_previous) m.g[g].done = link + (size_t)lb * DONE_STRIDE;
         if (!groups[g].after_previous) continue;
-        unsigned long long* link = reinterpret_cast<unsigned long long*>(counters + link_base);
-        m.g[g - 1].done = link + (2 * (g - 1)) * (CNT_STRIDE / 2);
-        m.g[g].wait_done = m.g[g - 1].done;
-        m.g[g].wait_total = m.nbt[g - 1];
-        m.g[g].pass = link + (2 * g + 1) * (CNT_STRIDE / 2);
-        m.g[g].pass_total = m.start[g + 1] - m.start[g];
+        // x must be a slice of whole 128-column blocks of the producer's y, every one of them an output of the producer
+        const esp_dense_group &P = groups[g - 1], &C = groups[g];
+        ESP_REQUIRE(C.x_dtype == P.y_dtype && C.x_stride == P.y_stride,
+                    "dense_multi: a group after the previous group reads its output (same dtype and row stride)");
+        const int64_t esz = P.y_dtype == ESP_F32 ? 4 : 2;
+        const intptr_t d = (const char*)C.x - (const char*)P.y;
+        ESP_REQUIRE(d >= 0 && d % (128 * esz) == 0 && d / esz + C.K <= P.y_cols,
+                    "dense_multi: x of a group after the previous one starts at a multiple of 128 columns of the "
+                    "previous group's y, inside its rows");
+        DenseArgs& A = m.g[g];
+        A.wait_off = (int)(d / esz / 128);
+        A.wp_n = m.g[g - 1].n;
+        for (int s = 0; s < A.wp_n; ++s) {
+            const Shard& S = m.g[g - 1].s[s];
+            ESP_REQUIRE(S.col0 % 128 == 0, "dense_multi: a producer's output columns start at a multiple of 128");
+            A.wp_c0[s] = S.col0 / 128;
+            A.wp_nb0[s] = S.nb0;
+            A.wp_nb[s] = S.nb;
+        }
+        for (int64_t yb = A.wait_off; yb < A.wait_off + C.K / 128; ++yb) {
+            bool covered = false;
+            for (int s = 0; s < A.wp_n; ++s) covered |= yb >= A.wp_c0[s] && yb < A.wp_c0[s] + A.wp_nb[s];
+            ESP_REQUIRE(covered, "dense_multi: every column of x must be an output of the previous group");
+        }
+        A.wait_done = m.g[g - 1].done;
+        A.pass = link + (size_t)(lb + nbs[g]) * DONE_STRIDE;
     }
     hipStream_t st = (hipStream_t)stream;
     const int rc = mg == 1 ? launch_multi<1>(m, (int)W, smem, st) : launch_multi<2>(m, (int)W, smem, st);

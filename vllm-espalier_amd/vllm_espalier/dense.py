@@ -202,10 +202,10 @@ class DenseMulti:
         self.W = W
         device = self.layers[0].mats[0].trellis.device
         blocks = sum(d.launches[0].n // 128 for d in self.layers)
-        # the split-K arrival counters (left zero by every launch), then a chain's 64-bit running hand-off counts
+        # the split-K arrival counters (left zero by every launch), then a chain's 64-bit running hand-off counts (a
+        # column block's done count and its ticket count)
         self.split_counters = COUNTER_STRIDE * blocks
-        self.counters = torch.zeros(self.split_counters + COUNTER_STRIDE * 2 * len(self.layers), dtype=torch.int32,
-                                    device=device)
+        self.counters = torch.zeros(3 * self.split_counters, dtype=torch.int32, device=device)
         z = sum(-(-(d.launches[0].sk * MAX_ROWS * d.launches[0].n) // 64) * 64 for d in self.layers)
         scratch(device, z, 0)
 
