@@ -268,6 +268,29 @@ void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optiona
                          members.size(1), cur_stream()));
 }
 
+// route_group's routing over any number of rows, without the grouping (no reference counterpart)
+void route_rows(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
+                int64_t shared_id, at::Tensor logits, at::Tensor counters, at::Tensor pick_out, at::Tensor wts_out) {
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1 && gate.is_contiguous(), "x / gate layout");
+    TORCH_CHECK(gate.scalar_type() == x.scalar_type(), "gate and x must share a dtype");
+    check(logits, at::kFloat, "logits");
+    check(counters, at::kInt, "counters");
+    check(pick_out, at::kInt, "pick_out");
+    check(wts_out, at::kFloat, "wts_out");
+    TORCH_CHECK(gate.dim() == 2 && gate.size(1) == x.size(1), "gate: [E, H]");
+    if (sgate.has_value())
+        TORCH_CHECK(sgate->scalar_type() == x.scalar_type() && sgate->is_contiguous() && sgate->numel() == x.size(1),
+                    "sgate: x's dtype, [H]");
+    const int64_t R = x.size(0), H = x.size(1), E = gate.size(0);
+    const int64_t slots = k + (shared_id >= 0);
+    TORCH_CHECK(pick_out.numel() >= R * slots && wts_out.numel() >= R * slots, "pick / wts too small");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_route_rows(x.data_ptr(), dtype_code(x), x.stride(0), R, H, gate.data_ptr(), E,
+                        sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits),
+                        logits.numel(), mptr<int32_t>(counters), counters.numel(), mptr<int32_t>(pick_out),
+                        mptr<float>(wts_out), cur_stream()));
+}
+
 // dense with its input rows normalised in the launch (no reference counterpart): h, d1, d2 [M, K] contiguous rows
 void dense_rmsnorm(const at::Tensor& h, const c10::optional<at::Tensor>& d1, const c10::optional<at::Tensor>& d2,
                    const at::Tensor& norm_w, double eps, at::Tensor h_out, const std::vector<at::Tensor>& T,
@@ -535,6 +558,7 @@ int64_t status(bool clear) {
 PYBIND11_MODULE(espalier_ext, m) {
     m.def("had", &had);
     m.def("route_group", &route_group);
+    m.def("route_rows", &route_rows);
     m.def("dense", &dense);
     m.def("group_shared", &group_shared);
     m.def("down_combine2", &down_combine2);

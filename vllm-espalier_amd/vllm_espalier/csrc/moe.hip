@@ -211,6 +211,7 @@ struct RouteArgs {
     int* ucount;
     int* members;
     int x_stride, bf16, R, H, E, k, shared_id, maxm;
+    int win;                         // rows a window (blockIdx.y): R for esp_route_group, 32 for esp_route_rows
     // esp_route_group_rmsnorm: x = RMSNorm(h + d1) * nw (norm.hpp), made in the launch into shared memory; workgroup 0
     // stores it to na_out and the residual h + d1 to nh_out. Rows of h, d1, nh_out and na_out are x_stride apart.
     const uint16_t* nh;
@@ -249,11 +250,18 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int has = a.shared_id >= 0, C = a.E + has, slots = a.k + has;
-    const uint16_t* xrows = a.x;
+    // window blockIdx.y of a.win rows (one window, all R rows, for esp_route_group): its rows, logits, counter line
+    // and pick / weight tables
+    const int r0 = (int)blockIdx.y * a.win, R = a.R - r0 < a.win ? a.R - r0 : a.win;
+    float* const logits = a.logits + (size_t)r0 * C;
+    int* const counter = a.counter + blockIdx.y * 32;
+    int* const pick_out = a.pick_out + (size_t)r0 * slots;
+    float* const wts_out = a.wts_out + (size_t)r0 * slots;
+    const uint16_t* xrows = a.x + (size_t)r0 * a.x_stride;
     int xstride = a.x_stride;
     // this wave's router column c, rows rg, rg + 4, ...; h in groups of 2048 (4 chunks of 8 a lane)
     const int c = blockIdx.x * RT_COLS + (wave & 3), rg = wave >> 2;
-    const bool active = c < C && rg < a.R;
+    const bool active = c < C && rg < R;
     const uint16_t* w = c < a.E ? a.gate + (size_t)c * a.H : a.sgate;
     auto load8 = [&](const uint16_t* p, int h, uint2 (&v)[2]) __attribute__((always_inline)) {
         if (h < a.H) {
@@ -278,12 +286,12 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         for (int c = 0; c < NORM_CHUNKS; ++c) {
             const int i = (c * 256 + t) * 8;
             wq[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (r < a.R && i < a.H) wq[c] = *reinterpret_cast<const uint4*>(a.nw + i);
+            if (r < R && i < a.H) wq[c] = *reinterpret_cast<const uint4*>(a.nw + i);
         }
         uint4 zq[NORM_CHUNKS];
-        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, a.R, a.H, a.neps, BF16, npart, ninv, zq);
+        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, R, a.H, a.neps, BF16, npart, ninv, zq);
         uint16_t* xs = reinterpret_cast<uint16_t*>(rsmem);
-        if (r < a.R) {
+        if (r < R) {
             const size_t o = (size_t)r * a.x_stride;
 #pragma unroll
             for (int c = 0; c < NORM_CHUNKS; ++c) {
@@ -324,13 +332,13 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
             if (a.H <= 2048) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) load8(xrows + (size_t)rg * xstride, 512 * q + 8 * lane, xv[q]);
-                for (int r = rg; r < a.R; r += 4) {
-                    if (r + 4 < a.R) {
+                for (int r = rg; r < R; r += 4) {
+                    if (r + 4 < R) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q) load8(xrows + (size_t)(r + 4) * xstride, 512 * q + 8 * lane, xn[q]);
                     }
                     const double s = wave_sum_f64_dpp(dot(xv, gv, 0.0));
-                    if (lane == 0) store_dev(a.logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
+                    if (lane == 0) store_dev(logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         xv[q][0] = xn[q][0];
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
                     }
                 }
             } else {
-                for (int r = rg; r < a.R; r += 4) {
+                for (int r = rg; r < R; r += 4) {
                     double acc = 0.0;
                     for (int h0 = 0; h0 < a.H; h0 += 2048) {
 #pragma unroll
@@ -349,17 +357,17 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
                         acc = dot(xv, gv, acc);
                     }
                     const double s = wave_sum_f64_dpp(acc);
-                    if (lane == 0) store_dev(a.logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
+                    if (lane == 0) store_dev(logits + (size_t)r * C + c, c < a.E ? bf2f(f64_to_bf16(s)) : (float)s);
                 }
             }
         }
     }
-    if (!arrive_last(a.counter, (int)gridDim.x, &last)) return;
+    if (!arrive_last(counter, (int)gridDim.x, &last)) return;
 
     // 2. per row (one wave a row): k maxima of the keys, softmax weights over the picks, the shared gate's sigmoid
     const int NW = RT / 64;
-    for (int r = wave; r < a.R; r += NW) {
-        const float* lr = a.logits + (size_t)r * C;
+    for (int r = wave; r < R; r += NW) {
+        const float* lr = logits + (size_t)r * C;
         uint32_t key[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -389,25 +397,29 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         for (int t = 0; t < a.k; ++t)
             psum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_mine), t));
         if (lane < a.k) {
-            a.pick_out[r * slots + lane] = e_mine;
-            a.wts_out[r * slots + lane] = p_mine / psum;
+            pick_out[r * slots + lane] = e_mine;
+            wts_out[r * slots + lane] = p_mine / psum;
             sh_pick[r * slots + lane] = e_mine;
         }
         if (has && lane == 0) {
-            a.pick_out[r * slots + a.k] = a.shared_id;
-            a.wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
+            pick_out[r * slots + a.k] = a.shared_id;
+            wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
             sh_pick[r * slots + a.k] = a.shared_id;
         }
     }
     __syncthreads();
 
-    // 3. grouping of the picks (ids < E + has): one wave for a few
-    if (a.R * slots <= GROUP_WAVE_MAX) {
-        if (wave == 0) group_wave(sh_pick, a.R * slots, slots, C, a.maxm, a.uids, a.ucount, a.members);
-    } else {
-        group_block(sh_pick, a.R * slots, a.R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    // 3. grouping of the picks (ids < E + has): one wave for a few; none for esp_route_rows (its caller groups)
+    if (a.uids == nullptr) {
+        if (tid == 0) store_dev(counter, 0);
+        return;
     }
-    if (tid == 0) store_dev(a.counter, 0);
+    if (R * slots <= GROUP_WAVE_MAX) {
+        if (wave == 0) group_wave(sh_pick, R * slots, slots, C, a.maxm, a.uids, a.ucount, a.members);
+    } else {
+        group_block(sh_pick, R * slots, R, slots, C, a.maxm, a.uids, a.ucount, a.members, g);
+    }
+    if (tid == 0) store_dev(counter, 0);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1063,6 +1075,7 @@ static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, i
     a.k = (int)k;
     a.shared_id = (int)shared_id;
     a.maxm = (int)maxm;
+    a.win = (int)R;
     size_t smem = 0;
     if (nrm) {
         ESP_REQUIRE(nrm->h && nrm->w && nrm->h_out && nrm->a_out, "route_group_rmsnorm: null pointer");
@@ -1089,6 +1102,51 @@ static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, i
     else
         route_group_kernel<0><<<grid, RT, smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("route_group");
+}
+
+// esp_route_rows: route_group_kernel over windows of ROUTE_WIN rows side by side (blockIdx.y), without the grouping
+constexpr int ROUTE_WIN = 32;
+
+extern "C" int esp_route_rows(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
+                              int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
+                              int64_t logits_numel, int32_t* counters, int64_t counters_numel, int32_t* pick_out,
+                              float* wts_out, void* stream) {
+    const int has = shared_id >= 0;
+    ESP_REQUIRE(x && gate && logits && counters && pick_out && wts_out, "route_rows: null pointer");
+    ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
+    ESP_REQUIRE(E >= 1 && E <= 256 && k >= 1 && k <= 16 && k <= E && H % 256 == 0 && H > 0,
+                "route_rows: shape limits");
+    ESP_REQUIRE(E + has <= RT_MAX_IDS && k + has <= 32, "route_rows: too many router columns or slots");
+    ESP_REQUIRE(!has || sgate, "the shared gate weight is needed with a shared slot");
+    ESP_REQUIRE(R >= 1 && R <= 65535LL * ROUTE_WIN, "route_rows: 1 to 2097120 rows");
+    const int64_t windows = (R + ROUTE_WIN - 1) / ROUTE_WIN;
+    ESP_REQUIRE(logits_numel >= R * (E + has), "logits scratch too small");
+    ESP_REQUIRE(counters_numel >= 32 * windows, "route_rows: counters need 32 ints a window of 32 rows");
+    ESP_REQUIRE(x_stride >= H && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE(((uintptr_t)x & 7) == 0 && ((uintptr_t)gate & 7) == 0 && (!sgate || ((uintptr_t)sgate & 7) == 0),
+                "route_rows: x / gate must be 8-byte aligned");
+    RouteArgs a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.gate = static_cast<const uint16_t*>(gate);
+    a.sgate = static_cast<const uint16_t*>(sgate);
+    a.logits = logits;
+    a.counter = counters;
+    a.pick_out = pick_out;
+    a.wts_out = wts_out;
+    a.x_stride = (int)x_stride;
+    a.bf16 = x_dtype == ESP_BF16;
+    a.R = (int)R;
+    a.H = (int)H;
+    a.E = (int)E;
+    a.k = (int)k;
+    a.shared_id = (int)shared_id;
+    a.win = ROUTE_WIN;
+    const dim3 grid((unsigned)((E + has + RT_COLS - 1) / RT_COLS), (unsigned)windows);
+    if (a.bf16)
+        route_group_kernel<1><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+    else
+        route_group_kernel<0><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+    return esp_host::launch_check("route_rows");
 }
 
 extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,

@@ -369,13 +369,12 @@ def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
 class PrefillScratch:
     """The buffers of one whole-prompt MoE pass (prefill) for up to `rows` tokens of `slots` picks: the pipeline's
     tables and activations for P = rows * slots slot rows, the grouping over the whole prompt (members [maxu][rows]),
-    and the window tables route_group writes (its window grouping is not used)."""
+    and route_rows' logits and counters (one 32-int line a window of `window` = 32 rows)."""
 
     def __init__(self, E: int, D: int, I: int, rows: int, slots: int, device, window: int = 32):
         self.rows, self.slots, self.E, self.window = rows, slots, E, window
         P = rows * slots
         maxu = min(P, E)
-        wmax = min(window * slots, E)
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
         layout = {
             "xg": ((P, D), f16, 0), "xu": ((P, D), f16, 0), "xd": ((P, I), f16, 0),
@@ -383,8 +382,7 @@ class PrefillScratch:
             "y": ((P, D), f32, 0),
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
-            "route_counter": ((1,), i32, 0), "logits": ((window * E,), f32, 0),
-            "win_ids": ((wmax,), i32, 0), "win_count": ((1,), i32, 0), "win_members": ((wmax * window,), i32, -1),
+            "route_counters": ((32 * -(-rows // window),), i32, 0), "logits": ((rows * E,), f32, 0),
         }
         for name, (shape, dtype, fill) in layout.items():
             setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
@@ -409,8 +407,8 @@ def prefill_scratch(layer: Layer, rows: int, slots: int, device) -> PrefillScrat
 def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: PrefillScratch,
             k: int, gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
             out_shared: torch.Tensor | None = None):
-    """The MoE layer over a whole prompt (ESPALIER_PREFILL_MODE=tile): the picks of every token (vLLM's, or route_group
-    over windows of s.window tokens, the bits decode gives them), ONE grouping of all of them, and the expert GEMMs
+    """The MoE layer over a whole prompt (ESPALIER_PREFILL_MODE=tile): the picks of every token (vLLM's, or route_rows
+    over the whole prompt, the bits decode's route_group gives them), ONE grouping of all of them, and the expert GEMMs
     over that grouping with one K split, so each picked expert's weights are decoded once for all its member rows
     (in tiles of 32) instead of once a 32-token window. Returns (routed sum, shared output or None), [T, D] in x's
     dtype; a token's output depends on its own picks and rows only (the K split is fixed), not on the other tokens."""
@@ -426,12 +424,7 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     if pick is None:
         if gate is None:
             raise ValueError("prefill needs the picks or the router weight")
-        for r0 in range(0, T, s.window):
-            R = min(s.window, T - r0)
-            wmax = min(R * slots, L.E)
-            e.route_group(x[r0:r0 + R], gate, L.gate_w, k, L.shared_id, s.logits, s.route_counter,
-                          s.pick[r0 * slots:(r0 + R) * slots], s.wts[r0 * slots:(r0 + R) * slots], s.win_ids[:wmax],
-                          s.win_count, s.win_members[:wmax * R].view(wmax, R))
+        e.route_rows(x, gate, L.gate_w, k, L.shared_id, s.logits, s.route_counters, pick_p, wts_p)
         e.group(pick_p, ids, s.count, members, T, slots, L.E)
     else:
         e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, T, k,
