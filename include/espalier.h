@@ -73,6 +73,20 @@ int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K
               float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK,
               int64_t W, int64_t PF, int64_t rot_smem, void* stream);
 
+/* esp_dense over any number of rows (a whole prompt), for prefill: the same layer, with each weight decoded once for
+ * every 128 rows instead of once a 32-row window. No counterpart in the reference (its prefill re-decodes the weights
+ * every window, README.md:115-117, and names a dedicated prefill GEMM as planned). Arguments as esp_dense, with
+ * T >= 1 rows. Scratch: xh fp16 (xh_numel >= n_shards * ceil(T / 16) * 16 * K halves: the rows rotated once a
+ * matrix, in MFMA fragment order), and with SK > 1, Z fp32 (z_numel >= ceil(T / 128) * SK * 128 * sum(n_cols), at most
+ * 2^30 floats) and counters int32 (counters_numel >= 32 * ceil(T / 128) * sum(n_cols) / 128; zero on entry and left
+ * zero). A row's bits depend on its own input and SK only: the same for any T and any place in the prompt, but not
+ * those of esp_dense (another order of the sums). */
+int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
+                   const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
+                   const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,
+                   int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel, int64_t k2,
+                   int64_t cb, int64_t SK, void* stream);
+
 /* Replaces `route_group` (experts.cpp:214-223, route.cu:35-207): router logits x @ gate^T (+ the shared gate), top-k
  * by the exactly rounded bf16 logits (lowest id on ties), weights renormalised over the picks, the shared slot's
  * weight sigmoid(x . sgate), then the grouping of the picks. x [R][x_stride] and gate [E][H] in one dtype (bf16 or

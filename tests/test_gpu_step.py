@@ -216,3 +216,28 @@ def test_decoder_multi_attention_equals_apart(small_decoder, T, monkeypatch):
     for x, y in zip(res[False], res[True]):
         assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x,
                            y.view(torch.int16) if y.dtype == torch.bfloat16 else y)
+
+
+def test_decoder_prefill_rows_alone_equal_prompt(small_decoder):
+    """The tile prefill (prompt launches for the dense layers, routing and grouping over the whole prompt): every
+    row's logits alone (a 1-token prompt) equal that row's logits in a 70-token prompt, bit for bit, and they stay
+    close to decode's windows (another order of the sums)."""
+    dec = small_decoder
+    T = 70
+    ids = [(11 + 977 * i) % 5120 for i in range(T)]
+    b = dec.prefill_buffers(T)
+    b.ids_in.copy_(torch.tensor(ids, dtype=torch.int32))
+    dec.prefill(T, head_rows=T)
+    torch.cuda.synchronize()
+    logits, out = b.logits.cpu().clone(), b.ids_out.cpu().clone()
+    assert torch.isfinite(logits.float()).all()
+    assert torch.equal(out, torch.argmax(logits.float(), dim=1).to(torch.int32))
+    for r in (0, 31, 32, 69):
+        b1 = dec.prefill_buffers(1)
+        b1.ids_in.fill_(ids[r])
+        dec.prefill(1)
+        torch.cuda.synchronize()
+        assert torch.equal(b1.logits.cpu().view(torch.int16), logits[r:r + 1].view(torch.int16)), r
+    _, lw, _ = _run(dec, ids[:32])
+    err = (lw.float() - logits[:32].float()).norm() / lw.float().norm()
+    assert err < 2e-2, float(err)

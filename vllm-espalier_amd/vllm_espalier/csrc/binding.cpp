@@ -239,6 +239,41 @@ void dense(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vec
                    rot_smem, cur_stream()));
 }
 
+// dense over a whole prompt (no reference counterpart): x [T, K], any T
+void dense_tile(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
+                const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y, at::Tensor xh,
+                at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK) {
+    TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1, "x: CUDA [T, K], unit column stride");
+    TORCH_CHECK(y.is_cuda() && y.dim() == 2 && y.stride(1) == 1 && y.size(0) == x.size(0),
+                "y: CUDA [T, N], unit column stride");
+    TORCH_CHECK(T.size() == suh.size() && T.size() == svh.size() && T.size() == col0.size(), "one entry a matrix");
+    TORCH_CHECK(T.size() >= 1 && T.size() <= 4, "1 to 4 matrices a launch");
+    const int64_t M = x.size(0), K = x.size(1);
+    std::vector<const void*> tp, sp, vp;
+    std::vector<int64_t> ncols;
+    for (size_t s = 0; s < T.size(); ++s) {
+        TORCH_CHECK(T[s].is_cuda() && T[s].scalar_type() == at::kShort && T[s].is_contiguous() && T[s].dim() == 3,
+                    "trellis: contiguous int16 [K/16, N/16, 16K]");
+        check(suh[s], at::kHalf, "suh");
+        check(svh[s], at::kHalf, "svh");
+        TORCH_CHECK(T[s].size(0) * 16 == K && T[s].size(1) * 16 == svh[s].numel() && T[s].size(2) == 8 * k2,
+                    "matrix shape");
+        TORCH_CHECK(suh[s].numel() == K, "suh must have K elements");
+        tp.push_back(T[s].data_ptr());
+        sp.push_back(suh[s].data_ptr());
+        vp.push_back(svh[s].data_ptr());
+        ncols.push_back(svh[s].numel());
+    }
+    check(Z, at::kFloat, "Z");
+    check(counters, at::kInt, "counters");
+    check(xh, at::kHalf, "xh");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_dense_tile(x.data_ptr(), dtype_code(x), x.stride(0), M, K, (int64_t)T.size(), tp.data(), sp.data(),
+                        vp.data(), ncols.data(), col0.data(), y.data_ptr(), dtype_code(y), y.stride(0), y.size(1),
+                        xh.data_ptr(), xh.numel(), mptr<float>(Z), Z.numel(), mptr<int32_t>(counters),
+                        counters.numel(), k2, cb, SK, cur_stream()));
+}
+
 void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
                  int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out, at::Tensor wts_out,
                  at::Tensor uids, at::Tensor ucount, at::Tensor members) {
@@ -559,6 +594,7 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("had", &had);
     m.def("route_group", &route_group);
     m.def("route_rows", &route_rows);
+    m.def("dense_tile", &dense_tile);
     m.def("dense", &dense);
     m.def("group_shared", &group_shared);
     m.def("down_combine2", &down_combine2);

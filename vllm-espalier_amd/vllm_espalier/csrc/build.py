@@ -1,7 +1,7 @@
 """Build the gfx950 kernel layer in-tree with hipcc (no hipify, no JIT cache):
 
-  libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, dense_multi.hip, moe.hip,
-                       step.hip, abi.cpp)
+  libespalier_hip.so   the HIP kernels and the C ABI of include/espalier.h (dense.hip, dense_multi.hip, dense_tile.hip,
+                       moe.hip, step.hip, abi.cpp)
   espalier_ext*.so     the torch extension module (binding.cpp, host code only), linked to libespalier_hip.so
   libespalier_probe.so bench.py --probes' measurement kernels (probe.hip), apart from the kernel layer
 
@@ -55,7 +55,7 @@ def ext_suffix() -> str:
 def build_lib(jobs: int, incremental: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
-    srcs = [CSRC / "dense.hip", CSRC / "dense_multi.hip", CSRC / "moe.hip", CSRC / "step.hip", CSRC / "abi.cpp"]
+    srcs = [CSRC / "dense.hip", CSRC / "dense_multi.hip", CSRC / "dense_tile.hip", CSRC / "moe.hip", CSRC / "step.hip", CSRC / "abi.cpp"]
     objs = [BUILD / (s.stem + ".o") for s in srcs]
     headers = [*CSRC.glob("*.hpp"), REPO / "include" / "espalier.h"]
     newest_header = max(h.stat().st_mtime for h in headers)

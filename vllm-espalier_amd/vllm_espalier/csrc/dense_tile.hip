@@ -1,0 +1,310 @@
+// esp_dense_tile: a dense layer over a whole prompt (any number of rows) on gfx950, each weight decoded once for every
+// 128 rows instead of once a 32-row window.
+//
+// Two launches. (1) tile_rot_kernel rotates every row once a matrix, xh_s = fp16(H(x * suh_s) / sqrt(128)), and stores
+// it in MFMA A-fragment order: [matrix][row group of 16][32-k step][64 lanes][8 halves], one 1 KiB block a (row
+// group, step) holding exactly what v_mfma_f32_16x16x32_f16 reads from each lane (lane c + 16 G: row c, the k slots
+// of trellis.hpp's B operand). (2) dense_tile_kernel: a workgroup is 8 waves on one 128-column block, one K split and
+// one tile of up to 128 rows (8 row groups). The tile's A blocks and the block's trellis tiles reach LDS through
+// global_load_lds (no VGPRs, no VALU), double-buffered in stages of 4 steps; a wave (pair p = n tiles 2p, 2p+1; k slot
+// kw of 2) decodes its two B operands of a step once and issues 16 MFMAs with them (8 row groups x 2 tiles). The two
+// k slots' sums are added in shared memory (slot 0, then slot 1), and split K goes through Z with the last split to
+// arrive adding the splits in order and finishing, as esp_dense does.
+//
+// Row invariance: a row's sums depend only on its own A rows, the K split (a function of the caller's plan) and the
+// fixed step order, never on the other rows of the prompt or its place in a tile.
+#include "dense.hpp"
+
+namespace esp {
+
+constexpr int TILE_ROWS = 128;                  // rows a workgroup
+constexpr int TILE_RG = TILE_ROWS / 16;         // row groups a workgroup
+constexpr int TILE_WAVES = 8;                   // 4 pairs x 2 k slots
+constexpr int TILE_KW = TILE_WAVES / 4;
+constexpr int TILE_STEPS = 4;                   // 32-k steps a stage
+constexpr int TILE_FRAG = 512;                  // halves a (row group, step) block: 64 lanes x 8
+constexpr int RED_STRIDE = 132;                 // floats between two rows of the block's sums (banks apart)
+
+struct TileArgs {
+    Shard s[MAX_SHARDS];
+    int n;
+    const uint16_t* xh;      // fragment-ordered rotated rows [n][RG][K / 32][64][8]
+    void* y;
+    int y_dtype, y_stride;
+    float* Z;                // [row tiles][SK][128][NBT * 128]
+    int* counters;           // [row tiles][NBT][CNT_STRIDE]
+    int T, K, SK, NBT, SQ, SR, RG;
+};
+
+// xh of tile_rot_kernel: a 32-lane half rotates one 128-chunk of one row for one matrix; rows past T (up to the last
+// row group's end) are zero
+__global__ __launch_bounds__(256) void tile_rot_kernel(const void* __restrict__ x, int x_dtype, int x_stride, int T,
+                                                       int K, int n, const uint16_t* suh0, const uint16_t* suh1,
+                                                       const uint16_t* suh2, const uint16_t* suh3,
+                                                       uint16_t* __restrict__ xh, int RG) {
+    const int l32 = threadIdx.x & 31;
+    const int nb = K >> 7, rows = RG * 16;
+    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);      // (matrix, row, chunk)
+    if (unit >= (long)n * rows * nb) return;
+    const int ch = (int)(unit % nb);
+    const int r = (int)((unit / nb) % rows);
+    const int s = (int)(unit / ((long)nb * rows));
+    const uint16_t* suh = s == 0 ? suh0 : s == 1 ? suh1 : s == 2 ? suh2 : suh3;
+    uint2 u = make_uint2(0u, 0u);
+    if (r < T) u = rot128(x, x_dtype, (size_t)r * x_stride + ch * 128, suh + ch * 128, l32);
+    // the lane's 4 consecutive k (kabs .. kabs + 3) are 4 consecutive halves of one A fragment lane
+    const int kabs = ch * 128 + 4 * l32;
+    const int step = kabs >> 5, kk = kabs & 31, kt = kk & 15;
+    const int G = 2 * (kk >> 4) + ((kt >> 2) & 1), hi = kt >> 3;
+    const int lane = (r & 15) + 16 * G;
+    uint16_t* dst = xh + ((((size_t)s * RG + (r >> 4)) * (K >> 5) + step) * 64 + lane) * 8 + 4 * hi;
+    *reinterpret_cast<uint2*>(dst) = u;
+}
+
+typedef __attribute__((address_space(3))) const f16x8* lds_f16x8_ptr;
+
+template <int CB, int K2>
+__global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int last;
+    constexpr int TW = 4 * K2;
+    constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;            // one k tile of the block
+    constexpr int B_BUF = TILE_STEPS * 2 * ROW_WORDS;              // words a B stage
+    constexpr int A_BUF = TILE_RG * TILE_STEPS * TILE_FRAG;        // halves an A stage
+    const int nbg = blockIdx.x, split = blockIdx.y, mt = blockIdx.z;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int l32 = lane & 31, half = lane >> 5, pair = wave & 3, kw = wave >> 2, G = lane >> 4;
+
+    // the column block's matrix: its fields picked by unrolled compares (an indexed read of the argument block would
+    // copy it to private memory)
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_SHARDS; ++i)
+        if (i < a.n && nbg >= a.s[i].nb0) si = i;
+    const uint32_t* Tw = a.s[0].T;
+    const uint16_t* svh = a.s[0].svh;
+    int nb0 = a.s[0].nb0, nbs = a.s[0].nb, col0 = a.s[0].col0;
+    float scale = a.s[0].scale;
+#pragma unroll
+    for (int i = 1; i < MAX_SHARDS; ++i)
+        if (si == i) {
+            Tw = a.s[i].T;
+            svh = a.s[i].svh;
+            nb0 = a.s[i].nb0;
+            nbs = a.s[i].nb;
+            col0 = a.s[i].col0;
+            scale = a.s[i].scale;
+        }
+    const int cb_local = nbg - nb0, NTILES = nbs * 8;
+    const int s0 = split * a.SQ + (split < a.SR ? split : a.SR), steps = a.SQ + (split < a.SR);
+    const int m0 = mt * TILE_ROWS, Mt = a.T - m0 < TILE_ROWS ? a.T - m0 : TILE_ROWS, rgt = (Mt + 15) >> 4;
+    const int ksteps = a.K >> 5;
+    const uint16_t* X = a.xh + (((size_t)si * a.RG + mt * TILE_RG) * ksteps + s0) * TILE_FRAG;
+    uint16_t* sa = reinterpret_cast<uint16_t*>(smem);
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + 2 * A_BUF * 2);
+
+    // stage st of the split into buffer buf: the block's trellis tiles, then the tile's A blocks (rgt row groups x n
+    // steps of 64 16-byte units; a wave's 64 units are one block, so its LDS destination is one contiguous KiB)
+    auto issue = [&](int st, int buf) __attribute__((always_inline)) {
+        const int first = st * TILE_STEPS, n = steps - first < TILE_STEPS ? steps - first : TILE_STEPS;
+        issue_stage<K2>(Tw, NTILES, (s0 + first) * 2, 2 * n, cb_local * 8, sb + buf * B_BUF);
+        const int units = rgt * n * 64;
+        for (int u0 = wave * 64; u0 < units; u0 += TILE_WAVES * 64) {
+            const int g = u0 / (n * 64), r0 = u0 - g * n * 64;
+            const uint16_t* src = X + ((size_t)g * ksteps + first) * TILE_FRAG + (r0 + lane) * 8;
+            uint16_t* dst = sa + buf * A_BUF + (g * TILE_STEPS * 64 + r0) * 8;
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)dst, 16, 0, 0);
+        }
+    };
+
+    f32x4 acc[2][TILE_RG];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < TILE_RG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const LanePlan<K2> lp(lane);
+    const LdsWords<K2> lw(lp);
+    const int lane_base = ((G >> 1) * 8 + 2 * pair) * TW;
+    const int nst = (steps + TILE_STEPS - 1) / TILE_STEPS;
+    const uint2 sv = *reinterpret_cast<const uint2*>(svh + cb_local * 128 + 4 * l32);
+
+    issue(0, 0);
+    for (int st = 0; st < nst; ++st) {
+        wait_stage();                           // stage st landed; every wave is done with buffer (st + 1) & 1
+        if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
+        const int first = st * TILE_STEPS, n = steps - first < TILE_STEPS ? steps - first : TILE_STEPS;
+        const uint32_t* bb = sb + (st & 1) * B_BUF + lane_base;
+        const uint16_t* ab = sa + (st & 1) * A_BUF + lane * 8;
+        for (int ls = kw; ls < n; ls += TILE_KW) {
+            uint32_t w[2][6];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 6; ++i) w[j][i] = bb[ls * 2 * ROW_WORDS + j * TW + lw.off[i]];
+            f16x8 b[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = decode_b<CB, K2>(w[j], lp);
+#pragma unroll
+            for (int g = 0; g < TILE_RG; ++g) {
+                if (g < rgt) {                  // uniform: the tile's last row groups may be absent
+                    const f16x8 av = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[j], acc[j][g], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // the block's [Mt][128] sums: k slot 0's accumulators into shared memory, then slot 1's added to them
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+    const int c = lane & 15;
+#pragma unroll
+    for (int q = 0; q < TILE_KW; ++q) {
+        if (kw == q) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < TILE_RG; ++g)
+                    if (g < rgt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float* p = red + (g * 16 + 4 * G + i) * RED_STRIDE + 32 * pair + 16 * j + c;
+                            *p = q == 0 ? acc[j][g][i] : *p + acc[j][g][i];
+                        }
+        }
+        __syncthreads();
+    }
+    const int ycol = col0 + cb_local * 128 + 4 * l32;
+    const size_t yrow0 = (size_t)m0 * a.y_stride;
+    if (a.SK == 1) {
+        for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES) {
+            const float4 s4 = *reinterpret_cast<const float4*>(red + r * RED_STRIDE + 4 * l32);
+            float v[4] = {s4.x, s4.y, s4.z, s4.w};
+            finish(v, l32, sv, scale);
+            store4(a.y, a.y_dtype, yrow0 + (size_t)r * a.y_stride + ycol, v);
+        }
+        return;
+    }
+    // K splits: partials to Z, the last split of the (row tile, column block) to arrive adds them in split order
+    const size_t zrow = (size_t)a.NBT * 128, zsplit = (size_t)TILE_ROWS * zrow;
+    float* Zt = a.Z + (size_t)mt * a.SK * zsplit;
+    const DevBuf zb(a.Z);
+    for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES)
+        zb.store4(Zt + split * zsplit + r * zrow + nbg * 128 + 4 * l32,
+                  *reinterpret_cast<const float4*>(red + r * RED_STRIDE + 4 * l32));
+    int* const cnt_p = a.counters + ((size_t)mt * a.NBT + nbg) * CNT_STRIDE;
+    if (!arrive_last(cnt_p, a.SK, &last)) return;
+    for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES) {
+        const float* zp = Zt + r * zrow + nbg * 128 + 4 * l32;
+        float4 s;
+        for (int q0 = 0; q0 < a.SK; q0 += 8) {              // up to eight splits' loads in flight at once
+            float4 u[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (q0 + i < a.SK) u[i] = zb.load4(zp + (q0 + i) * zsplit);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (q0 + i == 0) {
+                    s = u[0];
+                } else if (q0 + i < a.SK) {
+                    s.x += u[i].x; s.y += u[i].y; s.z += u[i].z; s.w += u[i].w;
+                }
+            }
+        }
+        float v[4] = {s.x, s.y, s.z, s.w};
+        finish(v, l32, sv, scale);
+        store4(a.y, a.y_dtype, yrow0 + (size_t)r * a.y_stride + ycol, v);
+    }
+    if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every split of the block arrived
+}
+
+template <int KCB, int K2>
+static int launch_tile(const TileArgs& a, dim3 grid, size_t smem, hipStream_t st) {
+    auto kern = dense_tile_kernel<KCB, K2>;
+    if (smem > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "dense_tile: cannot raise the shared memory limit to %zu bytes", smem);
+    kern<<<grid, TILE_WAVES * 64, smem, st>>>(a);
+    return ESP_OK;
+}
+
+}  // namespace esp
+
+using namespace esp;
+
+extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
+                              const void* const* trellis, const void* const* suh, const void* const* svh,
+                              const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                              int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel,
+                              int32_t* counters, int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK,
+                              void* stream) {
+    ESP_REQUIRE(x && y && xh && trellis && suh && svh && n_cols && col0, "dense_tile: null pointer");
+    ESP_REQUIRE(n_shards >= 1 && n_shards <= MAX_SHARDS, "dense_tile: 1 to 4 matrices a launch");
+    ESP_REQUIRE(T >= 1, "dense_tile: at least one row");
+    ESP_REQUIRE(K > 0 && K % 128 == 0 && SK >= 1 && SK <= K / 32,
+                "dense_tile: K must be a multiple of 128 and SK at most K / 32");
+    ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "dense_tile: x / y dtype");
+    ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "dense_tile: x / y row stride");
+    if (!supported((int)cb, (int)k2))
+        return esp_host::fail(ESP_ERR_UNSUPPORTED, "unsupported codebook/width: cb=%lld k2=%lld", (long long)cb,
+                              (long long)k2);
+    TileArgs a{};
+    int nbt = 0;
+    const float c = gemm_scale((int)cb);
+    const uint16_t* su[MAX_SHARDS] = {};
+    for (int s = 0; s < n_shards; ++s) {
+        const int64_t N = n_cols[s];
+        ESP_REQUIRE(N > 0 && N % 128 == 0, "dense_tile: matrix shape");
+        ESP_REQUIRE(col0[s] >= 0 && col0[s] + N <= y_cols, "dense_tile: matrix columns past y");
+        ESP_REQUIRE(trellis[s] && suh[s] && svh[s], "dense_tile: null matrix pointer");
+        a.s[s] = Shard{static_cast<const uint32_t*>(trellis[s]), static_cast<const uint16_t*>(suh[s]),
+                       static_cast<const uint16_t*>(svh[s]), nbt, (int)(N / 128), (int)col0[s], c};
+        su[s] = static_cast<const uint16_t*>(suh[s]);
+        nbt += (int)(N / 128);
+    }
+    const int64_t RG = (T + 15) / 16, tiles = (T + TILE_ROWS - 1) / TILE_ROWS;
+    ESP_REQUIRE(tiles <= 65535, "dense_tile: at most 65535 tiles of 128 rows");
+    ESP_REQUIRE(xh_numel >= n_shards * RG * 16 * K, "dense_tile: xh needs n_shards * ceil(T / 16) * 16 * K halves");
+    ESP_REQUIRE(SK == 1 || (Z && counters && z_numel >= tiles * SK * TILE_ROWS * nbt * 128 &&
+                            counters_numel >= tiles * nbt * CNT_STRIDE),
+                "dense_tile: with SK > 1, Z needs ceil(T / 128) * SK * 128 * N floats and counters 32 ints a "
+                "(128-row tile, 128-column block)");
+    ESP_REQUIRE(tiles * SK * TILE_ROWS * nbt * 128 <= (int64_t(1) << 30), "dense_tile: the partials must fit in 4 GiB");
+    a.n = (int)n_shards;
+    a.xh = static_cast<const uint16_t*>(xh);
+    a.y = y;
+    a.y_dtype = y_dtype;
+    a.y_stride = (int)y_stride;
+    a.Z = Z;
+    a.counters = counters;
+    a.T = (int)T;
+    a.K = (int)K;
+    a.SK = (int)SK;
+    a.NBT = nbt;
+    a.SQ = (int)((K / 32) / SK);
+    a.SR = (int)((K / 32) % SK);
+    a.RG = (int)RG;
+    const size_t stage = 2 * (size_t)TILE_RG * TILE_STEPS * TILE_FRAG * 2 + 2 * (size_t)TILE_STEPS * 2 * 32 * k2 * 4;
+    const size_t red = (size_t)TILE_ROWS * RED_STRIDE * 4;
+    const size_t smem = stage > red ? stage : red;
+    hipStream_t st = (hipStream_t)stream;
+    const long units = (long)n_shards * RG * 16 * (K / 128);
+    tile_rot_kernel<<<(unsigned)((units + 7) / 8), 256, 0, st>>>(x, x_dtype, (int)x_stride, (int)T, (int)K,
+                                                                 (int)n_shards, su[0], su[1], su[2], su[3],
+                                                                 static_cast<uint16_t*>(xh), (int)RG);
+    int rc = esp_host::launch_check("dense_tile rotation");
+    if (rc) return rc;
+    const dim3 grid((unsigned)nbt, (unsigned)SK, (unsigned)tiles);
+    switch (cb * 32 + k2) {
+#define ESP_TILE_CASE(CB_, K2_)                                          \
+    case CB_ * 32 + K2_:                                                 \
+        rc = launch_tile<gemm_cb(CB_), K2_>(a, grid, smem, st);          \
+        break;
+        ESP_CASES(ESP_TILE_CASE)
+#undef ESP_TILE_CASE
+    }
+    if (rc) return rc;
+    return esp_host::launch_check("dense_tile");
+}

@@ -50,6 +50,19 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
     return sk, w, 2
 
 
+def tile_plan(K: int, N: int) -> int:
+    """K splits of a prompt launch (esp_dense_tile) of a K -> N layer, from its shape alone (so a row's bits never
+    depend on the prompt's length): enough splits that a 512-row prompt (4 tiles of 128 rows) has ~256 workgroups,
+    SK = ceil(64 / blocks), but at least one 4-step stage a split. ESPALIER_DENSE_PROMPT_SK forces."""
+    forced = env("ESPALIER_DENSE_PROMPT_SK")
+    if forced:
+        return int(forced)
+    return max(1, min(-(-64 // (N // 128)), K // 128))
+
+
+TILE_ROWS = 128              # rows a prompt-launch workgroup
+
+
 class _SharedScratch:
     """The split-K partials Z (fp32) and the unfused rotation's rows xh (fp16), one pair a device, shared by every
     layer (layers run one after another). Sizes only grow, and only while layers are being built; a pair a growth
@@ -78,6 +91,22 @@ _SHARED = _SharedScratch()
 def scratch(device, z_floats: int, xh_halves: int):
     """(Z, xh) of the device, grown to at least the given sizes."""
     return _SHARED.reserve(device, z_floats, xh_halves)
+
+
+_PROMPT = _SharedScratch()
+_PROMPT_COUNTERS: dict = {}
+
+
+def prompt_scratch(device, z_floats: int, xh_halves: int, counters: int):
+    """(Z, xh, counters) of the device for prompt launches, grown to at least the given sizes (the counters zero, and
+    left zero by every launch)."""
+    z, xh = _PROMPT.reserve(device, z_floats, xh_halves)
+    cnt = _PROMPT_COUNTERS.get(device)
+    if cnt is None or cnt.numel() < counters:
+        if cnt is not None:
+            _PROMPT.retired.append((cnt,))
+        cnt = _PROMPT_COUNTERS[device] = torch.zeros(max(counters, 1), dtype=torch.int32, device=device)
+    return z, xh, cnt
 
 
 def _cu_count(device) -> int:
@@ -162,6 +191,34 @@ class Dense:
             pick = l.members
             e.dense(x, [codes[i] for i in pick], [pre[i] for i in pick], [post[i] for i in pick],
                     [self.col0[i] for i in pick], y, xh, z, self.counters, l.k2, l.cb, l.sk, l.w, l.pf, ROT_SMEM)
+        return y
+
+    def reserve_prompt(self, T: int) -> None:
+        """Grow the prompt scratch for forward_tile over T rows (done before a graph is captured)."""
+        device = self.mats[0].trellis.device
+        tiles = -(-T // TILE_ROWS)
+        z = max(tiles * tile_plan(self.K, l.n) * TILE_ROWS * l.n for l in self.launches)
+        xh = max(len(l.members) for l in self.launches) * -(-T // 16) * 16 * self.K
+        cnt = max(tiles * (l.n // 128) * COUNTER_STRIDE for l in self.launches)
+        prompt_scratch(device, z, xh, cnt)
+
+    def forward_tile(self, x, out=None):
+        """x [T, K], any T (a prompt) -> [T, n_out] in x's dtype, each weight decoded once for every 128 rows
+        (esp_dense_tile). A row's bits are its own (the same at any T), not those of forward."""
+        T = x.shape[0]
+        y = torch.empty((T, self.n_out), dtype=x.dtype, device=x.device) if out is None else out
+        if self.n_out > self.N:
+            y[:, self.N:].zero_()
+        if x.stride(-1) != 1:
+            x = x.contiguous()
+        self.reserve_prompt(T)
+        z, xh, cnt = prompt_scratch(x.device, 0, 0, 0)
+        e = ext()
+        for l in self.launches:
+            pick = l.members
+            ms = [self.mats[i] for i in pick]
+            e.dense_tile(x, [m.trellis for m in ms], [m.suh for m in ms], [m.svh for m in ms],
+                         [self.col0[i] for i in pick], y, xh, z, cnt, l.k2, l.cb, tile_plan(self.K, l.n))
         return y
 
     def norm_fusable(self, M: int) -> bool:

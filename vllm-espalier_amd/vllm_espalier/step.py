@@ -173,28 +173,30 @@ class SyntheticDecoder:
         return self._bufs[key]
 
     def prefill(self, T: int, head_rows: int = 1) -> Buffers:
-        """A whole prompt of T tokens (prefill_buffers(T).ids_in) in the tile mode: the dense layers in windows of
-        MAX_ROWS rows (qkv then o as one chained launch), every layer's MoE over the whole prompt (experts.prefill:
-        routing in windows, one grouping, each picked expert decoded once), then the head and argmax on the last
-        head_rows tokens. Rows still never interact, but a row's bits are those of the tile mode, not of decode."""
+        """A whole prompt of T tokens (prefill_buffers(T).ids_in) in the tile mode: the dense layers as prompt launches
+        (Dense.forward_tile: each weight decoded once for every 128 rows), every layer's MoE over the whole prompt
+        (experts.prefill: routing in one launch, one grouping, each picked expert decoded once), then the head (a prompt
+        launch too) and argmax on the last head_rows tokens. Rows still never interact, but a row's bits are those of the tile mode,
+        not of decode."""
         b = self.prefill_buffers(T)
         e = ext()
-        W = Dn.MAX_ROWS
         e.embed(b.ids_in, self.embedding, b.h)
         L0 = self.layers[0]
         ps = G.prefill_scratch(L0.moe, T, TOPK + 1, self.dev)
+        L0.qkv.reserve_prompt(T)
+        L0.o.reserve_prompt(T)
+        self.head.reserve_prompt(head_rows)
         q = b.qkv[:, :Q_OUT]
         for i, L in enumerate(self.layers):
             d1, d2 = (None, None) if i == 0 else (b.moe, b.moe_shared)
             e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
-            for r0 in range(0, T, W):
-                rows = slice(r0, r0 + W)
-                L.attn.forward([b.a[rows], q[rows]], [b.qkv[rows], b.o[rows]])
+            L.qkv.forward_tile(b.a, out=b.qkv)
+            L.o.forward_tile(q, out=b.o)
             e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
             G.prefill(b.a, None, None, L.moe, ps, TOPK, gate=L.router, out=b.moe, out_shared=b.moe_shared)
         e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
         tail = slice(T - head_rows, T)
-        self.head.forward(b.a[tail], out=b.logits[tail])
+        self.head.forward_tile(b.a[tail], out=b.logits[tail])
         e.argmax(b.logits[tail], b.ids_out[tail])
         return b
 
