@@ -162,6 +162,20 @@ def run_dense_multi(stack, M: int, dev, chain: bool):
     return graph_of(fn)
 
 
+def run_dense_prompt(stack, T: int, dev):
+    """A graph over every copy of the block as prompt launches (Dense.forward_tile) over T rows."""
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(3000 + T)
+    xs = {K: torch.randn((T, K), generator=gen, device=dev).to(torch.bfloat16) for K in (512, 2048, 4096)}
+    outs = [[torch.empty((T, d.n_out), dtype=torch.bfloat16, device=dev) for d in block] for block in stack]
+
+    def fn():
+        for block, ob in zip(stack, outs):
+            for d, o in zip(block, ob):
+                d.forward_tile(xs[d.K], out=o)
+    return graph_of(fn)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # MoE (config 4)
 # ---------------------------------------------------------------------------------------------------------------
@@ -281,7 +295,7 @@ def bench_decoder(dev, steps: int, warmup: int, layers: int = 40, prefill_tokens
     del g
     res["prefill"] = {"tokens": nwin * W, "window": W, "ms": round(ms, 3), "tok_per_s": round(nwin * W / (ms * 1e-3), 1)}
     log(f"prefill: {nwin * W} tokens in {ms:.2f} ms, {nwin * W / (ms * 1e-3):.0f} tok/s")
-    # the tile prefill: the same prompt with every layer's experts grouped over the whole prompt
+    # the tile prefill: prompt launches for the dense layers and the head, the MoE over the whole prompt
     T = nwin * W
     bp = dec.prefill_buffers(T)
     bp.ids_in.copy_(ids_all[:T])
@@ -292,7 +306,8 @@ def bench_decoder(dev, steps: int, warmup: int, layers: int = 40, prefill_tokens
     ms = time_graph(g, max(3, steps // 4), 1)
     del g
     res["prefill_tile"] = {"tokens": T, "ms": round(ms, 3), "tok_per_s": round(T / (ms * 1e-3), 1),
-                           "mode": "dense layers in 32-row windows, each layer's MoE grouped over the whole prompt"}
+                           "mode": "dense layers and head as prompt launches (128 rows a workgroup), routing in one "
+                                   "launch, each layer's MoE grouped over the whole prompt"}
     log(f"prefill (tile): {T} tokens in {ms:.2f} ms, {T / (ms * 1e-3):.0f} tok/s")
     del dec
     torch.cuda.empty_cache()
@@ -483,6 +498,20 @@ def probes(dev) -> dict:
             rates[f"{name} @{waves_per_simd}w"] = round(lane_ops / (ms * 1e-3) / (cus * khz * 1e3), 1)
             del g
     out["valu_lane_ops_per_cu_clk"] = rates
+    # random lookups into a shared-memory table (the codebook-table decode's inner operation), lookups a CU a clock
+    L.esp_probe_lds.argtypes = [ctypes.c_int, ctypes.c_int, I64, ctypes.c_int, P, P]
+    lds = {}
+    for wide, name in ((0, "u8 of 64 KiB"), (1, "u16 of 128 KiB")):
+        for waves in (4, 16):
+            iters = 4000
+            if L.esp_probe_lds(wide, iters, cus, waves, sink.data_ptr(), stream()) != 0:
+                raise RuntimeError("esp_probe_lds failed")
+            g = graph_of(lambda: L.esp_probe_lds(wide, iters, cus, waves, sink.data_ptr(), stream()))
+            ms = time_graph(g, 5)
+            lookups = cus * waves * 64 * 8 * iters
+            lds[f"{name} @{waves} waves"] = round(lookups / (ms * 1e-3) / (cus * khz * 1e3), 1)
+            del g
+    out["lds_lookups_per_cu_clk"] = lds
     for k, v in out.items():
         log(f"probe {k}: {v}")
     return out
@@ -630,6 +659,17 @@ def main() -> int:
             del g
             multi[key][str(M)] = {"us_per_layer": round(us, 3), "GBps": round(bpl / (us * 1e-6) / 1e9, 1)}
             log(f"dense block, one multi launch ({key}) M={M}: {us:.3f} us/layer, {bpl / (us * 1e-6) / 1e9:.0f} GB/s")
+    # the same block over a prompt: the prompt launches (each weight decoded once for every 128 rows)
+    prompt = {}
+    flops_row = 2 * sum(d.K * d.N for d in stack[0])
+    for T in (128, 512):
+        g = run_dense_prompt(stack, T, dev)
+        us = time_graph(g, max(3, a.steps // 4), 1) * 1000 / copies
+        del g
+        tf = flops_row * T / (us * 1e-6) / 1e12
+        prompt[str(T)] = {"us_per_layer": round(us, 2), "tok_per_s": round(T / (us * 1e-6), 1),
+                          "TFLOPs": round(tf, 1), "GBps": round(bpl / (us * 1e-6) / 1e9, 1)}
+        log(f"dense block, prompt launches T={T}: {us:.2f} us/layer, {T / (us * 1e-6):.0f} rows/s, {tf:.1f} TFLOP/s")
     # the timed steps of the headline: a step = one replay over the cold stack at batch 1
     for _ in range(a.warmup):
         g1.replay()
@@ -716,6 +756,7 @@ def main() -> int:
                    "bytes_per_layer": bpl, "layers_per_step": copies, "device": name},
         "dense_block": per_m,
         "dense_block_one_launch": multi,
+        "dense_block_prompt": prompt,
         "dense_launch_us_batch1": per_launch,
         "config1_us": round(c1_us, 3),
         "config1_GBps": round(c1_gbs, 1),

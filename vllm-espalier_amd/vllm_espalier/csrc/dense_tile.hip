@@ -24,6 +24,7 @@ constexpr int TILE_KW = TILE_WAVES / 4;
 constexpr int TILE_STEPS = 4;                   // 32-k steps a stage
 constexpr int TILE_FRAG = 512;                  // halves a (row group, step) block: 64 lanes x 8
 constexpr int RED_STRIDE = 132;                 // floats between two rows of the block's sums (banks apart)
+constexpr int RED_BYTES = TILE_ROWS * RED_STRIDE * 4;
 
 struct TileArgs {
     Shard s[MAX_SHARDS];
@@ -66,7 +67,9 @@ typedef __attribute__((address_space(3))) const f16x8* lds_f16x8_ptr;
 template <int CB, int K2>
 __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int last;
+    // the arrival flag sits past the block's sums (no static shared memory: at 4-bit widths two workgroups of 80 KiB
+    // then share a CU, each hiding the other's stage waits)
+    int* const last = reinterpret_cast<int*>(smem + RED_BYTES);
     constexpr int TW = 4 * K2;
     constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;            // one k tile of the block
     constexpr int B_BUF = TILE_STEPS * 2 * ROW_WORDS;              // words a B stage
@@ -195,7 +198,7 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         zb.store4(Zt + split * zsplit + r * zrow + nbg * 128 + 4 * l32,
                   *reinterpret_cast<const float4*>(red + r * RED_STRIDE + 4 * l32));
     int* const cnt_p = a.counters + ((size_t)mt * a.NBT + nbg) * CNT_STRIDE;
-    if (!arrive_last(cnt_p, a.SK, &last)) return;
+    if (!arrive_last(cnt_p, a.SK, last)) return;
     for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES) {
         const float* zp = Zt + r * zrow + nbg * 128 + 4 * l32;
         float4 s;
@@ -287,7 +290,7 @@ extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int6
     a.SR = (int)((K / 32) % SK);
     a.RG = (int)RG;
     const size_t stage = 2 * (size_t)TILE_RG * TILE_STEPS * TILE_FRAG * 2 + 2 * (size_t)TILE_STEPS * 2 * 32 * k2 * 4;
-    const size_t red = (size_t)TILE_ROWS * RED_STRIDE * 4;
+    const size_t red = (size_t)RED_BYTES + 16;                   // the sums, then the arrival flag
     const size_t smem = stage > red ? stage : red;
     hipStream_t st = (hipStream_t)stream;
     const long units = (long)n_shards * RG * 16 * (K / 128);

@@ -3,6 +3,8 @@
 //   esp_probe_empty   an empty kernel, for the launch floor of a graph of launches
 //   esp_probe_read    a streaming read of a buffer (16-byte nontemporal loads), for the attainable HBM read rate
 //   esp_probe_valu    8 independent chains of one VALU instruction a lane, for its issue rate
+//   esp_probe_lds     random byte / half lookups into a 64 KiB / 128 KiB shared-memory table, for the rate a table
+//                     decode of the codebooks could reach
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,6 +52,38 @@ __global__ __launch_bounds__(1024) void valu_kernel(int iters, uint32_t* __restr
     if (r == 0x9E3779B9u) out[0] = r;
 }
 
+// Every lane looks up 8 entries an iteration at byte offsets base + 4096 j (the immediate offset field), base a
+// lane's own pseudo-random position, stepped by an odd lane-dependent stride an iteration and kept inside the table:
+// 8 lookups for about 3 VALU instructions. WIDE: 16-bit entries of a 128 KiB table, else bytes of a 64 KiB one.
+template <bool WIDE>
+__global__ __launch_bounds__(1024) void lds_kernel(int iters, uint32_t* __restrict__ out) {
+    extern __shared__ __align__(16) uint32_t tab[];
+    constexpr uint32_t BYTES = WIDE ? 131072u : 65536u;
+    for (uint32_t i = threadIdx.x; i < BYTES / 4; i += blockDim.x) tab[i] = i * 0x9E3779B1u;
+    __syncthreads();
+    typedef __attribute__((address_space(3))) const unsigned char* lds_u8;
+    typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
+    const uint32_t span = BYTES - 8 * 4096;                     // base + 4096 * 7 + 1 stays inside the table
+    uint32_t base = (threadIdx.x * 2654435761u + blockIdx.x * 40503u) % span;
+    const uint32_t stride = ((threadIdx.x * 7919u) | 1u) % span;
+    uint32_t acc = 0u;
+    for (int it = 0; it < iters; ++it) {
+        uint32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (WIDE) v[j] = ((lds_u16)tab)[(base & ~1u) / 2 + 2048 * j];
+            else v[j] = ((lds_u8)tab)[base + 4096 * j];
+        }
+        acc = acc + v[0] + v[1];
+        acc = acc + v[2] + v[3];
+        acc = acc + v[4] + v[5];
+        acc = acc + v[6] + v[7];
+        base += stride;
+        base = base >= span ? base - span : base;
+    }
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
 }  // namespace
 
 extern "C" int esp_probe_clock_khz(void) {
@@ -87,6 +121,26 @@ extern "C" int esp_probe_valu(int op, int iters, int64_t grid, int waves, void* 
         case 5: valu_kernel<5><<<(unsigned)grid, threads, 0, s>>>(iters, o); break;
         case 6: valu_kernel<6><<<(unsigned)grid, threads, 0, s>>>(iters, o); break;
         default: return 1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// wide 0: byte lookups in a 64 KiB table; 1: 16-bit lookups in a 128 KiB table. One workgroup of `waves` waves a CU.
+extern "C" int esp_probe_lds(int wide, int iters, int64_t grid, int waves, void* out, void* stream) {
+    if (!out || iters < 1 || grid < 1 || waves < 1 || waves > 16) return 1;
+    hipStream_t s = (hipStream_t)stream;
+    const unsigned threads = 64u * (unsigned)waves;
+    uint32_t* o = static_cast<uint32_t*>(out);
+    if (wide) {
+        if (hipFuncSetAttribute((const void*)lds_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 131072) !=
+            hipSuccess)
+            return 2;
+        lds_kernel<true><<<(unsigned)grid, threads, 131072, s>>>(iters, o);
+    } else {
+        if (hipFuncSetAttribute((const void*)lds_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 65536) !=
+            hipSuccess)
+            return 2;
+        lds_kernel<false><<<(unsigned)grid, threads, 65536, s>>>(iters, o);
     }
     return hipGetLastError() == hipSuccess ? 0 : 3;
 }
