@@ -202,9 +202,13 @@ class Dense:
         cnt = max(tiles * (l.n // 128) * COUNTER_STRIDE for l in self.launches)
         prompt_scratch(device, z, xh, cnt)
 
-    def forward_tile(self, x, out=None):
+    def forward_tile(self, x, trellis=None, suh=None, svh=None, out=None):
         """x [T, K], any T (a prompt) -> [T, n_out] in x's dtype, each weight decoded once for every 128 rows
-        (esp_dense_tile). A row's bits are its own (the same at any T), not those of forward."""
+        (esp_dense_tile). A row's bits are its own (the same at any T), not those of forward. trellis / suh / svh:
+        lists that replace the matrices' own tensors, as in forward."""
+        codes = trellis or [m.trellis for m in self.mats]
+        pre = suh or [m.suh for m in self.mats]
+        post = svh or [m.svh for m in self.mats]
         T = x.shape[0]
         y = torch.empty((T, self.n_out), dtype=x.dtype, device=x.device) if out is None else out
         if self.n_out > self.N:
@@ -216,8 +220,7 @@ class Dense:
         e = ext()
         for l in self.launches:
             pick = l.members
-            ms = [self.mats[i] for i in pick]
-            e.dense_tile(x, [m.trellis for m in ms], [m.suh for m in ms], [m.svh for m in ms],
+            e.dense_tile(x, [codes[i] for i in pick], [pre[i] for i in pick], [post[i] for i in pick],
                          [self.col0[i] for i in pick], y, xh, z, cnt, l.k2, l.cb, tile_plan(self.K, l.n))
         return y
 

@@ -10,7 +10,9 @@ Rows beyond one launch (prefill) follow ESPALIER_PREFILL_MODE:
     chunk  (default) the decode kernels over windows of MAX_ROWS rows, so a row gets exactly its decode bits;
     gemm   each matrix decoded once (dequant kernel), both Hadamards by the had kernel, and an fp16 matmul
            (hipBLASLt) between them. A layer of HUGE weights or more (the LM head) stays windowed: its decoded weight
-           would not fit beside the model.
+           would not fit beside the model;
+    tile   the prompt launch (esp_dense_tile): every weight decoded once for each 128 rows, inside the GEMM; a row's
+           bits are its own (the same for any prompt), not its decode bits. No counterpart in the reference.
 The fake implementations give only the output shapes.
 """
 from __future__ import annotations
@@ -21,7 +23,7 @@ import torch
 
 from ._env import env
 
-PREFILL_MODES = ("chunk", "gemm")
+PREFILL_MODES = ("chunk", "gemm", "tile")
 PREFILL = env("ESPALIER_PREFILL_MODE", "chunk")
 if PREFILL not in PREFILL_MODES:
     raise ValueError(f"ESPALIER_PREFILL_MODE={PREFILL}: expected one of {PREFILL_MODES}")
@@ -79,13 +81,23 @@ def matmul(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch
     from .dense import MAX_ROWS
     if PREFILL == "gemm" and x.shape[0] > MAX_ROWS:
         return _decoded_matmul(x, trellis, suh, svh, K, cb)
-    return windowed(_single(trellis, suh, svh, K, cb), x)
+    layer = _single(trellis, suh, svh, K, cb)
+    if PREFILL == "tile" and x.shape[0] > MAX_ROWS and _tileable(layer):
+        return layer.forward_tile(x)
+    return windowed(layer, x)
+
+
+def _tileable(layer) -> bool:
+    """Whether a layer runs as prompt launches: 128-wide input and output blocks."""
+    return layer.K % 128 == 0 and all(m.out_features % 128 == 0 for m in layer.mats)
 
 
 @torch.library.custom_op("espalier::dense", mutates_args=())
 def dense(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
           key: int) -> torch.Tensor:
     layer = DENSE_LAYERS[key]
+    if PREFILL == "tile" and x.shape[0] > layer.MAX_ROWS:
+        return layer.forward_tile(x.contiguous(), trellis, suh, svh)
     decode_whole = PREFILL == "gemm" and x.shape[0] > layer.MAX_ROWS and layer.K * layer.N < HUGE
     if not decode_whole:
         return windowed(layer, x.contiguous(), trellis, suh, svh)
