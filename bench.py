@@ -46,7 +46,7 @@ def kernel_sources_sha() -> str:
     """sha256 of the sources the dense kernel is compiled from."""
     import hashlib
     h = hashlib.sha256()
-    for name in ("dense.hip", "common.hpp", "trellis.hpp", "gemm.hpp", "norm.hpp"):
+    for name in ("dense.hip", "dense.hpp", "common.hpp", "trellis.hpp", "gemm.hpp", "norm.hpp"):
         h.update(name.encode())
         h.update((CSRC / name).read_bytes())
     return h.hexdigest()[:16]
@@ -426,7 +426,8 @@ def counter_probe(dev) -> None:
     """The workload of the shader-counter passes over the expert kernels and the LM head: 8 cold 256-expert layers
     at 1 token (route_group, the fused gate/up launch, the grouped down launch, down_combine2) and at 32 tokens
     (route_group, rot_in, the grouped gate/up launch, its epilogue, the grouped down launch, down_combine2), one
-    replay each, then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row."""
+    replay each, then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row, then two cold config-2 blocks
+    as prompt launches over 512 rows (esp_dense_tile)."""
     import torch
     from vllm_espalier import dense as D, experts as G, workloads as WL
     gen = torch.Generator(device=dev).manual_seed(4)
@@ -447,8 +448,11 @@ def counter_probe(dev) -> None:
     x = torch.randn((1, 2048), device=dev).to(torch.bfloat16)
     y = torch.empty((1, 151936), dtype=torch.bfloat16, device=dev)
     graph_of(lambda: [h.forward(x, out=y) for h in heads]).replay()
+    del heads
+    g = run_dense_prompt(dense_stack(2, 12, dev), 512, dev)
+    g.replay()
     torch.cuda.synchronize()
-    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row")
+    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row, 2 dense blocks over 512 rows")
 
 
 # ---------------------------------------------------------------------------------------------------------------

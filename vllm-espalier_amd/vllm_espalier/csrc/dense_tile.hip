@@ -139,23 +139,25 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         const uint32_t* bb = sb + (st & 1) * B_BUF + lane_base;
         const uint16_t* ab = sa + (st & 1) * A_BUF + lane * 8;
         for (int ls = kw; ls < n; ls += TILE_KW) {
+            // the trellis words, then every row group's A fragment, all in flight while the words are decoded (LDS
+            // reads return in order). A row group past the tile's rows reads whatever its slot holds: row i of an
+            // MFMA result depends on row i of A alone, and those rows' sums are never stored.
             uint32_t w[2][6];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int i = 0; i < 6; ++i) w[j][i] = bb[ls * 2 * ROW_WORDS + j * TW + lw.off[i]];
+            f16x8 av[TILE_RG];
+#pragma unroll
+            for (int g = 0; g < TILE_RG; ++g) av[g] = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
             f16x8 b[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) b[j] = decode_b<CB, K2>(w[j], lp);
 #pragma unroll
-            for (int g = 0; g < TILE_RG; ++g) {
-                if (g < rgt) {                  // uniform: the tile's last row groups may be absent
-                    const f16x8 av = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
+            for (int g = 0; g < TILE_RG; ++g)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[j], acc[j][g], 0, 0, 0);
-                }
-            }
+                for (int j = 0; j < 2; ++j)
+                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b[j], acc[j][g], 0, 0, 0);
         }
     }
 

@@ -39,7 +39,7 @@ VOCAB = 151936
 TOPK = 8
 EPS = 1e-6
 FUSE_NORMS = True            # the norms inside their consumers' launches for up to 4 rows (same bits)
-MULTI_ATTN = True            # qkv and o as one chained launch (same bits)
+MULTI_ATTN = False            # qkv and o as one chained launch (same bits)
 
 
 @dataclass
