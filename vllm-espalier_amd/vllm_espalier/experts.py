@@ -46,6 +46,7 @@ ACT_F32 = 1
 FUSED = env("ESPALIER_MOE_FUSED", "1") != "0"
 FUSED_ROWS = 4
 PREFILL_WAVES = 4          # waves a workgroup of the whole-prompt (prefill) grouped launches
+PREFILL_SK_GU = 1          # K splits of the whole-prompt gate/up launch
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 
@@ -378,7 +379,7 @@ class PrefillScratch:
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
         layout = {
             "xg": ((P, D), f16, 0), "xu": ((P, D), f16, 0), "xd": ((P, I), f16, 0),
-            "z": ((P * max(2 * I, D),), f32, 0),                     # one K split: the partials are the sums
+            "z": ((P * max(2 * I * PREFILL_SK_GU, D),), f32, 0),     # the gate/up splits' partials, or down's sums
             "y": ((P, D), f32, 0),
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
@@ -430,9 +431,10 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
         e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, T, k,
                        L.E)
     e.rot_in(x, x.stride(0), pick_p, L.suh_g, L.suh_u, s.xg, s.xu, T, L.D, slots, L.E)
+    sk = PREFILL_SK_GU
     e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
-              L.D, L.I, P, 1, slots, 8, PREFILL_WAVES, 2, *L.k2_gu)
-    e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, 1, slots, L.E, math.inf, ACT_F32)
+              L.D, L.I, P, sk, slots, 8, PREFILL_WAVES, 2, *L.k2_gu)
+    e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
     t, b, c = L.ptr[2], L.k2[2], L.cb[2]
     e.grouped(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.z, 1, L.I, L.D, P, 1, slots, 8, PREFILL_WAVES,
               2, *L.k2_d)
