@@ -14,6 +14,10 @@
 - Prefill windows (ESPALIER_PREFILL_MODE=chunk): at 33, 100 and 517 rows the espalier::dense op (every dense kind of
   config 2 and the head) and experts.windows (given picks and fused routing) equal the same rows run one at a time,
   bit for bit (the reference's gate P1, tests/gpu_prefill.py:3-5).
+- The prompt paths (ESPALIER_PREFILL_MODE=tile) at full size: every dense kind of config 2 as prompt launches over
+  517 rows within the GEMM bars against the oracle (the head on a sample of its rows), and the 256-expert layer over
+  a whole prompt (one routing launch, one grouping, member tiles: the shared expert has every row) with exact
+  routing and its outputs within the MoE bars on sampled rows; rows alone == rows in the prompt, bit for bit.
 """
 import numpy as np
 import pytest
@@ -340,3 +344,50 @@ def test_prefill_moe_rows_alone_equal_window(dev, moe256, T, routing):
             o1, s1 = G.routed2(x[r:r + 1], None, None, L, s, k=8)
         assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), r
         assert torch.equal(s1.view(torch.int16), sh[r:r + 1].view(torch.int16)), r
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the prompt paths (tile mode) at full size
+# ---------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("kind", ["qkv", "o", "shared_gate_up", "shared_down", "lm_head"])
+def test_prompt_dense_full_size(dev, dense_kinds, kind):
+    """Dense.forward_tile over 517 rows (four full 128-row tiles and a 5-row one) against the oracle; rows at tile
+    edges alone equal the same rows in the prompt, bit for bit."""
+    print(f"prompt dense {kind} T=517", flush=True)
+    key, mats = dense_kinds[kind]
+    d = ops.DENSE_LAYERS[key]
+    T = 517
+    x = torch.randn((T, mats[0].in_features), generator=torch.Generator().manual_seed(700)).to(torch.bfloat16).to(dev)
+    y = d.forward_tile(x).clone()
+    torch.cuda.synchronize()
+    xf = bf(x)
+    if kind == "lm_head":
+        rows = [0, 127, 128, 516]                            # the head's fp64 reference on a sample of rows
+        check_gemm(y[rows], head_ref(xf[rows], mats[0]))
+    else:
+        for m, c0 in zip(mats, d.col0):
+            check_gemm(y[:, c0:c0 + m.out_features], lin(xf, m))
+    for r in (0, 127, 128, 512, 516):
+        y1 = d.forward_tile(x[r:r + 1])
+        assert torch.equal(y1.view(torch.int16), y[r:r + 1].view(torch.int16)), r
+
+
+@pytest.mark.parametrize("T", [200, 517])
+def test_prompt_moe_256_experts(dev, moe256, T):
+    """experts.prefill over a whole prompt with fused routing (route_rows): picks bit-exact against exact routing,
+    outputs within the MoE bars on sampled rows, rows alone == rows in the prompt."""
+    print(f"prompt moe 256 experts T={T}", flush=True)
+    L, experts, shared, gate_w, router = moe256
+    x = torch.randn((T, D), generator=torch.Generator().manual_seed(800 + T)).to(torch.bfloat16).to(dev)
+    ps = G.prefill_scratch(L, T, 9, dev)
+    out, osh = (t.clone() for t in G.prefill(x, None, None, L, ps, 8, gate=router))
+    torch.cuda.synchronize()
+    assert int(G.ext().status(True)) == 0
+    opick, owts, _, _ = O.route(bits(x), bits(router), 8, bits(gate_w), 256)
+    assert np.array_equal(ps.pick[:T * 9].view(T, 9).cpu().numpy(), opick)
+    rows = [0, 1, 31, 32, 100, T - 2, T - 1]
+    check_moe(out[rows], osh[rows], x[rows], opick[rows, :8], owts[rows, :8], experts, shared, gate_w)
+    for r in (0, 33, T - 1):
+        o1, s1 = G.prefill(x[r:r + 1], None, None, L, ps, 8, gate=router)
+        assert torch.equal(o1.view(torch.int16), out[r:r + 1].view(torch.int16)), r
+        assert torch.equal(s1.view(torch.int16), osh[r:r + 1].view(torch.int16)), r
