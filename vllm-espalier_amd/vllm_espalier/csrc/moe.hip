@@ -607,6 +607,7 @@ struct GroupedArgs {
     int stage_bytes, xs_stride;    // rotated rows in shared memory after the stages
     int lo, hi;                    // the K2 range the launch's stages are sized for
     int mt;                        // member tiles of 32 an expert (MODE 0: ceil(maxm / 32); MODE 1: 1)
+    int staged;                    // MODE 0: the member rows staged through shared memory (grouped_body_staged)
 };
 
 // Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
@@ -660,6 +661,106 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
             DevBuf(a.Z).store4(zp, s4);
         else
             *reinterpret_cast<float4*>(zp) = s4;
+    }
+}
+
+// The unfused launch's K loop for K ranges of several stages (a whole prompt's gate/up: 64 steps a program): the member
+// rows' K slices reach shared memory by DMA in the same stages as the trellis tiles. Read from global memory at each
+// step instead, a row load is queued behind the next stage's copies (vector-memory loads return in order), so with two
+// waves a SIMD nothing hides it. Stage s holds AST_STEPS steps: the block's tiles, then one slice of AST_STEPS * 32
+// halves a member row, AST_ROW halves apart (16 bytes of padding keep the 16 rows an MFMA reads on different banks).
+// Each wave takes the same steps in the same order as block_gemm, so the sums are bit-identical to grouped_body's.
+constexpr int AST_STEPS = 8;
+constexpr int AST_ROW = AST_STEPS * 32 + 8;
+__host__ __device__ constexpr int staged_buf_bytes(int k2) { return AST_STEPS * 2 * 32 * k2 * 4 + 32 * AST_ROW * 2; }
+
+template <int CB, int K2, int MG>
+__device__ __forceinline__ void grouped_body_staged(const GroupedArgs& a, const uint32_t* __restrict__ T,
+                                                    const uint16_t* abase, const int* rows_sh, int nrows, int mat,
+                                                    int split, float scale, uint32_t* stage) {
+    constexpr int TW = 4 * K2;
+    constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;
+    constexpr int B_WORDS = AST_STEPS * 2 * ROW_WORDS;
+    constexpr int BUF_BYTES = staged_buf_bytes(K2);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int l32 = lane & 31, half = lane >> 5, c = lane & 15, G = lane >> 4;
+    const int NW = (int)(blockDim.x >> 6), KW = NW >> 2, pair = wave & 3, kw = wave >> 2;
+    const int NTILES = a.N >> 4, nt0 = blockIdx.y * 8;
+    const int kr = a.K / a.SK, k0 = split * kr, steps = kr >> 5;
+    const int nst = (steps + AST_STEPS - 1) / AST_STEPS;
+    unsigned char* const sbase = reinterpret_cast<unsigned char*>(stage);
+    // stage st into buffer st & 1: the tiles (every thread), then a member row a wave instruction (4 16-byte units a
+    // step, lanes past them idle), rows past nrows never copied (their A slots are read, their sums never stored)
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        const int first = st * AST_STEPS, n = steps - first < AST_STEPS ? steps - first : AST_STEPS;
+        unsigned char* buf = sbase + (st & 1) * BUF_BYTES;
+        issue_stage<K2>(T, NTILES, (k0 >> 4) + 2 * first, 2 * n, nt0, reinterpret_cast<uint32_t*>(buf));
+        uint16_t* abuf = reinterpret_cast<uint16_t*>(buf + B_WORDS * 4);
+        for (int m = wave; m < nrows; m += NW) {
+            const int p = rows_sh[m];
+            if (lane < 4 * n) {
+                const uint16_t* src = abase + (size_t)p * a.K + k0 + first * 32 + lane * 8;
+                __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(abuf + m * AST_ROW), 16, 0, 0);
+            }
+        }
+    };
+    f32x4 acc[2][MG];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const LanePlan<K2> lp(lane);
+    const LdsWords<K2> lw(lp);
+    const int lane_base = ((G >> 1) * 8 + 2 * pair) * TW;
+    issue(0);
+    for (int st = 0; st < nst; ++st) {
+        wait_stage();
+        if (st + 1 < nst) issue(st + 1);
+        const int first = st * AST_STEPS, n = steps - first < AST_STEPS ? steps - first : AST_STEPS;
+        const unsigned char* buf = sbase + (st & 1) * BUF_BYTES;
+        const uint32_t* bb = reinterpret_cast<const uint32_t*>(buf) + lane_base;
+        const uint16_t* ab = reinterpret_cast<const uint16_t*>(buf + B_WORDS * 4);
+        RowsA<MG, true> al;
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+            const int m = g * 16 + c;
+            al.set(g, ab + (m < nrows ? m : 0) * AST_ROW + 16 * (G >> 1) + 4 * (G & 1));
+        }
+        al.kbase = 0;
+        const int st0 = ((kw - first) % KW + KW) % KW;          // this wave's first step of the stage
+        for (int ls = st0; ls < n; ls += KW) {
+            const uint32_t* tl = bb + ls * 2 * ROW_WORDS;
+            uint32_t w[2][6];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 6; ++i) w[j][i] = tl[j * TW + lw.off[i]];
+            f16x8 av[MG];
+#pragma unroll
+            for (int g = 0; g < MG; ++g) al(g, 32 * ls, av[g]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const f16x8 b = __builtin_bit_cast(f16x8, decode_words<CB, K2>(w[j], lp));
+#pragma unroll
+                for (int g = 0; g < MG; ++g)
+                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
+            }
+        }
+    }
+    // the k slots' partials added in order, then one member row a 32-lane half (as grouped_body)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(stage);
+    store_partials<MG>(red, nrows, acc);
+    __syncthreads();
+    float* Zm = a.Z + ((size_t)mat * a.SK + split) * a.P * a.N;
+    for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+        float4 s4 = *reinterpret_cast<const float4*>(red + (size_t)m * 128 + 4 * l32);
+        for (int q = 1; q < KW; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(red + ((size_t)q * nrows + m) * 128 + 4 * l32);
+            s4.x += u.x; s4.y += u.y; s4.z += u.z; s4.w += u.w;
+        }
+        s4.x *= scale; s4.y *= scale; s4.z *= scale; s4.w *= scale;
+        *reinterpret_cast<float4*>(Zm + (size_t)rows_sh[m] * a.N + nt0 * 16 + 4 * l32) = s4;
     }
 }
 
@@ -965,12 +1066,18 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     case CB_ * 32 + K2_: {                                                                                    \
         constexpr int KCB = gemm_cb(CB_);                                                                     \
         const float scale = gemm_scale(CB_);                                                                  \
-        if (two)                                                                                              \
+        if (MODE == 0 && a.staged) {                                                                          \
+            if (two)                                                                                          \
+                grouped_body_staged<KCB, K2_, 2>(a, T, abase, rows_sh, nrows, mat, split, scale, stage);      \
+            else                                                                                              \
+                grouped_body_staged<KCB, K2_, 1>(a, T, abase, rows_sh, nrows, mat, split, scale, stage);      \
+        } else if (two) {                                                                                     \
             grouped_body<KCB, K2_, 2, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
                                       scale, stage, MODE == 1, MODE == 1);                                    \
-        else                                                                                                  \
+        } else {                                                                                              \
             grouped_body<KCB, K2_, 1, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
                                       scale, stage, MODE == 1, MODE == 1);                                    \
+        }                                                                                                     \
         break;                                                                                                \
     }
         ESP_CASES(ESP_GROUPED_CASE)
@@ -1261,7 +1368,10 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.lo = (int)lo;
     a.hi = (int)hi;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK * mt));
-    const size_t stage = (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;     // the widest expert's stages
+    // K ranges of more than two stages' worth of steps stage the member rows with the tiles (grouped_body_staged)
+    a.staged = (K / SK) / 32 > 2 * AST_STEPS;
+    const size_t stage = a.staged ? 2 * (size_t)staged_buf_bytes((int)hi)
+                                  : (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;   // the widest expert's
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
     const size_t smem = stage > red ? stage : red;
     if (smem > 64 * 1024 &&
