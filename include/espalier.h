@@ -66,7 +66,9 @@ int esp_dequant(const void* trellis, void* out, int64_t K, int64_t N, int64_t k2
  * are addressed by 32-bit byte offsets), counters int32 (counters_numel >= 2 * sum(n_cols)/128 when SK > 1, the
  * reference's size; one counter a 128-column block, min(32, counters_numel / (sum(n_cols)/128)) ints apart, so 32 a
  * block keeps each on a 128-byte line of its own; zero on entry and left zero). SK K splits; W, PF tile hints; the
- * input rotation is fused when M * (K / SK) * 2 <= rot_smem bytes. */
+ * input rotation is fused when M * (K / SK) * 2 <= rot_smem bytes. Alignment (torch's allocations meet it): x and y
+ * 8-byte aligned (16 for fp32) with row strides a multiple of 4 elements, col0 a multiple of 4, trellis 16-byte
+ * aligned, suh / svh and xh 8-byte aligned, Z 16-byte aligned; else ESP_ERR_ARG. */
 int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
               const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
               const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh, int64_t xh_numel,
@@ -80,7 +82,7 @@ int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K
  * matrix, in MFMA fragment order), and with SK > 1, Z fp32 (z_numel >= ceil(T / 128) * SK * 128 * sum(n_cols), at most
  * 2^30 floats) and counters int32 (counters_numel >= 32 * ceil(T / 128) * sum(n_cols) / 128; zero on entry and left
  * zero). A row's bits depend on its own input and SK only: the same for any T and any place in the prompt, but not
- * those of esp_dense (another order of the sums). */
+ * those of esp_dense (another order of the sums). Alignment as esp_dense, xh and Z 16-byte aligned. */
 int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
                    const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
                    const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,

@@ -55,12 +55,14 @@ def _dense(lib, **over):
     f.argtypes = [P, ctypes.c_int, I64, I64, I64, I64, ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(P),
                   ctypes.POINTER(I64), ctypes.POINTER(I64), P, ctypes.c_int, I64, I64, P, I64, P, I64, P, I64, I64,
                   I64, I64, I64, I64, I64, P]
-    a = dict(M=1, K=2048, n=1, ncols=2048, col0=0, y_cols=2048, k2=8, cb=7, SK=1, W=4, z_numel=1 << 30)
+    a = dict(M=1, K=2048, n=1, ncols=2048, col0=0, y_cols=2048, k2=8, cb=7, SK=1, W=4, z_numel=1 << 30, x=16, y=16,
+             t=16, x_stride=None)
     a.update(over)
     one = (P * 1)(16)                                   # non-null, never dereferenced: the checks fail first
+    tp = (P * 1)(a["t"])
     nc, c0 = (I64 * 1)(a["ncols"]), (I64 * 1)(a["col0"])
-    rc = f(16, 1, a["K"], a["M"], a["K"], a["n"], one, one, one, nc, c0, 16, 1, a["y_cols"], a["y_cols"], 16, 1 << 30,
-           16, a["z_numel"], 16, 1 << 20, a["k2"], a["cb"], a["SK"], a["W"], 2, 0, None)
+    rc = f(a["x"], 1, a["x_stride"] or a["K"], a["M"], a["K"], a["n"], tp, one, one, nc, c0, a["y"], 1, a["y_cols"],
+           a["y_cols"], 16, 1 << 30, 16, a["z_numel"], 16, 1 << 20, a["k2"], a["cb"], a["SK"], a["W"], 2, 0, None)
     return rc, lib.esp_last_error().decode()
 
 
@@ -69,6 +71,9 @@ def _dense(lib, **over):
     (dict(W=6), "W"), (dict(ncols=100), "shape"), (dict(col0=100), "past y"), (dict(SK=65), "SK"), (dict(SK=0), "SK"),
     # the split-K partials are addressed by 32-bit byte offsets from Z (16-byte buffer accesses): at most 4 GiB
     (dict(M=32, SK=64, ncols=4160 * 128, y_cols=4160 * 128, z_numel=1 << 40), "4 GiB"),
+    # the kernels move 4 elements of a row and 16-byte trellis units at a time: misaligned operands are refused
+    (dict(x=18), "aligned"), (dict(y=20), "aligned"), (dict(x_stride=2050), "aligned"), (dict(t=24), "aligned"),
+    (dict(col0=2, y_cols=4096), "multiple of 4"),
 ])
 def test_dense_argument_errors(lib, over, needle):
     rc, msg = _dense(lib, **over)

@@ -193,6 +193,10 @@ int prepare_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64
     ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "x / y dtype");
     ESP_REQUIRE(W == 4 || W == 8 || W == 16, "W (waves a workgroup) must be 4, 8 or 16");
     ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "x / y row stride");
+    // the kernels move 4 elements of a row at once (8 bytes, 16 for fp32) and trellis tiles 16 bytes at a time
+    ESP_REQUIRE(((uintptr_t)x % (x_dtype == ESP_F32 ? 16 : 8)) == 0 && x_stride % 4 == 0 &&
+                    ((uintptr_t)y % (y_dtype == ESP_F32 ? 16 : 8)) == 0 && y_stride % 4 == 0,
+                "x / y must be 8-byte aligned (16 for fp32) with row strides a multiple of 4 elements");
     if (!supported((int)cb, (int)k2))
         return esp_host::fail(ESP_ERR_UNSUPPORTED, "unsupported codebook/width: cb=%lld k2=%lld", (long long)cb,
                               (long long)k2);
@@ -204,6 +208,9 @@ int prepare_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64
         ESP_REQUIRE(N > 0 && N % 128 == 0, "matrix shape");
         ESP_REQUIRE(col0[s] >= 0 && col0[s] + N <= y_cols, "matrix columns past y");
         ESP_REQUIRE(trellis[s] && suh[s] && svh[s], "dense: null matrix pointer");
+        ESP_REQUIRE(((uintptr_t)trellis[s] & 15) == 0 && ((uintptr_t)suh[s] & 7) == 0 && ((uintptr_t)svh[s] & 7) == 0 &&
+                        col0[s] % 4 == 0,
+                    "dense: trellis 16-byte aligned, suh / svh 8-byte aligned, col0 a multiple of 4");
         a.s[s] = Shard{static_cast<const uint32_t*>(trellis[s]), static_cast<const uint16_t*>(suh[s]),
                        static_cast<const uint16_t*>(svh[s]), nbt, (int)(N / 128), (int)col0[s], c};
         nbt += (int)(N / 128);
@@ -215,6 +222,8 @@ int prepare_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64
     ESP_REQUIRE(SK == 1 || (Z && z_numel >= SK * M * nbt * 128 && counters && counters_numel >= 2 * (int64_t)nbt),
                 "scratch too small: Z needs SK*M*N floats, counters 2 per 128 columns");
     ESP_REQUIRE(SK * M * nbt * 128 <= (int64_t(1) << 30), "dense: the partials must fit in 4 GiB");
+    ESP_REQUIRE(SK == 1 || (((uintptr_t)Z & 15) == 0 && ((uintptr_t)counters & 3) == 0),
+                "dense: Z must be 16-byte aligned");
     const int64_t sq = (K / 32) / SK, sr = (K / 32) % SK;
     const int64_t steps_max = sq + (sr > 0);                  // the longest split
     const int64_t kr = steps_max * 32;
@@ -241,7 +250,7 @@ int prepare_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64
         a.neps = (float)nrm->eps;
         a.norm = 1;
     }
-    if (!fused) ESP_REQUIRE(xh && xh_numel >= n_shards * M * K, "xh too small");
+    if (!fused) ESP_REQUIRE(xh && xh_numel >= n_shards * M * K && ((uintptr_t)xh & 7) == 0, "xh too small or unaligned");
     a.x = x;
     a.x_dtype = x_dtype;
     a.x_stride = (int)x_stride;

@@ -252,6 +252,11 @@ extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int6
                 "dense_tile: K must be a multiple of 128 and SK at most K / 32");
     ESP_REQUIRE(x_dtype >= 0 && x_dtype <= 2 && y_dtype >= 0 && y_dtype <= 2, "dense_tile: x / y dtype");
     ESP_REQUIRE(x_stride >= K && y_stride >= y_cols, "dense_tile: x / y row stride");
+    ESP_REQUIRE(((uintptr_t)x % (x_dtype == ESP_F32 ? 16 : 8)) == 0 && x_stride % 4 == 0 &&
+                    ((uintptr_t)y % (y_dtype == ESP_F32 ? 16 : 8)) == 0 && y_stride % 4 == 0 &&
+                    ((uintptr_t)xh & 15) == 0 && ((uintptr_t)Z & 15) == 0,
+                "dense_tile: x / y 8-byte aligned (16 for fp32) with row strides a multiple of 4 elements, xh and Z "
+                "16-byte aligned");
     if (!supported((int)cb, (int)k2))
         return esp_host::fail(ESP_ERR_UNSUPPORTED, "unsupported codebook/width: cb=%lld k2=%lld", (long long)cb,
                               (long long)k2);
@@ -264,6 +269,9 @@ extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int6
         ESP_REQUIRE(N > 0 && N % 128 == 0, "dense_tile: matrix shape");
         ESP_REQUIRE(col0[s] >= 0 && col0[s] + N <= y_cols, "dense_tile: matrix columns past y");
         ESP_REQUIRE(trellis[s] && suh[s] && svh[s], "dense_tile: null matrix pointer");
+        ESP_REQUIRE(((uintptr_t)trellis[s] & 15) == 0 && ((uintptr_t)suh[s] & 7) == 0 && ((uintptr_t)svh[s] & 7) == 0 &&
+                        col0[s] % 4 == 0,
+                    "dense_tile: trellis 16-byte aligned, suh / svh 8-byte aligned, col0 a multiple of 4");
         a.s[s] = Shard{static_cast<const uint32_t*>(trellis[s]), static_cast<const uint16_t*>(suh[s]),
                        static_cast<const uint16_t*>(svh[s]), nbt, (int)(N / 128), (int)col0[s], c};
         su[s] = static_cast<const uint16_t*>(suh[s]);
