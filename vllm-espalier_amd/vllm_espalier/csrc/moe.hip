@@ -1317,6 +1317,8 @@ extern "C" int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const in
     ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
     ESP_REQUIRE(K % 128 == 0 && K > 0, "K must be a multiple of 128");
     ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE((((uintptr_t)x | (uintptr_t)suh0 | (uintptr_t)suh1 | (uintptr_t)out0 | (uintptr_t)out1) & 7) == 0,
+                "rot_in: x, suh and the outputs must be 8-byte aligned");
     const long units = rows * slots * (K / 128);
     if (units <= 0) return esp_host::ok();
     rot_in_kernel<<<units_grid(units, 4), 256, 0, (hipStream_t)stream>>>(
@@ -1342,6 +1344,8 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
     ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
     ESP_REQUIRE(warps == 4 || warps == 8 || warps == 16, "warps (waves a workgroup) must be 4, 8 or 16");
+    ESP_REQUIRE((((uintptr_t)X0 | (uintptr_t)X1 | (uintptr_t)Z) & 15) == 0,
+                "grouped: X0 / X1 and Z must be 16-byte aligned (rows and partials move 16 bytes at a time)");
     const int64_t mt = (maxm + 31) / 32;                 // an expert's members in tiles of 32 (experts_grouped.cuh:244)
     ESP_REQUIRE(mats * SK * mt <= 65535, "grouped: too many member tiles, splits and matrices for one launch");
     if (nexp_max <= 0) return esp_host::ok();
@@ -1405,6 +1409,9 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
     ESP_REQUIRE(SK >= 1 && K > 0 && N > 0 && K % (128 * SK) == 0 && N % 128 == 0,
                 "moe_gateup: K must split into whole 128-blocks, N a multiple of 128");
     ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
+    ESP_REQUIRE(((uintptr_t)Z & 15) == 0 && (((uintptr_t)x | (uintptr_t)suh_g | (uintptr_t)suh_u | (uintptr_t)svh_g |
+                                               (uintptr_t)svh_u | (uintptr_t)suh_d | (uintptr_t)xd) & 7) == 0,
+                "moe_gateup: Z 16-byte aligned, x, the scales and xd 8-byte aligned");
     ESP_REQUIRE(z_numel >= 2 * SK * P * N, "Z too small");
     ESP_REQUIRE(2 * SK * P * N <= (int64_t(1) << 30), "moe_gateup: the partials must fit in 4 GiB");
     ESP_REQUIRE(maxm >= 1 && maxm <= 32, "at most 32 member rows an expert");
@@ -1464,6 +1471,9 @@ extern "C" int esp_gateup_epilogue(const float* Z, const int32_t* pick, const vo
     ESP_REQUIRE(N % 128 == 0 && N > 0, "N must be a multiple of 128");
     ESP_REQUIRE(SK >= 1, "SK must be positive");
     ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
+    ESP_REQUIRE(((uintptr_t)Z & 15) == 0 && (((uintptr_t)svh_g | (uintptr_t)svh_u | (uintptr_t)suh_d |
+                                               (uintptr_t)xd) & 7) == 0,
+                "gateup_epilogue: Z 16-byte aligned, the scales and xd 8-byte aligned");
     const long units = rows * slots * (N / 128);
     if (units <= 0) return esp_host::ok();
     gateup_epilogue_kernel<<<units_grid(units, 8), 256, 0, (hipStream_t)stream>>>(
