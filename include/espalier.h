@@ -100,15 +100,16 @@ int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int
                     int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount,
                     int32_t* members, int64_t maxm, void* stream);
 
-/* esp_route_group's routing for any number of rows, without the grouping: rows in windows of 32, every window routed
- * as esp_route_group routes it (the same logits, picks and weights, bit for bit: a row's routing depends on that row
- * alone), all windows in one launch, side by side. No counterpart in the reference, which routes a prompt one
- * 32-token window a launch; for prompts grouped afterwards in one piece (esp_group / esp_group_shared over all rows).
- * pick_out / wts_out [R][k + has]; logits >= R * (E + has) floats; counters >= 32 ints a window, zero on entry and
- * left zero. R <= 2097120. */
+/* esp_route_group's routing for any number of rows, without the grouping: the same logits, picks and weights (a row's
+ * routing depends on that row alone; bf16 x bf16 products and their sums are exact in fp64 for ordinary data, so the
+ * order of the sums does not show after the rounding), for a whole prompt in two launches: the logits on the fp64
+ * matrix cores (16-row x 16-column tiles), then one wave a row for the top-k. No counterpart in the reference, which
+ * routes a prompt one 32-token window a launch; for prompts grouped afterwards in one piece (esp_group /
+ * esp_group_shared over all rows). pick_out / wts_out [R][k + has]; logits >= R * (E + has) floats. H a multiple of
+ * 256, x rows and gate 16-byte aligned, x_stride a multiple of 8. */
 int esp_route_rows(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
                    const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
-                   int32_t* counters, int64_t counters_numel, int32_t* pick_out, float* wts_out, void* stream);
+                   int32_t* pick_out, float* wts_out, void* stream);
 
 /* Replaces `group_shared` (experts.cpp:154-172, experts.cu:247-330, 518-539): pick/weight tables with the shared
  * expert as slot slots_in (weight sigmoid(x . gate_w), fp32), then the grouping. pick_in int32 / wts_in fp32

@@ -135,8 +135,8 @@ def test_route_group_exact(dev, ext, R, shared):
 
 @pytest.mark.parametrize("R,shared", [(1, True), (33, True), (100, False), (517, True)])
 def test_route_rows_equals_windows_and_oracle(dev, ext, R, shared):
-    """route_rows over a whole prompt (windows of 32 side by side, no grouping) against route_group window by window,
-    bit for bit (logits, picks, weights), and against the oracle's exact routing; counters left zero."""
+    """route_rows over a whole prompt (fp64-MFMA logits, then a wave a row) against route_group window by window, bit
+    for bit (logits, picks, weights), and against the oracle's exact routing."""
     print(f"route_rows R={R} shared={shared}", flush=True)
     x, gate, sgate = router_inputs(R, 500 + R)
     k, E = 8, 256
@@ -144,13 +144,10 @@ def test_route_rows_equals_windows_and_oracle(dev, ext, R, shared):
     slots = k + shared
     xd, gd, sd = x.to(dev), gate.to(dev), sgate.to(dev) if shared else None
     logits = torch.full((R * (E + shared),), float("nan"), dtype=torch.float32, device=dev)
-    counters = torch.zeros(32 * -(-R // 32), dtype=torch.int32, device=dev)
     pick = torch.full((R * slots,), -7, dtype=torch.int32, device=dev)
     wts = torch.full((R * slots,), float("nan"), dtype=torch.float32, device=dev)
-    for _ in range(2):                                   # twice: the counters come back zero
-        ext.route_rows(xd, gd, sd, k, sid, logits, counters, pick, wts)
-        torch.cuda.synchronize()
-        assert int(counters.abs().sum()) == 0
+    ext.route_rows(xd, gd, sd, k, sid, logits, pick, wts)
+    torch.cuda.synchronize()
     for r0 in range(0, R, 32):
         n = min(32, R - r0)
         lw, pw, ww, *_ = run_route(ext, dev, x[r0:r0 + n].contiguous(), gate, sgate, k, sid)

@@ -305,11 +305,10 @@ void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optiona
 
 // route_group's routing over any number of rows, without the grouping (no reference counterpart)
 void route_rows(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
-                int64_t shared_id, at::Tensor logits, at::Tensor counters, at::Tensor pick_out, at::Tensor wts_out) {
+                int64_t shared_id, at::Tensor logits, at::Tensor pick_out, at::Tensor wts_out) {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1 && gate.is_contiguous(), "x / gate layout");
     TORCH_CHECK(gate.scalar_type() == x.scalar_type(), "gate and x must share a dtype");
     check(logits, at::kFloat, "logits");
-    check(counters, at::kInt, "counters");
     check(pick_out, at::kInt, "pick_out");
     check(wts_out, at::kFloat, "wts_out");
     TORCH_CHECK(gate.dim() == 2 && gate.size(1) == x.size(1), "gate: [E, H]");
@@ -322,8 +321,7 @@ void route_rows(const at::Tensor& x, const at::Tensor& gate, const c10::optional
     c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     call(esp_route_rows(x.data_ptr(), dtype_code(x), x.stride(0), R, H, gate.data_ptr(), E,
                         sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits),
-                        logits.numel(), mptr<int32_t>(counters), counters.numel(), mptr<int32_t>(pick_out),
-                        mptr<float>(wts_out), cur_stream()));
+                        logits.numel(), mptr<int32_t>(pick_out), mptr<float>(wts_out), cur_stream()));
 }
 
 // dense with its input rows normalised in the launch (no reference counterpart): h, d1, d2 [M, K] contiguous rows

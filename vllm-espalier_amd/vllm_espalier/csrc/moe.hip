@@ -241,6 +241,51 @@ __device__ __forceinline__ float bf16_unorder(uint32_t k) {
     return __builtin_bit_cast(float, h << 16);
 }
 
+// One row's routing from its logits, by one wave: lr holds the E bf16-rounded router logits, then the shared gate's
+// logit. The k largest (one order-preserving 32-bit key an expert: the logit's bf16 bits, then 0xFFFF - id, so ties go
+// to the lowest id), their softmax weights (exponentials of the k maxima at once, the sum in pick order), and the
+// shared slot's sigmoid weight. Lane t < k returns pick t; every lane returns the shared weight (when has). DEV: the
+// logits were stored by other workgroups of the same launch (device-coherent loads).
+template <bool DEV>
+__device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has, int lane, int& e_out, float& w_out,
+                                         float& w_shared) {
+    uint32_t key[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = lane + 64 * q;
+        const float l = e < E ? (DEV ? load_dev(lr + e) : lr[e]) : 0.f;
+        key[q] = e < E ? (bf16_order(l) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
+    }
+    float l_mine = 0.f;
+    int e_mine = -1;
+    for (int t = 0; t < k; ++t) {
+        uint32_t m = key[0] > key[1] ? key[0] : key[1];
+        const uint32_t m2 = key[2] > key[3] ? key[2] : key[3];
+        m = m > m2 ? m : m2;
+        m = wave_max_u32(m);
+        const int e = (int)(0xFFFFu - (m & 0xFFFFu));
+        if (lane == t) {
+            e_mine = e;
+            l_mine = bf16_unorder(m >> 16);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (lane + 64 * q == e) key[q] = 0u;
+    }
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_mine), 0));   // pick 0's
+    const float p_mine = expf(l_mine - mx);
+    float psum = 0.f;
+    for (int t = 0; t < k; ++t)
+        psum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_mine), t));
+    e_out = e_mine;
+    w_out = p_mine / psum;
+    w_shared = 0.f;
+    if (has) {
+        const float ls = DEV ? load_dev(lr + E) : lr[E];
+        w_shared = 1.f / (1.f + expf(-ls));
+    }
+}
+
 template <int BF16>
 __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     extern __shared__ __align__(16) unsigned char rsmem[];     // norm: the normalised rows [R][H]
@@ -367,43 +412,17 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     // 2. per row (one wave a row): k maxima of the keys, softmax weights over the picks, the shared gate's sigmoid
     const int NW = RT / 64;
     for (int r = wave; r < R; r += NW) {
-        const float* lr = logits + (size_t)r * C;
-        uint32_t key[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = lane + 64 * q;
-            key[q] = e < a.E ? (bf16_order(load_dev(lr + e)) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
-        }
-        // the k maxima first (lane t keeps pick t), then their exponentials at once; the sum runs in pick order
-        float l_mine = 0.f;
-        int e_mine = -1;
-        for (int t = 0; t < a.k; ++t) {
-            uint32_t m = key[0] > key[1] ? key[0] : key[1];
-            const uint32_t m2 = key[2] > key[3] ? key[2] : key[3];
-            m = m > m2 ? m : m2;
-            m = wave_max_u32(m);
-            const int e = (int)(0xFFFFu - (m & 0xFFFFu));
-            if (lane == t) {
-                e_mine = e;
-                l_mine = bf16_unorder(m >> 16);
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (lane + 64 * q == e) key[q] = 0u;
-        }
-        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_mine), 0));   // pick 0's
-        const float p_mine = expf(l_mine - mx);
-        float psum = 0.f;
-        for (int t = 0; t < a.k; ++t)
-            psum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_mine), t));
+        int e_mine;
+        float w_mine, w_shared;
+        topk_row<true>(logits + (size_t)r * C, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
         if (lane < a.k) {
             pick_out[r * slots + lane] = e_mine;
-            wts_out[r * slots + lane] = p_mine / psum;
+            wts_out[r * slots + lane] = w_mine;
             sh_pick[r * slots + lane] = e_mine;
         }
         if (has && lane == 0) {
             pick_out[r * slots + a.k] = a.shared_id;
-            wts_out[r * slots + a.k] = 1.f / (1.f + expf(-load_dev(lr + a.E)));
+            wts_out[r * slots + a.k] = w_shared;
             sh_pick[r * slots + a.k] = a.shared_id;
         }
     }
@@ -1107,6 +1126,100 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// esp_route_rows: a whole prompt's routing in two launches. The router logits on the fp64 matrix cores: a workgroup is
+// RL_WAVES waves on one tile of 16 rows x 16 router columns (column E is the shared gate), wave w summing the products
+// of K range w with v_mfma_f64_16x16x4f64. Lane (i, q) of a wave feeds row i's and column i's elements at the same k;
+// a step of 32 k gives lane group q the 8 from 8 q (one 16-byte load a lane, 64 contiguous bytes a row), so each MFMA
+// adds 4 products and the steps cover every k once.
+// bf16 x bf16 products are exact in fp64 and so are their sums for ordinary data, so after the one rounding (bf16 for
+// the experts, fp32 for the shared gate) the logits equal route_group's, whose sums run in another order. The waves'
+// partials are added in wave order. Then route_topk_kernel: one wave a row (topk_row).
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int RL_WAVES = 4;
+constexpr int RL_BATCH = 4;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// 8 consecutive k of one row (xv) and one router column (gv): 8 MFMAs, in k order
+template <int BF16>
+__device__ __forceinline__ f64x4 route_mfma8(uint4 xv, uint4 gv, f64x4 acc) {
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t xh = (t & 1) ? xw[t >> 1] >> 16 : xw[t >> 1] & 0xFFFFu;
+        const uint32_t gh = (t & 1) ? gw[t >> 1] >> 16 : gw[t >> 1] & 0xFFFFu;
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(bits16_to_f64(xh, BF16), bits16_to_f64(gh, BF16), acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+template <int BF16>
+__global__ __launch_bounds__(RL_WAVES * 64) void route_logits_kernel(const uint16_t* __restrict__ x, int x_stride,
+                                                                     const uint16_t* __restrict__ gate,
+                                                                     const uint16_t* __restrict__ sgate, int R, int H,
+                                                                     int E, int C, float* __restrict__ logits) {
+    __shared__ double part[RL_WAVES - 1][4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 15, q = lane >> 4;
+    const int r0 = blockIdx.y * 16, c0 = blockIdx.x * 16;
+    const int r = r0 + i < R ? r0 + i : R - 1;                 // rows and columns past the ends: their sums unused
+    const int c = c0 + i < C ? c0 + i : C - 1;
+    const uint16_t* xr = x + (size_t)r * x_stride;
+    const uint16_t* gr = c < E ? gate + (size_t)c * H : sgate;
+    const int kw = H / RL_WAVES;                                // elements of a wave, a multiple of 64
+    const int kb = wave * kw + 8 * q;                           // a row's 4 lane groups read 64 contiguous bytes
+    f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+    int k = 0;
+    for (; k + 32 * RL_BATCH <= kw; k += 32 * RL_BATCH) {       // RL_BATCH loads in flight before the first MFMA
+        uint4 xv[RL_BATCH], gv[RL_BATCH];
+#pragma unroll
+        for (int j = 0; j < RL_BATCH; ++j) {
+            xv[j] = *reinterpret_cast<const uint4*>(xr + kb + k + 32 * j);
+            gv[j] = *reinterpret_cast<const uint4*>(gr + kb + k + 32 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < RL_BATCH; ++j) acc = route_mfma8<BF16>(xv[j], gv[j], acc);
+    }
+    for (; k < kw; k += 32)
+        acc = route_mfma8<BF16>(*reinterpret_cast<const uint4*>(xr + kb + k),
+                                *reinterpret_cast<const uint4*>(gr + kb + k), acc);
+    // lane l holds D[l / 16 + 4 v][l % 16], v = 0..3 (the f64 instruction's layout, unlike the f32 ones' 4 (l / 16) + v)
+    if (wave > 0) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wave - 1][v][lane] = acc[v];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        double sum = acc[v];
+        for (int w = 1; w < RL_WAVES; ++w) sum += part[w - 1][v][lane];
+        const int row = r0 + q + 4 * v, col = c0 + i;
+        if (row < R && col < C) logits[(size_t)row * C + col] = col < E ? bf2f(f64_to_bf16(sum)) : (float)sum;
+    }
+}
+
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int R, int E, int k,
+                                                         int shared_id, int* __restrict__ pick_out,
+                                                         float* __restrict__ wts_out) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= R) return;                                        // wave-uniform
+    const bool has = shared_id >= 0;
+    const int C = E + has, slots = k + has;
+    int e_mine;
+    float w_mine, w_shared;
+    topk_row<false>(logits + (size_t)r * C, E, k, has, lane, e_mine, w_mine, w_shared);
+    if (lane < k) {
+        pick_out[(size_t)r * slots + lane] = e_mine;
+        wts_out[(size_t)r * slots + lane] = w_mine;
+    }
+    if (has && lane == 0) {
+        pick_out[(size_t)r * slots + k] = shared_id;
+        wts_out[(size_t)r * slots + k] = w_shared;
+    }
+}
+
 }  // namespace esp
 
 // ======================================================================================================================
@@ -1211,48 +1324,36 @@ static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, i
     return esp_host::launch_check("route_group");
 }
 
-// esp_route_rows: route_group_kernel over windows of ROUTE_WIN rows side by side (blockIdx.y), without the grouping
-constexpr int ROUTE_WIN = 32;
-
 extern "C" int esp_route_rows(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
                               int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
-                              int64_t logits_numel, int32_t* counters, int64_t counters_numel, int32_t* pick_out,
-                              float* wts_out, void* stream) {
+                              int64_t logits_numel, int32_t* pick_out, float* wts_out, void* stream) {
     const int has = shared_id >= 0;
-    ESP_REQUIRE(x && gate && logits && counters && pick_out && wts_out, "route_rows: null pointer");
+    ESP_REQUIRE(x && gate && logits && pick_out && wts_out, "route_rows: null pointer");
     ESP_REQUIRE(x_dtype == ESP_BF16 || x_dtype == ESP_F16, "x: bf16/fp16");
     ESP_REQUIRE(E >= 1 && E <= 256 && k >= 1 && k <= 16 && k <= E && H % 256 == 0 && H > 0,
                 "route_rows: shape limits");
-    ESP_REQUIRE(E + has <= RT_MAX_IDS && k + has <= 32, "route_rows: too many router columns or slots");
+    ESP_REQUIRE(k + has <= 32, "route_rows: at most 32 slots a row");
     ESP_REQUIRE(!has || sgate, "the shared gate weight is needed with a shared slot");
-    ESP_REQUIRE(R >= 1 && R <= 65535LL * ROUTE_WIN, "route_rows: 1 to 2097120 rows");
-    const int64_t windows = (R + ROUTE_WIN - 1) / ROUTE_WIN;
+    ESP_REQUIRE(R >= 1 && (R + 15) / 16 <= 65535, "route_rows: 1 to 1048560 rows");
     ESP_REQUIRE(logits_numel >= R * (E + has), "logits scratch too small");
-    ESP_REQUIRE(counters_numel >= 32 * windows, "route_rows: counters need 32 ints a window of 32 rows");
-    ESP_REQUIRE(x_stride >= H && x_stride % 4 == 0, "x row stride");
-    ESP_REQUIRE(((uintptr_t)x & 7) == 0 && ((uintptr_t)gate & 7) == 0 && (!sgate || ((uintptr_t)sgate & 7) == 0),
-                "route_rows: x / gate must be 8-byte aligned");
-    RouteArgs a{};
-    a.x = static_cast<const uint16_t*>(x);
-    a.gate = static_cast<const uint16_t*>(gate);
-    a.sgate = static_cast<const uint16_t*>(sgate);
-    a.logits = logits;
-    a.counter = counters;
-    a.pick_out = pick_out;
-    a.wts_out = wts_out;
-    a.x_stride = (int)x_stride;
-    a.bf16 = x_dtype == ESP_BF16;
-    a.R = (int)R;
-    a.H = (int)H;
-    a.E = (int)E;
-    a.k = (int)k;
-    a.shared_id = (int)shared_id;
-    a.win = ROUTE_WIN;
-    const dim3 grid((unsigned)((E + has + RT_COLS - 1) / RT_COLS), (unsigned)windows);
-    if (a.bf16)
-        route_group_kernel<1><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+    ESP_REQUIRE(x_stride >= H && x_stride % 8 == 0, "route_rows: x row stride a multiple of 8 elements");
+    ESP_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)gate & 15) == 0 && (!sgate || ((uintptr_t)sgate & 15) == 0),
+                "route_rows: x / gate must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const int C = (int)(E + has);
+    const dim3 grid((unsigned)((C + 15) / 16), (unsigned)((R + 15) / 16));
+    const uint16_t *xp = static_cast<const uint16_t*>(x), *gp = static_cast<const uint16_t*>(gate),
+                   *sp = static_cast<const uint16_t*>(sgate);
+    if (x_dtype == ESP_BF16)
+        route_logits_kernel<1><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, sp, (int)R, (int)H, (int)E, C,
+                                                               logits);
     else
-        route_group_kernel<0><<<grid, RT, 0, (hipStream_t)stream>>>(a);
+        route_logits_kernel<0><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, sp, (int)R, (int)H, (int)E, C,
+                                                               logits);
+    int rc = esp_host::launch_check("route_rows logits");
+    if (rc) return rc;
+    route_topk_kernel<<<(unsigned)((R + 3) / 4), 256, 0, st>>>(logits, (int)R, (int)E, (int)k, (int)shared_id,
+                                                               pick_out, wts_out);
     return esp_host::launch_check("route_rows");
 }
 

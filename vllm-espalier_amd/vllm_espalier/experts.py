@@ -370,7 +370,7 @@ def windows(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
 class PrefillScratch:
     """The buffers of one whole-prompt MoE pass (prefill) for up to `rows` tokens of `slots` picks: the pipeline's
     tables and activations for P = rows * slots slot rows, the grouping over the whole prompt (members [maxu][rows]),
-    and route_rows' logits and counters (one 32-int line a window of `window` = 32 rows)."""
+    and route_rows' logits."""
 
     def __init__(self, E: int, D: int, I: int, rows: int, slots: int, device, window: int = 32):
         self.rows, self.slots, self.E, self.window = rows, slots, E, window
@@ -383,7 +383,7 @@ class PrefillScratch:
             "y": ((P, D), f32, 0),
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
-            "route_counters": ((32 * -(-rows // window),), i32, 0), "logits": ((rows * E,), f32, 0),
+            "logits": ((rows * E,), f32, 0),
         }
         for name, (shape, dtype, fill) in layout.items():
             setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
@@ -425,7 +425,7 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     if pick is None:
         if gate is None:
             raise ValueError("prefill needs the picks or the router weight")
-        e.route_rows(x, gate, L.gate_w, k, L.shared_id, s.logits, s.route_counters, pick_p, wts_p)
+        e.route_rows(x, gate, L.gate_w, k, L.shared_id, s.logits, pick_p, wts_p)
         e.group(pick_p, ids, s.count, members, T, slots, L.E)
     else:
         e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, T, k,
