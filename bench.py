@@ -581,6 +581,85 @@ def rocprof_summary(d: str, top: int = 30) -> str:
 
 
 # ---------------------------------------------------------------------------------------------------------------
+PHASE_ROOT = CSRC / "_phase"         # csrc/build.py --phase-trace puts the timing copy of the package here
+PHASE_NAMES = ("start", "copies issued", "rows ready", "K loop (wave 0)", "partials stored", "arrived last",
+               "finished")
+
+
+def phase_trace(dev) -> dict:
+    """Where a batch-1 dense launch spends its time, from the timing build (csrc/build.py --phase-trace: thread 0 of
+    every workgroup records the 100 MHz real-time counter at each phase of the launch, dense.hpp). Each of config 2's
+    four launches runs in a graph of 24 back-to-back launches over one weight copy (timed with HIP events), then one
+    more replay whose last launch's records are read back. Times are ns from the launch's first workgroup start;
+    each phase is the median (and 90th percentile) over workgroups of the time since the previous phase, the
+    finisher's phases over the finishers (the last split of each column block to arrive)."""
+    import ctypes
+    import numpy as np
+    import torch
+    import vllm_espalier
+    pkg = Path(vllm_espalier.__file__).resolve().parent
+    if pkg.parent != PHASE_ROOT.resolve():
+        raise RuntimeError(f"--phase-trace needs the timing build (csrc/build.py --phase-trace); imported {pkg}")
+    lib = ctypes.CDLL(str(pkg / "libespalier_hip.so"))
+    lib.esp_phase_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    words = 8192 * 8
+    buf = np.zeros(words, dtype=np.uint64)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    block = dense_block(gen, dev)
+    res = {}
+    for M in (1, 32):
+        for d, nm in zip(block, ("qkv", "o", "shared gate/up", "shared down")):
+            x = torch.randn((M, d.K), generator=gen, device=dev).to(torch.bfloat16)
+            y = torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev)
+            reps = 24
+
+            def fn():
+                for _ in range(reps):
+                    d.forward(x, out=y)
+            g = graph_of(fn)
+            us = time_graph(g, 20) * 1000 / reps
+            if lib.esp_phase_clear() != 0:
+                raise RuntimeError("esp_phase_clear failed")
+            g.replay()
+            torch.cuda.synchronize()
+            if lib.esp_phase_read(buf.ctypes.data, words) != 0:
+                raise RuntimeError("esp_phase_read failed")
+            del g
+            t = buf.reshape(-1, 8).astype(np.int64)
+            wg = np.nonzero(t[:, 0] > 0)[0]
+            T = t[wg]
+            rel = (T[:, :7] - T[:, 0].min()) * 10
+            fin = (T[:, 7] >> 8) & 1 == 1
+            xcd = T[:, 7] & 0xF
+
+            def stat(v):
+                return {"p50": float(np.median(v)), "p90": float(np.percentile(v, 90))}
+            ph = {PHASE_NAMES[0]: stat(rel[:, 0])}
+            for i in range(1, 5):
+                ph[PHASE_NAMES[i]] = stat(rel[:, i] - rel[:, i - 1])
+            for i in (5, 6):
+                ph[PHASE_NAMES[i]] = stat(rel[fin, i] - rel[fin, i - 1])
+            res[f"{nm}, M={M}"] = {
+                "us_per_launch": round(us, 2), "workgroups": int(len(wg)), "finishers": int(fin.sum()),
+                "span_us": round(float(rel[fin, 6].max()) / 1000, 2),
+                "stored_p50_us": round(float(np.median(rel[:, 4])) / 1000, 2),
+                "xcd_is_workgroup_mod_8": bool(np.all(xcd == wg % 8)), "phases_ns": ph}
+            log(f"phase trace {nm} M={M}: {us:.2f} us a launch, span {res[f'{nm}, M={M}']['span_us']} us")
+    return res
+
+
+def phase_table(res: dict) -> str:
+    """The markdown table of phase_trace's result (medians, ns)."""
+    head = ["launch", "us a launch (graph)", "workgroups", *PHASE_NAMES[1:], "last finisher done (us)"]
+    lines = ["| " + " | ".join(head) + " |", "|" + "---|" * len(head)]
+    for k, r in res.items():
+        ph = r["phases_ns"]
+        cells = [k, f"{r['us_per_launch']:.2f}", f"{r['workgroups']}",
+                 *(f"{ph[n]['p50']:.0f} ({ph[n]['p90']:.0f})" for n in PHASE_NAMES[1:]), f"{r['span_us']:.2f}"]
+        lines.append("| " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -600,6 +679,8 @@ def main() -> int:
                     "passes over the expert kernels and the LM head, and exit")
     ap.add_argument("--probes", action="store_true", help="measure the ceilings the kernels are held to (graph "
                     "launch floor, streaming read bandwidth, VALU issue rates) and exit")
+    ap.add_argument("--phase-trace", action="store_true", help="time the phases of config 2's batch-1 launches with "
+                    "the timing build (csrc/build.py --phase-trace) and exit")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
@@ -618,6 +699,9 @@ def main() -> int:
         print("bench.py: no GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if a.phase_trace:                         # the timing copy of the package, in place of the product one
+        sys.path[:] = [p for p in sys.path if Path(p).resolve() != (REPO / "vllm-espalier_amd").resolve()]
+        sys.path.insert(0, str(PHASE_ROOT))
     from vllm_espalier import experts as G
     G.ext()                                   # the HIP extension must be there: no fallback
     name = torch.cuda.get_device_name(dev)
@@ -630,6 +714,11 @@ def main() -> int:
         return 0
     if a.probes:
         print(json.dumps({"probes": probes(dev), "device": name}), flush=True)
+        return 0
+    if a.phase_trace:
+        res = phase_trace(dev)
+        print(phase_table(res), flush=True)
+        print(json.dumps({"phase_trace": res, "device": name}), flush=True)
         return 0
 
     # ---- config 2 dense block, cold stack

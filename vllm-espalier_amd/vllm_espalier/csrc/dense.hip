@@ -440,3 +440,19 @@ extern "C" int esp_dense_noalloc(const void* x, int x_dtype, int64_t x_stride, i
                       y_cols, fused ? nullptr : xh, xh_numel, SK > 1 ? Z : nullptr, z_numel, counters,
                       counters_numel, k2, cb, SK, W, rot_smem, nullptr, stream);
 }
+
+#ifdef ESP_PHASE_TRACE
+// The timing build's phase records of esp_dense's workgroups (dense.hpp): copy n words out, or clear them all
+extern "C" int esp_phase_read(unsigned long long* host, int64_t n) {
+    ESP_REQUIRE(host && n >= 0 && n <= (int64_t)esp::PHASE_WGS * 8, "phase_read: 0 to %d words", esp::PHASE_WGS * 8);
+    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(esp::g_phase), (size_t)n * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "phase_read: copy failed");
+    return esp_host::ok();
+}
+extern "C" int esp_phase_clear(void) {
+    static unsigned long long zero[esp::PHASE_WGS * 8];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(esp::g_phase), zero, sizeof(zero), 0, hipMemcpyHostToDevice) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "phase_clear: copy failed");
+    return esp_host::ok();
+}
+#endif

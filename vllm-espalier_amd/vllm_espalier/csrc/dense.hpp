@@ -13,6 +13,38 @@ namespace esp {
 
 constexpr int MAX_SHARDS = 4;
 
+#ifdef ESP_PHASE_TRACE
+// Timing build only (build.py --phase-trace; bench.py --phase-trace reads it): thread 0 of each workgroup records the
+// 100 MHz real-time counter at the phases of dense_program into g_phase[workgroup][8]: 0 start, 1 the first stage's
+// copies issued, 2 input rows ready, 3 its own wave's K loop done, 4 partials stored, 5 last to arrive (the finisher),
+// 6 the finisher's stores drained; slot 7 holds the XCD (bits 0-3) and 1 << 8 for a finisher. The arithmetic is the
+// product build's; only the finisher's final drain is added.
+constexpr int PHASE_WGS = 8192;
+static __device__ unsigned long long g_phase[PHASE_WGS * 8];
+__device__ __forceinline__ int phase_wg() { return (int)(blockIdx.x + blockIdx.y * gridDim.x); }
+__device__ __forceinline__ void phase_mark(int slot) {
+    if (threadIdx.x == 0 && phase_wg() < PHASE_WGS) g_phase[phase_wg() * 8 + slot] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void phase_xcd(int finisher) {
+    if (threadIdx.x == 0 && phase_wg() < PHASE_WGS) {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        g_phase[phase_wg() * 8 + 7] = (unsigned long long)(xcc & 0xFu) | ((unsigned long long)finisher << 8);
+    }
+}
+#define ESP_PHASE(slot) esp::phase_mark(slot)
+#define ESP_PHASE_XCD(finisher) esp::phase_xcd(finisher)
+#define ESP_PHASE_DRAIN()               \
+    do {                                \
+        __builtin_amdgcn_s_waitcnt(0);  \
+        __syncthreads();                \
+    } while (0)
+#else
+#define ESP_PHASE(slot) ((void)0)
+#define ESP_PHASE_XCD(finisher) ((void)0)
+#define ESP_PHASE_DRAIN() ((void)0)
+#endif
+
 struct Shard {
     const uint32_t* T;       // trellis words [K/16][N/16][4*K2]
     const uint16_t* suh;     // [K]
@@ -132,19 +164,25 @@ template <int CB, int K2, int MG, bool MULTI>
 __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg, const int split, unsigned char* smem,
                                               int& last, float* npart, float* ninv) {
     // a consumer group's ticket, taken first so its round trip overlaps the producer's work
+    ESP_PHASE(0);
+    ESP_PHASE_XCD(0);
     unsigned long long ticket = 0;
     if (MULTI && a.wait_done && threadIdx.x == 0)
         ticket = __hip_atomic_fetch_add(a.pass + (size_t)nbg * DONE_STRIDE, 1ull, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
-    // What the first copy needs -- every shard's trellis pointer, first block and width, the split and the launch
-    // shape -- in one round of kernel-argument loads, consumed together by one empty asm: an indexed load of the
-    // workgroup's shard would wait for the shard's selection, and each later first use for its own round trip.
+    // What the first copy and the input rows need -- every shard's trellis and sign pointers, first block and width,
+    // the split and the launch shape -- in one round of kernel-argument loads, consumed together by one empty asm: an
+    // indexed load of the workgroup's shard would wait for the shard's selection, and each later first use for its
+    // own round trip.
     const Shard* sa = a.s;
     const uint32_t* T4[MAX_SHARDS];
+    const uint16_t *suh4[MAX_SHARDS], *svh4[MAX_SHARDS];
     int nb04[MAX_SHARDS], nb4[MAX_SHARDS];
 #pragma unroll
     for (int i = 0; i < MAX_SHARDS; ++i) {
         T4[i] = sa[i].T;
+        suh4[i] = sa[i].suh;
+        svh4[i] = sa[i].svh;
         nb04[i] = sa[i].nb0;
         nb4[i] = sa[i].nb;
     }
@@ -153,27 +191,30 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     asm volatile("" ::"s"(T4[0]), "s"(T4[1]), "s"(T4[2]), "s"(T4[3]), "s"(nb04[0]), "s"(nb04[1]), "s"(nb04[2]),
                  "s"(nb04[3]), "s"(nb4[0]), "s"(nb4[1]), "s"(nb4[2]), "s"(nb4[3]), "s"(an), "s"(aM), "s"(aSQ),
                  "s"(aSR), "s"(anorm), "s"(afused), "s"(nthreads));
+    asm volatile("" ::"s"(suh4[0]), "s"(suh4[1]), "s"(suh4[2]), "s"(suh4[3]), "s"(svh4[0]), "s"(svh4[1]),
+                 "s"(svh4[2]), "s"(svh4[3]));
     int si = 0;
 #pragma unroll
     for (int i = 1; i < MAX_SHARDS; ++i)
         if (i < an && nbg >= nb04[i]) si = i;
-    // the copy's fields picked among the loaded ones; the rest of the shard read by index where first used
+    // the shard's fields picked among the loaded ones; its output column and factor read by index (first used at the
+    // end, so their round trip is hidden)
     struct {
         const uint32_t* T;
         int nb0, nb;
         const uint16_t *suh, *svh;
         int col0;
         float scale;
-    } S{T4[0], nb04[0], nb4[0], nullptr, nullptr, 0, 0.f};
+    } S{T4[0], nb04[0], nb4[0], suh4[0], svh4[0], 0, 0.f};
 #pragma unroll
     for (int i = 1; i < MAX_SHARDS; ++i)
         if (si == i) {
             S.T = T4[i];
             S.nb0 = nb04[i];
             S.nb = nb4[i];
+            S.suh = suh4[i];
+            S.svh = svh4[i];
         }
-    S.suh = a.s[si].suh;
-    S.svh = a.s[si].svh;
     S.col0 = a.s[si].col0;
     S.scale = a.s[si].scale;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
@@ -202,6 +243,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
     }
     const uint2 sv = *reinterpret_cast<const uint2*>(S.svh + cb_local * 128 + 4 * l32);
+    ESP_PHASE(1);
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
     RowsA<MG, true> al;       // fused: the rotated rows in shared memory
@@ -274,12 +316,14 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     }
 
     // 2. the K loop (its first wait is a workgroup barrier, after which the rotated rows are visible)
+    ESP_PHASE(2);
     f32x4 acc[2][MG];
     if (a.fused)
         block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, al, acc, true);
     else
         block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, ag, acc, true);
 
+    ESP_PHASE(3);
     // 3. the block's [M][128] sums: every wave's partials in shared memory (the stages are no longer read), the KW
     // k slots added in order
     __syncthreads();
@@ -304,6 +348,11 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             finish(v, l32, sv, S.scale);
             store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
         }
+        ESP_PHASE(4);
+        ESP_PHASE(5);
+        ESP_PHASE_XCD(1);
+        ESP_PHASE_DRAIN();
+        ESP_PHASE(6);
         if (coherent) signal_done(a, nbg);
         return;
     }
@@ -313,7 +362,10 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     for (int r = wave * 2 + half; r < M; r += 2 * NW)
         zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
     int* const cnt_p = a.counters + (size_t)nbg * a.cnt_stride;
+    ESP_PHASE(4);
     if (!arrive_last(cnt_p, a.SK, &last)) return;
+    ESP_PHASE(5);
+    ESP_PHASE_XCD(1);
     const size_t zsplit = (size_t)M * zrow;
     if (a.gather) {
         // every (row, split) partial in flight at once, one a 32-lane half, through shared memory (the k slots'
@@ -336,6 +388,8 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
         }
         if (threadIdx.x == 0) store_dev(cnt_p, 0);
+        ESP_PHASE_DRAIN();
+        ESP_PHASE(6);
         if (coherent) signal_done(a, nbg);
         return;
     }
@@ -361,6 +415,8 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
         store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
     }
     if (threadIdx.x == 0) store_dev(cnt_p, 0);  // every split of the block arrived
+    ESP_PHASE_DRAIN();
+    ESP_PHASE(6);
     if (coherent) signal_done(a, nbg);
 }
 
