@@ -689,7 +689,8 @@ __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_
 // waves a SIMD nothing hides it. Stage s holds AST_STEPS steps: the block's tiles, then one slice of AST_STEPS * 32
 // halves a member row, AST_ROW halves apart (16 bytes of padding keep the 16 rows an MFMA reads on different banks).
 // Each wave takes the same steps in the same order as block_gemm, so the sums are bit-identical to grouped_body's.
-constexpr int AST_STEPS = 8;
+constexpr int AST_STEPS = 4;
+constexpr int AST_MIN_STEPS = 9;         // K ranges of at least this many steps take the staged path
 constexpr int AST_ROW = AST_STEPS * 32 + 8;
 __host__ __device__ constexpr int staged_buf_bytes(int k2) { return AST_STEPS * 2 * 32 * k2 * 4 + 32 * AST_ROW * 2; }
 
@@ -1474,7 +1475,7 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.hi = (int)hi;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK * mt));
     // K ranges of more than two stages' worth of steps stage the member rows with the tiles (grouped_body_staged)
-    a.staged = (K / SK) / 32 > 2 * AST_STEPS;
+    a.staged = (K / SK) / 32 >= AST_MIN_STEPS;
     const size_t stage = a.staged ? 2 * (size_t)staged_buf_bytes((int)hi)
                                   : (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;   // the widest expert's
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
