@@ -159,6 +159,30 @@ def test_route_rows_equals_windows_and_oracle(dev, ext, R, shared):
     assert np.abs(wts.view(R, slots).cpu().numpy().astype(np.float64) - owts).max() < 1e-6
 
 
+@pytest.mark.parametrize("R", [1, 45])
+def test_route_rows_fp16_strided(dev, ext, R):
+    """route_rows with fp16 rows and router weights, the rows a view into wider rows (row stride 2304): the same
+    logits, picks and weights as route_group's fp16 path, window by window."""
+    print(f"route_rows fp16 R={R}", flush=True)
+    x, gate, sgate = router_inputs(R, 900 + R, near_ties=False)
+    x, gate, sgate = x.half(), gate.half(), sgate.half()
+    k, E, sid, slots = 8, 256, 256, 9
+    wide = torch.zeros((R, 2048 + 256), dtype=torch.float16)
+    wide[:, :2048] = x
+    xd = wide.to(dev)[:, :2048]
+    logits = torch.full((R * (E + 1),), float("nan"), dtype=torch.float32, device=dev)
+    pick = torch.full((R * slots,), -7, dtype=torch.int32, device=dev)
+    wts = torch.full((R * slots,), float("nan"), dtype=torch.float32, device=dev)
+    ext.route_rows(xd, gate.to(dev), sgate.to(dev), k, sid, logits, pick, wts)
+    torch.cuda.synchronize()
+    for r0 in range(0, R, 32):
+        n = min(32, R - r0)
+        lw, pw, ww, *_ = run_route(ext, dev, x[r0:r0 + n].contiguous(), gate, sgate, k, sid)
+        assert torch.equal(lw, logits[r0 * (E + 1):(r0 + n) * (E + 1)]), r0
+        assert torch.equal(pw.reshape(-1), pick[r0 * slots:(r0 + n) * slots]), r0
+        assert torch.equal(ww.reshape(-1), wts[r0 * slots:(r0 + n) * slots]), r0
+
+
 def test_route_group_rows_alone_and_graph(dev, ext):
     x, gate, sgate = router_inputs(8, 77, near_ties=False)
     logits, pick, wts, *_ = run_route(ext, dev, x, gate, sgate, 8, 256)

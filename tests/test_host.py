@@ -56,6 +56,25 @@ def test_dense_splits_cover_k_and_fit_the_rotation_buffer(K):
             assert 32 * (s1 - s0) <= 32 * ((S + SK - 1) // SK)          # the stage buffer's size
 
 
+@pytest.mark.parametrize("K,N", SHAPES + [(2048, 512), (1024, 1024), (8192, 4096)])
+def test_prompt_plan_is_valid(K, N):
+    """The prompt launches' K splits: whole 4-step stages a split, K of 512 or less unsplit, and at 512 rows (four
+    128-row tiles) a grid past one workgroup a CU filled as far as whole splits go: one more split would pass the
+    two-a-CU 512."""
+    sk = D.tile_plan(K, N)
+    assert 1 <= sk <= K // 128
+    if K <= 512:
+        assert sk == 1
+    per_split = 4 * (N // 128)
+    if per_split * sk > 256 and K > 512:
+        assert per_split * (sk + 1) > 512 or sk == K // 128
+
+
+def test_prompt_plan_config2():
+    """config 2's launches: qkv 3 splits (480 workgroups at 512 rows), o 4, shared gate/up 8, shared down 1."""
+    assert [D.tile_plan(K, N) for K, N in ((2048, 5120), (4096, 2048), (2048, 1024), (512, 2048))] == [3, 4, 8, 1]
+
+
 def test_dense_plan_depends_on_shape_only(monkeypatch):
     assert D.plan(2048, 5120, 256) == D.plan(2048, 5120, 256)
     monkeypatch.setenv("ESPALIER_DENSE_TILE_PLAN", "2,8,1")

@@ -1137,7 +1137,7 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
 // the experts, fp32 for the shared gate) the logits equal route_group's, whose sums run in another order. The waves'
 // partials are added in wave order. Then route_topk_kernel: one wave a row (topk_row).
 // ------------------------------------------------------------------------------------------------------------------
-constexpr int RL_WAVES = 4;
+constexpr int RL_WAVES = 8;
 constexpr int RL_BATCH = 4;
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
