@@ -709,19 +709,48 @@ __device__ __forceinline__ void grouped_body_staged(const GroupedArgs& a, const 
     const int kr = a.K / a.SK, k0 = split * kr, steps = kr >> 5;
     const int nst = (steps + AST_STEPS - 1) / AST_STEPS;
     unsigned char* const sbase = reinterpret_cast<unsigned char*>(stage);
-    // stage st into buffer st & 1: the tiles (every thread), then a member row a wave instruction (4 16-byte units a
-    // step, lanes past them idle), rows past nrows never copied (their A slots are read, their sums never stored)
+    // The copies' addresses, worked out once: a stage moves every trellis unit by whole k-tile rows and every member
+    // row's slice by whole steps, so a wave keeps its units' offsets inside a stage (issue_stage's units u = u0 +
+    // lane, u0 = wave * 64 + i * threads, 16-byte units of k-tile row u / UPR) and its member rows' offsets
+    // (rows wave, wave + NW, ...: at most 32 / 4).
+    constexpr int UPR = 2 * TW, TU = 2 * AST_STEPS * UPR, TU_IT = (TU + 255) / 256;
+    const int nthr = (int)blockDim.x;
+    int t_off[TU_IT];
+#pragma unroll
+    for (int i = 0; i < TU_IT; ++i) {
+        const int u = wave * 64 + i * nthr + lane, r = u / UPR;
+        t_off[i] = (r * NTILES + nt0) * TW + (u - r * UPR) * 4;
+    }
+    int a_row[8];                                           // wave-uniform: kept in scalar registers
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int m = wave + j * NW;
+        a_row[j] = __builtin_amdgcn_readfirstlane(m < nrows ? rows_sh[m] * a.K + k0 : 0);
+    }
+    const int lane8 = lane * 8;
+    const uint32_t* Tk = T + (size_t)(k0 >> 4) * NTILES * TW;      // the split's first k-tile row
+    // stage st into buffer st & 1: the tiles (every thread, as issue_stage), then a member row a wave instruction (4
+    // 16-byte units a step, lanes past them idle), rows past nrows never copied (their A slots are read, their sums
+    // never stored)
     auto issue = [&](int st) __attribute__((always_inline)) {
         const int first = st * AST_STEPS, n = steps - first < AST_STEPS ? steps - first : AST_STEPS;
         unsigned char* buf = sbase + (st & 1) * BUF_BYTES;
-        issue_stage<K2>(T, NTILES, (k0 >> 4) + 2 * first, 2 * n, nt0, reinterpret_cast<uint32_t*>(buf));
+        uint32_t* tb = reinterpret_cast<uint32_t*>(buf);
+        const uint32_t* Ts = Tk + (size_t)(2 * first) * NTILES * TW;
+#pragma unroll
+        for (int i = 0; i < TU_IT; ++i) {
+            const int u0 = wave * 64 + i * nthr;
+            if (u0 < 2 * n * UPR && u0 + lane < 2 * n * UPR)
+                __builtin_amdgcn_global_load_lds((global_void_ptr)(Ts + t_off[i]), (lds_void_ptr)(tb + u0 * 4), 16, 0,
+                                                 0);
+        }
         uint16_t* abuf = reinterpret_cast<uint16_t*>(buf + B_WORDS * 4);
-        for (int m = wave; m < nrows; m += NW) {
-            const int p = rows_sh[m];
-            if (lane < 4 * n) {
-                const uint16_t* src = abase + (size_t)p * a.K + k0 + first * 32 + lane * 8;
-                __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(abuf + m * AST_ROW), 16, 0, 0);
-            }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int m = wave + j * NW;
+            if (m < nrows && lane < 4 * n)
+                __builtin_amdgcn_global_load_lds((global_void_ptr)(abase + a_row[j] + first * 32 + lane8),
+                                                 (lds_void_ptr)(abuf + m * AST_ROW), 16, 0, 0);
         }
     };
     f32x4 acc[2][MG];
@@ -1003,12 +1032,14 @@ __global__ __launch_bounds__(1024) void down_combine_kernel(const float* __restr
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// The grouped kernel. MODE 0: esp_grouped. MODE 1 (esp_moe_gateup): the member rows' K range rotated into shared
-// memory in the launch (rot_in's arithmetic), and the last of the 2 * SK programs of an (expert, 128-column block) to
-// arrive runs gateup_epilogue for its member rows.
+// The grouped kernel. MODE 0: esp_grouped, its member rows read from global memory at each step. MODE 2: esp_grouped
+// with the member rows staged through shared memory (grouped_body_staged), an instance of its own so that its copy
+// plan's registers do not lower the occupancy of MODE 0. MODE 1 (esp_moe_gateup): the member rows' K range rotated
+// into shared memory in the launch (rot_in's arithmetic), and the last of the 2 * SK programs of an (expert,
+// 128-column block) to arrive runs gateup_epilogue for its member rows.
 // ------------------------------------------------------------------------------------------------------------------
 template <int MODE>
-__global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void grouped_kernel_t(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
     const int u = blockIdx.x;
@@ -1053,7 +1084,7 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
             else
                 *reinterpret_cast<float4*>(zp) = nan4;
         }
-        if constexpr (MODE == 0) return;
+        if constexpr (MODE != 1) return;
     }
     const bool runs = supported(cb, k2) && k2 >= a.lo && k2 <= a.hi;
     const uint16_t* abase = mat ? a.X1 : a.X0;
@@ -1086,7 +1117,7 @@ __global__ __launch_bounds__(1024) void grouped_kernel_t(GroupedArgs a) {
     case CB_ * 32 + K2_: {                                                                                    \
         constexpr int KCB = gemm_cb(CB_);                                                                     \
         const float scale = gemm_scale(CB_);                                                                  \
-        if (MODE == 0 && a.staged) {                                                                          \
+        if constexpr (MODE == 2) {                                                                            \
             if (two)                                                                                          \
                 grouped_body_staged<KCB, K2_, 2>(a, T, abase, rows_sh, nrows, mat, split, scale, stage);      \
             else                                                                                              \
@@ -1474,17 +1505,24 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.lo = (int)lo;
     a.hi = (int)hi;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK * mt));
-    // K ranges of more than two stages' worth of steps stage the member rows with the tiles (grouped_body_staged)
+    // K ranges of AST_MIN_STEPS steps or more stage the member rows with the tiles (grouped_body_staged), whose
+    // member-row offsets are 32-bit and whose waves hold at most 8 member rows each
     a.staged = (K / SK) / 32 >= AST_MIN_STEPS;
+    ESP_REQUIRE(!a.staged || (P * K < (int64_t(1) << 31) && warps >= 4),
+                "grouped: a staged launch needs P * K below 2^31 and at least 4 waves");
     const size_t stage = a.staged ? 2 * (size_t)staged_buf_bytes((int)hi)
                                   : (size_t)host_stage_words((int)hi, (int)(K / SK)) * 4;   // the widest expert's
     const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;                         // the k slots' partials
     const size_t smem = stage > red ? stage : red;
     if (smem > 64 * 1024 &&
-        hipFuncSetAttribute((const void*)grouped_kernel_t<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
+        hipFuncSetAttribute(a.staged ? (const void*)grouped_kernel_t<2> : (const void*)grouped_kernel_t<0>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) !=
             hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "grouped: cannot raise the shared memory limit to %zu bytes", smem);
-    grouped_kernel_t<0><<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
+    if (a.staged)
+        grouped_kernel_t<2><<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
+    else
+        grouped_kernel_t<0><<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("grouped");
 }
 
