@@ -168,7 +168,9 @@ int esp_down_combine(const float* Z, const int32_t* pick, const void* svh_d, flo
                      int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E, void* stream);
 
 /* Replaces `down_combine2` (experts.cpp:175-190, experts.cu:340-393, 541-559): as down_combine, the routed sum over
- * the first n_routed slots into out, and w * y of slot n_routed into out_shared (may be NULL), both in out_dtype. */
+ * the first n_routed slots into out, and w * y of slot n_routed into out_shared (may be NULL), both in out_dtype.
+ * y may be NULL here and in esp_down_combine (no counterpart in the reference, whose y is always given): then no
+ * slot's output is stored and an invalid pick adds zero instead of y's stored row. */
 int esp_down_combine2(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts, void* out,
                       int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK, int64_t slots,
                       int64_t E, int64_t n_routed, void* stream);

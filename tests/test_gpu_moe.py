@@ -329,6 +329,26 @@ def test_down_combine2_bit_exact(dev, ext, out_dtype):
     assert np.array_equal(oc.cpu().numpy(), wo_all)
 
 
+def test_down_combine2_without_y(dev, ext):
+    """y = None (esp_down_combine2 with a null y, the whole-prompt path): no per-slot outputs stored, and an invalid
+    pick adds zero, which is the oracle's sum over stale rows of zeros, bit for bit."""
+    gen = torch.Generator().manual_seed(9)
+    R, slots, E, Dd, SK = 5, 9, 20, 512, 1
+    P = R * slots
+    Z = torch.randn((SK, P, Dd), generator=gen)
+    pick = torch.randint(-2, E, (P,), generator=gen).to(torch.int32)
+    svh_d = torch.randn((E, Dd), generator=gen).half()
+    wts = torch.rand((P,), generator=gen)
+    out = torch.zeros((R, Dd), dtype=torch.bfloat16, device=dev)
+    osh = torch.zeros((R, Dd), dtype=torch.bfloat16, device=dev)
+    ext.down_combine2(Z.to(dev), pick.to(dev), svh_d.to(dev), None, wts.to(dev), out, osh, R, P, Dd, SK, slots, E,
+                      slots - 1)
+    wo, ws, _ = O.down_combine2(Z.numpy(), pick.numpy(), bits(svh_d), np.zeros((P, Dd), np.float32), wts.numpy(), R,
+                                P, Dd, SK, E, slots, slots - 1)
+    assert (pick < 0).any() and np.array_equal(bits(out), O.f32_to_bf16(wo))
+    assert np.array_equal(bits(osh), O.f32_to_bf16(ws))
+
+
 @pytest.mark.parametrize("slots", [4, 8, 13, 32])
 def test_down_combine2_slot_counts(dev, ext, slots):
     """down_combine2 launches a 32-lane half a slot (at least 256 threads, up to 1024 at 32 slots): bit-exact against

@@ -181,13 +181,14 @@ void group_shared(const at::Tensor& pick_in, const at::Tensor& wts_in, const at:
                           cur_stream()));
 }
 
-void down_combine2(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_d, at::Tensor y,
-                   const at::Tensor& wts, at::Tensor out, const c10::optional<at::Tensor>& out_shared, int64_t rows,
-                   int64_t P, int64_t D, int64_t SK, int64_t slots, int64_t E, int64_t n_routed) {
+void down_combine2(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor& svh_d,
+                   const c10::optional<at::Tensor>& y, const at::Tensor& wts, at::Tensor out,
+                   const c10::optional<at::Tensor>& out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK,
+                   int64_t slots, int64_t E, int64_t n_routed) {
     check(Z, at::kFloat, "Z");
     check(pick, at::kInt, "pick");
     check(svh_d, at::kHalf, "svh_d");
-    check(y, at::kFloat, "y");
+    if (y.has_value()) check(*y, at::kFloat, "y");   // None: no per-slot outputs stored (esp_down_combine2)
     check(wts, at::kFloat, "wts");
     TORCH_CHECK(out.is_cuda() && out.is_contiguous(), "out: contiguous CUDA");
     TORCH_CHECK(out.scalar_type() == at::kBFloat16 || out.scalar_type() == at::kHalf ||
@@ -199,7 +200,8 @@ void down_combine2(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor
     TORCH_CHECK(D % 128 == 0, "D must be a multiple of 128");
     TORCH_CHECK(n_routed <= slots, "n_routed <= slots");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(Z.device());
-    call(esp_down_combine2(cptr<float>(Z), cptr<int32_t>(pick), svh_d.data_ptr(), mptr<float>(y), cptr<float>(wts),
+    call(esp_down_combine2(cptr<float>(Z), cptr<int32_t>(pick), svh_d.data_ptr(),
+                           y.has_value() ? mptr<float>(*y) : nullptr, cptr<float>(wts),
                            out.data_ptr(), dtype_code(out), out_shared.has_value() ? out_shared->data_ptr() : nullptr,
                            rows, P, D, SK, slots, E, n_routed, cur_stream()));
 }

@@ -971,7 +971,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 // down epilogue of every slot of one (row r, 128-block) into part, then the routed fma chain in slot order and the
 // shared slot's gated output (experts.cu:340-393); n_routed == slots and out_shared == nullptr give down_combine. At
-// least 256 threads; every thread calls it.
+// least 256 threads; every thread calls it. y == nullptr: no slot's output is stored, and an invalid pick adds zero
+// (where it would reuse y's stored row).
 template <int OUT_DTYPE>
 __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, const int* __restrict__ pick,
                                                   const uint16_t* __restrict__ svh_d, float* __restrict__ y,
@@ -995,10 +996,10 @@ __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, c
             fwht128(v, l32);
 #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = v[j] * HAD_SCALE * sv[j];
-            *reinterpret_cast<float4*>(y + (size_t)p * D + n) = make_float4(o[0], o[1], o[2], o[3]);
+            if (y != nullptr) *reinterpret_cast<float4*>(y + (size_t)p * D + n) = make_float4(o[0], o[1], o[2], o[3]);
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = y[(size_t)p * D + n + j];   // an invalid pick reuses y's row
+            for (int j = 0; j < 4; ++j) o[j] = y != nullptr ? y[(size_t)p * D + n + j] : 0.f;   // reuses y's row
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) part[k][4 * l32 + j] = o[j];
@@ -1647,7 +1648,7 @@ extern "C" int esp_combine(const float* y, const float* wts, float* out, int64_t
 static int down_combine_any(const float* Z, const int32_t* pick, const void* svh_d, float* y, const float* wts,
                             void* out, int out_dtype, void* out_shared, int64_t rows, int64_t P, int64_t D, int64_t SK,
                             int64_t slots, int64_t E, int64_t n_routed, void* stream) {
-    ESP_REQUIRE(Z && pick && svh_d && y && wts && out, "down_combine: null pointer");
+    ESP_REQUIRE(Z && pick && svh_d && wts && out, "down_combine: null pointer");
     ESP_REQUIRE(slots >= 1 && slots <= 32, "at most 32 slots a row");
     ESP_REQUIRE(D % 128 == 0 && D > 0, "D must be a multiple of 128");
     ESP_REQUIRE(n_routed >= 0 && n_routed <= slots, "n_routed <= slots");

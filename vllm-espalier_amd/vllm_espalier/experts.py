@@ -380,7 +380,6 @@ class PrefillScratch:
         layout = {
             "xg": ((P, D), f16, 0), "xu": ((P, D), f16, 0), "xd": ((P, I), f16, 0),
             "z": ((P * max(2 * I * PREFILL_SK_GU, D),), f32, 0),     # the gate/up splits' partials, or down's sums
-            "y": ((P, D), f32, 0),
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
             "logits": ((rows * E,), f32, 0),
@@ -442,7 +441,8 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     if has_shared and out_shared is None:
         out_shared = torch.empty((T, L.D), dtype=x.dtype, device=x.device)
     shared_out = out_shared if has_shared else None
-    e.down_combine2(s.z, pick_p, L.svh_d, s.y, wts_p, out, shared_out, T, P, L.D, 1, slots, L.E, k)
+    # no per-slot outputs: nothing reads them, and every pick of route_rows / the caller's tables is valid
+    e.down_combine2(s.z, pick_p, L.svh_d, None, wts_p, out, shared_out, T, P, L.D, 1, slots, L.E, k)
     return out, shared_out
 
 
