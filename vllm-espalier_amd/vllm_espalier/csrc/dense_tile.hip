@@ -37,29 +37,32 @@ struct TileArgs {
     int T, K, SK, NBT, SQ, SR, RG;
 };
 
-// xh of tile_rot_kernel: a 32-lane half rotates one 128-chunk of one row for one matrix; rows past T (up to the last
-// row group's end) are zero
+// xh of tile_rot_kernel: a workgroup takes one matrix, one row group of 16 rows and one 128-chunk of K, which fill
+// exactly the 4 (row group, step) A blocks of that chunk: a 32-lane half rotates 2 rows (rows past T are zero) into
+// their fragment places in shared memory, then the 4 KiB go out as one 16-byte store a thread, contiguous in xh
 __global__ __launch_bounds__(256) void tile_rot_kernel(const void* __restrict__ x, int x_dtype, int x_stride, int T,
                                                        int K, int n, const uint16_t* suh0, const uint16_t* suh1,
                                                        const uint16_t* suh2, const uint16_t* suh3,
                                                        uint16_t* __restrict__ xh, int RG) {
-    const int l32 = threadIdx.x & 31;
-    const int nb = K >> 7, rows = RG * 16;
-    const long unit = (long)blockIdx.x * 8 + (threadIdx.x >> 5);      // (matrix, row, chunk)
-    if (unit >= (long)n * rows * nb) return;
-    const int ch = (int)(unit % nb);
-    const int r = (int)((unit / nb) % rows);
-    const int s = (int)(unit / ((long)nb * rows));
+    __shared__ __align__(16) uint16_t frag[4 * TILE_FRAG];
+    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    const int nb = K >> 7;
+    const int ch = (int)(blockIdx.x % nb), rg = (int)((blockIdx.x / nb) % RG), s = (int)(blockIdx.x / (nb * RG));
     const uint16_t* suh = s == 0 ? suh0 : s == 1 ? suh1 : s == 2 ? suh2 : suh3;
-    uint2 u = make_uint2(0u, 0u);
-    if (r < T) u = rot128(x, x_dtype, (size_t)r * x_stride + ch * 128, suh + ch * 128, l32);
-    // the lane's 4 consecutive k (kabs .. kabs + 3) are 4 consecutive halves of one A fragment lane
-    const int kabs = ch * 128 + 4 * l32;
-    const int step = kabs >> 5, kk = kabs & 31, kt = kk & 15;
+    // the lane's 4 consecutive k (ch * 128 + 4 l32 ...) are 4 consecutive halves of one A fragment lane
+    const int kk = (4 * l32) & 31, kt = kk & 15;
+    const int sl = l32 >> 3;                                  // the step inside the chunk
     const int G = 2 * (kk >> 4) + ((kt >> 2) & 1), hi = kt >> 3;
-    const int lane = (r & 15) + 16 * G;
-    uint16_t* dst = xh + ((((size_t)s * RG + (r >> 4)) * (K >> 5) + step) * 64 + lane) * 8 + 4 * hi;
-    *reinterpret_cast<uint2*>(dst) = u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rr = 2 * hw + i, r = rg * 16 + rr;
+        uint2 u = make_uint2(0u, 0u);
+        if (r < T) u = rot128(x, x_dtype, (size_t)r * x_stride + ch * 128, suh + ch * 128, l32);
+        *reinterpret_cast<uint2*>(frag + (sl * 64 + rr + 16 * G) * 8 + 4 * hi) = u;
+    }
+    __syncthreads();
+    uint16_t* dst = xh + (((size_t)s * RG + rg) * (K >> 5) + ch * 4) * TILE_FRAG;
+    reinterpret_cast<uint4*>(dst)[threadIdx.x] = reinterpret_cast<const uint4*>(frag)[threadIdx.x];
 }
 
 typedef __attribute__((address_space(3))) const f16x8* lds_f16x8_ptr;
@@ -303,8 +306,8 @@ extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int6
     const size_t red = (size_t)RED_BYTES + 16;                   // the sums, then the arrival flag
     const size_t smem = stage > red ? stage : red;
     hipStream_t st = (hipStream_t)stream;
-    const long units = (long)n_shards * RG * 16 * (K / 128);
-    tile_rot_kernel<<<(unsigned)((units + 7) / 8), 256, 0, st>>>(x, x_dtype, (int)x_stride, (int)T, (int)K,
+    const long units = (long)n_shards * RG * (K / 128);          // (matrix, row group, 128-chunk)
+    tile_rot_kernel<<<(unsigned)units, 256, 0, st>>>(x, x_dtype, (int)x_stride, (int)T, (int)K,
                                                                  (int)n_shards, su[0], su[1], su[2], su[3],
                                                                  static_cast<uint16_t*>(xh), (int)RG);
     int rc = esp_host::launch_check("dense_tile rotation");

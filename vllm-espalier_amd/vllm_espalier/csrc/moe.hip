@@ -570,25 +570,44 @@ __global__ __launch_bounds__(256) void shared_slots_kernel(const int* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// rot_in (experts.cu:97-115): one wave per (slot row, 128-block); lanes 0-31 the gate input, 32-63 the up input
+// rot_in (experts.cu:97-115): one workgroup a slot row p. Its pick is read once (workgroup-uniform, so the expert's
+// sign rows are scalar addresses); the row's 2 * K / 128 (matrix, 128-block) chunks go 4 a 32-lane half, every chunk's
+// row and sign loads in flight before the first rotation. A chunk's arithmetic is rot128's, so the bits are too.
 // ------------------------------------------------------------------------------------------------------------------
+constexpr int RI_CHUNKS = 4;                 // chunks a 32-lane half holds in flight
+
 __global__ __launch_bounds__(256) void rot_in_kernel(const uint16_t* __restrict__ x, int x_dtype, int x_stride,
                                                      const int* __restrict__ pick, const uint16_t* __restrict__ suh0,
                                                      const uint16_t* __restrict__ suh1, uint16_t* __restrict__ out0,
-                                                     uint16_t* __restrict__ out1, int P, int K, int slots, int E) {
-    const int l32 = threadIdx.x & 31, mat = (threadIdx.x >> 5) & 1;
-    const long unit = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int nb = K >> 7;
-    if (unit >= (long)P * nb) return;
-    const int p = (int)(unit / nb), blk = (int)(unit % nb);
-    const int row = p / slots;
-    // x's load goes out with the pick's; the sign vector's waits for the pick
-    RotIn in = rot128_load(x, x_dtype, (size_t)row * x_stride + blk * 128, suh0, l32);
+                                                     uint16_t* __restrict__ out1, int K, int slots, int E) {
+    const int p = blockIdx.x;
     const int e = pick[p];
-    if (e < 0 || e >= E) return;
-    in.su = *reinterpret_cast<const uint2*>((mat ? suh1 : suh0) + (size_t)e * K + blk * 128 + 4 * l32);
-    const uint2 u = rot128_apply(in, x_dtype, l32);
-    *reinterpret_cast<uint2*>((mat ? out1 : out0) + (size_t)p * K + blk * 128 + 4 * l32) = u;
+    if (e < 0 || e >= E) return;                         // workgroup-uniform: an invalid pick's rows stay as they are
+    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    const int nb = K >> 7, jobs = 2 * nb;                // chunk j: matrix j / nb, 128-block j % nb
+    const size_t xrow = (size_t)(p / slots) * x_stride, orow = (size_t)p * K;
+    const uint16_t* s0 = suh0 + (size_t)e * K;
+    const uint16_t* s1 = suh1 + (size_t)e * K;
+    for (int j0 = hw; j0 < jobs; j0 += 8 * RI_CHUNKS) {
+        RotIn in[RI_CHUNKS];
+#pragma unroll
+        for (int c = 0; c < RI_CHUNKS; ++c) {
+            const int j = j0 + 8 * c;
+            if (j < jobs) {
+                const int mat = j >= nb, blk = j - mat * nb;
+                in[c] = rot128_load(x, x_dtype, xrow + blk * 128, (mat ? s1 : s0) + blk * 128, l32);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < RI_CHUNKS; ++c) {
+            const int j = j0 + 8 * c;
+            if (j < jobs) {
+                const int mat = j >= nb, blk = j - mat * nb;
+                *reinterpret_cast<uint2*>((mat ? out1 : out0) + orow + blk * 128 + 4 * l32) =
+                    rot128_apply(in[c], x_dtype, l32);
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1453,12 +1472,12 @@ extern "C" int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const in
     ESP_REQUIRE(x_stride >= K && x_stride % 4 == 0, "x row stride");
     ESP_REQUIRE((((uintptr_t)x | (uintptr_t)suh0 | (uintptr_t)suh1 | (uintptr_t)out0 | (uintptr_t)out1) & 7) == 0,
                 "rot_in: x, suh and the outputs must be 8-byte aligned");
-    const long units = rows * slots * (K / 128);
-    if (units <= 0) return esp_host::ok();
-    rot_in_kernel<<<units_grid(units, 4), 256, 0, (hipStream_t)stream>>>(
+    ESP_REQUIRE(rows * slots < (int64_t(1) << 31), "rot_in: at most 2^31 - 1 slot rows");
+    if (rows * slots <= 0) return esp_host::ok();
+    rot_in_kernel<<<(unsigned)(rows * slots), 256, 0, (hipStream_t)stream>>>(
         static_cast<const uint16_t*>(x), x_dtype, (int)x_stride, pick, static_cast<const uint16_t*>(suh0),
-        static_cast<const uint16_t*>(suh1), static_cast<uint16_t*>(out0), static_cast<uint16_t*>(out1),
-        (int)(rows * slots), (int)K, (int)slots, (int)E);
+        static_cast<const uint16_t*>(suh1), static_cast<uint16_t*>(out0), static_cast<uint16_t*>(out1), (int)K,
+        (int)slots, (int)E);
     return esp_host::launch_check("rot_in");
 }
 
