@@ -349,6 +349,38 @@ def test_down_combine2_without_y(dev, ext):
     assert np.array_equal(bits(osh), O.f32_to_bf16(ws))
 
 
+@pytest.mark.parametrize("R,Dd,SK,slots,out_dtype,with_y", [(70, 640, 2, 9, torch.bfloat16, True),
+                                                          (64, 2048, 1, 9, torch.bfloat16, False),
+                                                          (100, 512, 3, 32, torch.float32, True),
+                                                          (65, 256, 1, 4, torch.float16, False)])
+def test_down_combine2_many_rows(dev, ext, R, Dd, SK, slots, out_dtype, with_y):
+    """From 64 rows down_combine2 runs a workgroup a row (blocks in groups of 4, the last one short when D / 128 is
+    not a multiple of 4): bit-exact against the oracle, invalid picks included, with y stored or absent."""
+    print(f"down_combine2 rows={R} D={Dd} SK={SK} slots={slots} {out_dtype} y={with_y}", flush=True)
+    gen = torch.Generator().manual_seed(R + Dd + slots)
+    E = 24
+    P = R * slots + 3
+    Z = torch.randn((SK, P, Dd), generator=gen)
+    pick = torch.randint(-2, E, (P,), generator=gen).to(torch.int32)
+    svh_d = torch.randn((E, Dd), generator=gen).half()
+    y0 = torch.randn((P, Dd), generator=gen) if with_y else torch.zeros((P, Dd))
+    wts = torch.rand((P,), generator=gen)
+    y = y0.clone().to(dev) if with_y else None
+    out = torch.zeros((R, Dd), dtype=out_dtype, device=dev)
+    osh = torch.zeros((R, Dd), dtype=out_dtype, device=dev)
+    ext.down_combine2(Z.to(dev), pick.to(dev), svh_d.to(dev), y, wts.to(dev), out, osh, R, P, Dd, SK, slots, E,
+                      slots - 1)
+    wo, ws, wy = O.down_combine2(Z.numpy(), pick.numpy(), bits(svh_d), y0.numpy(), wts.numpy(), R, P, Dd, SK, E,
+                                 slots, slots - 1)
+    if with_y:
+        assert np.array_equal(y.cpu().numpy()[:R * slots], wy[:R * slots])
+    if out_dtype == torch.float32:
+        assert np.array_equal(out.cpu().numpy(), wo) and np.array_equal(osh.cpu().numpy(), ws)
+    else:
+        cast = (lambda a: O.f32_to_bf16(a)) if out_dtype == torch.bfloat16 else (lambda a: a.astype(np.float16).view(np.uint16))
+        assert np.array_equal(bits(out), cast(wo)) and np.array_equal(bits(osh), cast(ws))
+
+
 @pytest.mark.parametrize("slots", [4, 8, 13, 32])
 def test_down_combine2_slot_counts(dev, ext, slots):
     """down_combine2 launches a 32-lane half a slot (at least 256 threads, up to 1024 at 32 slots): bit-exact against

@@ -19,7 +19,13 @@ constexpr float HAD_SCALE = 0.08838834764831845f;
 enum DType : int { F16 = 0, BF16 = 1, F32 = 2 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }   // RNE
+// fp32 -> fp16, RNE, of f as an fp32 value: the empty asm keeps the compiler from folding the operation that made f
+// into the conversion (a product would become one v_fma_mixlo_f16, rounded once to fp16, where the reference rounds
+// to fp32 first and then to fp16)
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 __device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) {                                                      // RNE
     uint32_t u = __builtin_bit_cast(uint32_t, f);

@@ -1051,6 +1051,84 @@ __global__ __launch_bounds__(1024) void down_combine_kernel(const float* __restr
                                  blockIdx.y, part);
 }
 
+// down_combine for many rows (a prompt): one workgroup (8 32-lane halves) a (row, group of DCR_BLOCKS 128-blocks), the
+// row's picks and weights read once into shared memory for the group; a half-wave takes up to DCR_U (slot, block)
+// units of the group with all their loads in flight, then the fma chain in slot order over the group's columns.
+// Element for element the arithmetic of down_combine_unit (a workgroup a (row, 128-block)), which the few-row launches
+// keep.
+constexpr int DCR_BLOCKS = 4, DCR_U = 5, DCR_ROWS = 64;   // DCR_ROWS: rows from which esp_down_combine* use this form
+
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(256) void down_combine_rows_kernel(const float* __restrict__ Z,
+                                                                const int* __restrict__ pick,
+                                                                const uint16_t* __restrict__ svh_d,
+                                                                float* __restrict__ y, const float* __restrict__ wts,
+                                                                void* __restrict__ out, void* __restrict__ out_shared,
+                                                                int P, int D, int SK, int E, int slots, int n_routed) {
+    extern __shared__ float dcr_part[];                      // [slots][DCR_BLOCKS * 128]
+    __shared__ float wts_sh[32];
+    __shared__ int e_sh[32];
+    constexpr int GW = DCR_BLOCKS * 128;
+    const int r = blockIdx.x, l32 = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    if ((int)threadIdx.x < slots) {
+        wts_sh[threadIdx.x] = wts[r * slots + threadIdx.x];
+        e_sh[threadIdx.x] = pick[r * slots + threadIdx.x];
+    }
+    __syncthreads();
+    const int nbt = D >> 7;
+    {
+        const int b0 = blockIdx.y * DCR_BLOCKS;
+        const int nbk = nbt - b0 < DCR_BLOCKS ? nbt - b0 : DCR_BLOCKS, units = slots * nbk;
+        for (int u0 = hw; u0 < units; u0 += 8 * DCR_U) {
+            float v[DCR_U][4], sv[DCR_U][4];
+#pragma unroll
+            for (int i = 0; i < DCR_U; ++i) {               // every unit's loads first
+                const int u = u0 + 8 * i;
+                if (u < units) {
+                    const int k = u / nbk, n = (b0 + u - k * nbk) * 128 + 4 * l32, e = e_sh[k];
+                    sum_splits4(Z + (size_t)(r * slots + k) * D + n, (size_t)P * D, SK, v[i]);
+                    if (e >= 0 && e < E) load4_f16(svh_d + (size_t)e * D + n, sv[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < DCR_U; ++i) {
+                const int u = u0 + 8 * i;
+                if (u < units) {                            // uniform over the half-wave
+                    const int k = u / nbk, bl = u - k * nbk, n = (b0 + bl) * 128 + 4 * l32, e = e_sh[k];
+                    const size_t pi = (size_t)(r * slots + k) * D + n;
+                    float o[4];
+                    if (e >= 0 && e < E) {
+                        fwht128(v[i], l32);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] = v[i][j] * HAD_SCALE * sv[i][j];
+                        if (y != nullptr) *reinterpret_cast<float4*>(y + pi) = make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) o[j] = y != nullptr ? y[pi + j] : 0.f;   // reuses y's row
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dcr_part[k * GW + bl * 128 + 4 * l32 + j] = o[j];
+                }
+            }
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < nbk * 128; c += 256) {
+            const size_t at = (size_t)r * D + b0 * 128 + c;
+            float acc = 0.f;
+            for (int q = 0; q < n_routed; ++q) acc = fmaf(wts_sh[q], dcr_part[q * GW + c], acc);
+            if constexpr (OUT_DTYPE == F32) static_cast<float*>(out)[at] = acc;
+            else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out)[at] = f2bf(acc);
+            else static_cast<uint16_t*>(out)[at] = f2h(acc);
+            if (out_shared != nullptr && n_routed < slots) {
+                const float sv1 = wts_sh[n_routed] * dcr_part[n_routed * GW + c];
+                if constexpr (OUT_DTYPE == F32) static_cast<float*>(out_shared)[at] = sv1;
+                else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(out_shared)[at] = f2bf(sv1);
+                else static_cast<uint16_t*>(out_shared)[at] = f2h(sv1);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // The grouped kernel. MODE 0: esp_grouped, its member rows read from global memory at each step. MODE 2: esp_grouped
 // with the member rows staged through shared memory (grouped_body_staged), an instance of its own so that its copy
@@ -1673,11 +1751,26 @@ static int down_combine_any(const float* Z, const int32_t* pick, const void* svh
     ESP_REQUIRE(n_routed >= 0 && n_routed <= slots, "n_routed <= slots");
     ESP_REQUIRE(rows * slots <= P, "rows * slots must not exceed P");
     if (rows <= 0) return esp_host::ok();
+    hipStream_t s = (hipStream_t)stream;
+    auto svh = static_cast<const uint16_t*>(svh_d);
+    if (rows >= DCR_ROWS) {                                 // a workgroup a (row, 4 128-blocks)
+        ESP_REQUIRE(rows < (int64_t(1) << 31), "down_combine: at most 2^31 - 1 rows");
+        const size_t smem = (size_t)slots * DCR_BLOCKS * 128 * 4;
+        const dim3 g((unsigned)rows, (unsigned)((D / 128 + DCR_BLOCKS - 1) / DCR_BLOCKS));
+        if (out_dtype == ESP_BF16)
+            down_combine_rows_kernel<BF16><<<g, 256, smem, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D,
+                                                                (int)SK, (int)E, (int)slots, (int)n_routed);
+        else if (out_dtype == ESP_F16)
+            down_combine_rows_kernel<F16><<<g, 256, smem, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D,
+                                                               (int)SK, (int)E, (int)slots, (int)n_routed);
+        else
+            down_combine_rows_kernel<F32><<<g, 256, smem, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D,
+                                                               (int)SK, (int)E, (int)slots, (int)n_routed);
+        return esp_host::launch_check("down_combine");
+    }
     dim3 grid((unsigned)rows, (unsigned)(D / 128));
     // a 32-lane half a slot, so every slot's partials are loaded in one round (9 slots: 320 threads, not 256)
     const unsigned nt = slots * 32 <= 256 ? 256u : (unsigned)((slots * 32 + 63) / 64 * 64);
-    hipStream_t s = (hipStream_t)stream;
-    auto svh = static_cast<const uint16_t*>(svh_d);
     if (out_dtype == ESP_BF16)
         down_combine_kernel<BF16><<<grid, nt, 0, s>>>(Z, pick, svh, y, wts, out, out_shared, (int)P, (int)D, (int)SK,
                                                       (int)E, (int)slots, (int)n_routed);
