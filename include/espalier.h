@@ -34,6 +34,7 @@ extern "C" {
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
 #define ESP_STATUS_WAIT_TIMEOUT 4 /* a dense_multi group gave up waiting for its producer group (~20 ms) */
+#define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table) */
 
 /* Message of the last failed call on this host thread ("" if none). */
 const char* esp_last_error(void);
@@ -145,6 +146,22 @@ int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_
                 const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int64_t mats,
                 int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t nt, int64_t warps, int64_t pf,
                 int64_t lo, int64_t hi, void* stream);
+
+/* esp_grouped over a work list, for groupings of a whole prompt. No counterpart in the reference, which groups a
+ * 32-token window at a time: there an expert has at most 32 * slots members, here up to the prompt's length, and a
+ * grid of every expert slot times every possible member tile is mostly empty workgroups (at 512 tokens 4112 of which
+ * ~400 have members). esp_tile_list writes the non-empty (expert slot u, member tile t) pairs of a grouping (uids,
+ * ucount, members as esp_group writes them) into tiles: tiles[0] = their number, tiles[1 + i] = u << 16 | t in (u, t)
+ * order; tiles needs 1 + min(nexp_max * ceil(maxm / 32), ceil(P / 32) + nexp_max) ints, and nexp_max *
+ * ceil(maxm / 32) <= 32768. esp_grouped_list then runs esp_grouped's programs for the listed pairs only, with the same
+ * arguments (less the tile hints) and the same bits. One list serves every launch over the same grouping. */
+int esp_tile_list(const int32_t* ucount, const int32_t* members, int64_t nexp_max, int64_t maxm, int64_t P,
+                  int32_t* tiles, int64_t tiles_numel, void* stream);
+int esp_grouped_list(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
+                     const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
+                     const int32_t* ucount, const int32_t* members, int64_t maxm, const int32_t* tiles, float* Z,
+                     int64_t z_numel, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
+                     int64_t warps, int64_t lo, int64_t hi, void* stream);
 
 /* Replaces `gateup_epilogue` (experts.cpp:106-118, experts.cu:120-162, 477-487): per valid pick p, the gate / up
  * splits of Z [2][SK][P][N] summed in order, H, * svh, SwiGLU (act_mode 1: fp32; 0: bf16 roundings; clamped to

@@ -184,3 +184,58 @@ def test_prefill_close_to_windows(dev, layer16):
     wo, ws = G.windows(x, pick, wts, L, G.scratch(L, 32, 9, dev))
     assert O.rel_l2(out.float().cpu().numpy(), wo.float().cpu().numpy()) < 1e-2
     assert O.rel_l2(osh.float().cpu().numpy(), ws.float().cpu().numpy()) < 1e-2
+
+
+@pytest.mark.parametrize("T,sk", [(40, 1), (100, 1), (100, 8), (517, 1)])
+def test_tile_list_and_grouped_list(dev, ext, layer16, T, sk):
+    """esp_tile_list: the non-empty (expert slot, member tile) pairs of a whole prompt's grouping, in order, against a
+    count of each expert's members; esp_grouped_list over them: the partials of esp_grouped bit for bit (gate/up and
+    down, staged and unstaged programs, one K split and eight)."""
+    print(f"tile list T={T} sk={sk}", flush=True)
+    L = layer16[0]
+    E = 16
+    gen = torch.Generator().manual_seed(700 + T)
+    pick = torch.stack([torch.randperm(E, generator=gen)[:8] for _ in range(T)]).to(torch.int32).to(dev)
+    slots, P = 8, T * 8
+    maxu = min(P, E)
+    uids = torch.zeros(maxu, dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    members = torch.full((maxu, T), -1, dtype=torch.int32, device=dev)
+    ext.group(pick.reshape(-1), uids, count, members, T, slots, E)
+    cap = G.tile_list_cap(maxu, T, P)
+    tiles = torch.full((1 + cap,), -5, dtype=torch.int32, device=dev)
+    ext.tile_list(count, members, maxu, P, tiles)
+    torch.cuda.synchronize()
+    cnt = int(count.item())
+    m = members.cpu().numpy()
+    want = [(u << 16) | t for u in range(cnt) for t in range(-(-int((m[u] >= 0).sum()) // 32))]
+    got = tiles.cpu().numpy()
+    assert got[0] == len(want) and list(got[1:1 + len(want)]) == want
+    for mats, K, N, X, ptr, k2, cb, kk in ((2, D, I, None, L.ptr[:2], L.k2[:2], L.cb[:2], L.k2_gu),
+                                           (1, I, D, None, L.ptr[2:] * 2, L.k2[2:] * 2, L.cb[2:] * 2, L.k2_d)):
+        xs = torch.randn((P, K), generator=gen).half().to(dev)
+        s_ = sk if mats == 2 else 1
+        z0 = torch.zeros((mats * s_ * P * N,), dtype=torch.float32, device=dev)
+        z1 = torch.zeros_like(z0)
+        ext.grouped(xs, xs, ptr[0], ptr[1], k2[0], k2[1], cb[0], cb[1], uids, count, members, z0, mats, K, N, P, s_,
+                    slots, 8, G.PREFILL_WAVES, 2, *kk)
+        ext.grouped_list(xs, xs, ptr[0], ptr[1], k2[0], k2[1], cb[0], cb[1], uids, count, members, tiles, z1, mats,
+                         K, N, P, s_, slots, G.PREFILL_WAVES, *kk)
+        torch.cuda.synchronize()
+        assert torch.equal(z0.view(torch.int32), z1.view(torch.int32)), (mats, s_)
+    assert int(ext.status(True)) == 0
+
+
+def test_tile_list_over_its_bound_raises_status(dev, ext):
+    """A member table with more non-empty tiles than a grouping of P picks can have (P given as 1): the list keeps its
+    bound's entries and the status word reports ESP_STATUS_TILE_LIST (8)."""
+    ext.status(True)
+    maxu, maxm = 16, 100
+    members = torch.arange(maxu * maxm, dtype=torch.int32, device=dev).reshape(maxu, maxm)
+    count = torch.tensor([maxu], dtype=torch.int32, device=dev)
+    cap = G.tile_list_cap(maxu, maxm, 1)
+    tiles = torch.zeros((1 + cap,), dtype=torch.int32, device=dev)
+    ext.tile_list(count, members, maxu, 1, tiles)
+    torch.cuda.synchronize()
+    assert int(tiles[0].item()) == cap == 17
+    assert int(ext.status(True)) & 8

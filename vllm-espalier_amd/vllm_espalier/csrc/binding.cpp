@@ -61,6 +61,46 @@ void grouped(const at::Tensor& X0, const at::Tensor& X1, const at::Tensor& TP0, 
                      K, N, P, SK, slots, nt, warps, pf, lo, hi, cur_stream()));
 }
 
+// esp_tile_list: the non-empty (expert slot, member tile) pairs of a grouping, for grouped_list
+void tile_list(const at::Tensor& ucount, const at::Tensor& members, int64_t nexp_max, int64_t P, at::Tensor tiles) {
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    check(tiles, at::kInt, "tiles");
+    TORCH_CHECK(members.dim() == 2 && members.size(0) >= nexp_max, "members: [nexp_max, maxm]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(members.device());
+    call(esp_tile_list(cptr<int32_t>(ucount), cptr<int32_t>(members), nexp_max, members.size(1), P,
+                       mptr<int32_t>(tiles), tiles.numel(), cur_stream()));
+}
+
+// esp_grouped_list: grouped's programs over tile_list's entries only (the same bits)
+void grouped_list(const at::Tensor& X0, const at::Tensor& X1, const at::Tensor& TP0, const at::Tensor& TP1,
+                  const at::Tensor& B0, const at::Tensor& B1, const at::Tensor& C0, const at::Tensor& C1,
+                  const at::Tensor& uids, const at::Tensor& ucount, const at::Tensor& members,
+                  const at::Tensor& tiles, at::Tensor Z, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK,
+                  int64_t slots, int64_t warps, int64_t lo, int64_t hi) {
+    check(X0, at::kHalf, "X0");
+    check(X1, at::kHalf, "X1");
+    check(TP0, at::kLong, "TP0");
+    check(TP1, at::kLong, "TP1");
+    check(B0, at::kInt, "B0");
+    check(B1, at::kInt, "B1");
+    check(C0, at::kInt, "C0");
+    check(C1, at::kInt, "C1");
+    check(uids, at::kInt, "uids");
+    check(ucount, at::kInt, "ucount");
+    check(members, at::kInt, "members");
+    check(tiles, at::kInt, "tiles");
+    check(Z, at::kFloat, "Z");
+    TORCH_CHECK(Z.numel() >= mats * SK * P * N, "Z too small");
+    TORCH_CHECK(X0.numel() >= P * K && X1.numel() >= P * K, "X too small");
+    TORCH_CHECK(members.dim() == 2 && members.size(0) >= uids.numel(), "members: [nexp_max, maxm]");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(X0.device());
+    call(esp_grouped_list(X0.data_ptr(), X1.data_ptr(), cptr<int64_t>(TP0), cptr<int64_t>(TP1), cptr<int32_t>(B0),
+                          cptr<int32_t>(B1), cptr<int32_t>(C0), cptr<int32_t>(C1), cptr<int32_t>(uids), uids.numel(),
+                          cptr<int32_t>(ucount), cptr<int32_t>(members), members.size(1), cptr<int32_t>(tiles),
+                          mptr<float>(Z), Z.numel(), mats, K, N, P, SK, slots, warps, lo, hi, cur_stream()));
+}
+
 void dequant(const at::Tensor& T, at::Tensor out, int64_t k2, int64_t cb) {
     TORCH_CHECK(T.is_cuda() && T.scalar_type() == at::kShort && T.is_contiguous() && T.dim() == 3,
                 "T: int16 [K/16, N/16, 8 * k2]");
@@ -599,6 +639,8 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("group_shared", &group_shared);
     m.def("down_combine2", &down_combine2);
     m.def("grouped", &grouped);
+    m.def("tile_list", &tile_list);
+    m.def("grouped_list", &grouped_list);
     m.def("dequant", &dequant);
     m.def("group", &group);
     m.def("rot_in", &rot_in);

@@ -645,6 +645,8 @@ struct GroupedArgs {
     int stage_bytes, xs_stride;    // rotated rows in shared memory after the stages
     int lo, hi;                    // the K2 range the launch's stages are sized for
     int mt;                        // member tiles of 32 an expert (MODE 0: ceil(maxm / 32); MODE 1: 1)
+    const int* tiles;              // esp_grouped_list: the non-empty (expert slot, member tile) pairs (tile_list_kernel);
+                                   // null: grid x is the expert slot and grid z holds the member tile
     int staged;                    // MODE 0: the member rows staged through shared memory (grouped_body_staged)
 };
 
@@ -1130,6 +1132,67 @@ __global__ __launch_bounds__(256) void down_combine_rows_kernel(const float* __r
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// esp_tile_list: the non-empty (expert slot u, member tile t) pairs of a grouping, in (u, t) order, for
+// esp_grouped_list: tiles[0] = their number, tiles[1 + i] = u << 16 | t. A tile is non-empty iff its first member is
+// (members come first in a row, -1 padded). One workgroup: each thread tests its run of consecutive pairs with every
+// load in flight, then a block-wide prefix of the counts places the entries. At most cap entries are written; a
+// grouping with more raises ESP_STATUS_TILE_LIST (its grouped launches would miss tiles).
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int TL_THREADS = 1024, TL_PER = 32;           // pairs a thread at most (maxu * mt <= 32768)
+
+__global__ __launch_bounds__(TL_THREADS) void tile_list_kernel(const int* __restrict__ ucount,
+                                                              const int* __restrict__ members, int maxu, int maxm,
+                                                              int mt, int* __restrict__ tiles, int cap) {
+    __shared__ int wave_tot[TL_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int cnt = ucount[0];
+    cnt = cnt < maxu ? cnt : maxu;
+    const int pairs = cnt * mt, per = (maxu * mt + TL_THREADS - 1) / TL_THREADS, q0 = tid * per;
+    unsigned flags = 0u;
+    for (int i0 = 0; i0 < per; i0 += 8) {                  // eight pairs' first members in flight at a time
+        int v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = q0 + i0 + i;
+            v[i] = -1;
+            if (i0 + i < per && q < pairs) {
+                const int u = q / mt, t = q - u * mt;
+                v[i] = members[(size_t)u * maxm + t * 32];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (v[i] >= 0) flags |= 1u << (i0 + i);
+    }
+    const int n = __builtin_popcount(flags);
+    int incl = n;                                          // inclusive prefix of n over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int before = incl - n, total = 0;
+#pragma unroll
+    for (int w = 0; w < TL_THREADS / 64; ++w) {
+        const int c = wave_tot[w];
+        before += w < wave ? c : 0;
+        total += c;
+    }
+    for (int i = 0; i < per; ++i)
+        if ((flags >> i) & 1u) {
+            const int q = q0 + i, u = q / mt;
+            if (before < cap) tiles[1 + before] = (u << 16) | (q - u * mt);
+            ++before;
+        }
+    if (tid == 0) {
+        tiles[0] = total < cap ? total : cap;
+        if (total > cap) raise_status(ESP_STATUS_TILE_LIST);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // The grouped kernel. MODE 0: esp_grouped, its member rows read from global memory at each step. MODE 2: esp_grouped
 // with the member rows staged through shared memory (grouped_body_staged), an instance of its own so that its copy
 // plan's registers do not lower the occupancy of MODE 0. MODE 1 (esp_moe_gateup): the member rows' K range rotated
@@ -1140,16 +1203,27 @@ template <int MODE>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void grouped_kernel_t(GroupedArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
-    const int u = blockIdx.x;
-    // program: member tile (32 members of the expert's list), K split, matrix
-    const int mtile = blockIdx.z % a.mt, zz = blockIdx.z / a.mt;
+    // program: expert slot u, member tile (32 members of the expert's list), K split, matrix; with a work list, the
+    // slot and tile are the list's entry blockIdx.x (workgroups past the list's length exit: workgroup-uniform)
+    int u, mtile, zz;
+    if (MODE != 1 && a.tiles != nullptr) {
+        if ((int)blockIdx.x >= a.tiles[0]) return;
+        const int ent = a.tiles[1 + blockIdx.x];
+        u = ent >> 16;
+        mtile = ent & 0xFFFF;
+        zz = blockIdx.z;
+    } else {
+        u = blockIdx.x;
+        mtile = blockIdx.z % a.mt;
+        zz = blockIdx.z / a.mt;
+    }
     const int split = zz % a.SK, mat = zz / a.SK;
     const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
     const int NW = (int)(blockDim.x >> 6);
     __shared__ int rows_sh[32];
     __shared__ int nrows;
     // the count, the expert id and the member rows depend on u alone: all three loads in flight at once
-    // (u < gridDim.x <= the tables' length, so the loads stay in bounds past the count)
+    // (u < gridDim.x <= the tables' length, or u < the count for a list entry, so the loads stay in bounds)
     const int cnt = a.ucount[0];
     const int e = a.uids[u];
     if (threadIdx.x < 64) {
@@ -1559,13 +1633,19 @@ extern "C" int esp_rot_in(const void* x, int x_dtype, int64_t x_stride, const in
     return esp_host::launch_check("rot_in");
 }
 
-extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
-                           const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids,
-                           int64_t nexp_max, const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z,
-                           int64_t z_numel, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
-                           int64_t nt, int64_t warps, int64_t pf, int64_t lo, int64_t hi, void* stream) {
-    (void)nt;
-    (void)pf;
+// the largest number of non-empty member tiles a grouping of P picks over nexp_max expert slots can have: the sum
+// over experts of ceil(members / 32) is at most P / 32 + the experts used
+static int64_t tile_list_cap(int64_t nexp_max, int64_t maxm, int64_t P) {
+    const int64_t mt = (maxm + 31) / 32, bound = (P + 31) / 32 + nexp_max;
+    return nexp_max * mt < bound ? nexp_max * mt : bound;
+}
+
+// esp_grouped, or esp_grouped_list when tiles is given (then grid x runs over the list's entries)
+static int grouped_impl(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
+                        const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
+                        const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel,
+                        int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps,
+                        int64_t lo, int64_t hi, const int32_t* tiles, void* stream) {
     ESP_REQUIRE(X0 && X1 && TP0 && TP1 && B0 && B1 && C0 && C1 && uids && ucount && members && Z,
                 "grouped: null pointer");
     ESP_REQUIRE(mats == 1 || mats == 2, "mats must be 1 or 2");
@@ -1602,7 +1682,9 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     a.slots = (int)slots;
     a.lo = (int)lo;
     a.hi = (int)hi;
+    a.tiles = tiles;
     dim3 grid((unsigned)nexp_max, (unsigned)(N / 128), (unsigned)(mats * SK * mt));
+    if (tiles != nullptr) grid = dim3((unsigned)tile_list_cap(nexp_max, maxm, P), (unsigned)(N / 128), (unsigned)(mats * SK));
     // K ranges of AST_MIN_STEPS steps or more stage the member rows with the tiles (grouped_body_staged), whose
     // member-row offsets are 32-bit and whose waves hold at most 8 member rows each
     a.staged = (K / SK) / 32 >= AST_MIN_STEPS;
@@ -1622,6 +1704,42 @@ extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, c
     else
         grouped_kernel_t<0><<<grid, (unsigned)(64 * warps), smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("grouped");
+}
+
+extern "C" int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1, const int32_t* B0,
+                           const int32_t* B1, const int32_t* C0, const int32_t* C1, const int32_t* uids,
+                           int64_t nexp_max, const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z,
+                           int64_t z_numel, int64_t mats, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
+                           int64_t nt, int64_t warps, int64_t pf, int64_t lo, int64_t hi, void* stream) {
+    (void)nt;
+    (void)pf;
+    return grouped_impl(X0, X1, TP0, TP1, B0, B1, C0, C1, uids, nexp_max, ucount, members, maxm, Z, z_numel, mats, K,
+                        N, P, SK, slots, warps, lo, hi, nullptr, stream);
+}
+
+extern "C" int esp_tile_list(const int32_t* ucount, const int32_t* members, int64_t nexp_max, int64_t maxm, int64_t P,
+                             int32_t* tiles, int64_t tiles_numel, void* stream) {
+    ESP_REQUIRE(ucount && members && tiles, "tile_list: null pointer");
+    ESP_REQUIRE(nexp_max >= 1 && nexp_max < 65536 && maxm >= 1 && maxm <= 65536 && P >= 1,
+                "tile_list: 1 to 65535 expert slots, 1 to 65536 members a row, P >= 1");
+    const int64_t mt = (maxm + 31) / 32, cap = tile_list_cap(nexp_max, maxm, P);
+    ESP_REQUIRE(nexp_max * mt <= (int64_t)TL_THREADS * TL_PER, "tile_list: at most 32768 (expert, member tile) pairs");
+    ESP_REQUIRE(tiles_numel >= 1 + cap, "tile_list: tiles needs 1 + min(E * ceil(maxm / 32), ceil(P / 32) + E) ints");
+    tile_list_kernel<<<1, TL_THREADS, 0, (hipStream_t)stream>>>(ucount, members, (int)nexp_max, (int)maxm, (int)mt,
+                                                                tiles, (int)cap);
+    return esp_host::launch_check("tile_list");
+}
+
+extern "C" int esp_grouped_list(const void* X0, const void* X1, const int64_t* TP0, const int64_t* TP1,
+                                const int32_t* B0, const int32_t* B1, const int32_t* C0, const int32_t* C1,
+                                const int32_t* uids, int64_t nexp_max, const int32_t* ucount, const int32_t* members,
+                                int64_t maxm, const int32_t* tiles, float* Z, int64_t z_numel, int64_t mats, int64_t K,
+                                int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps, int64_t lo, int64_t hi,
+                                void* stream) {
+    ESP_REQUIRE(tiles, "grouped_list: null tile list");
+    ESP_REQUIRE(nexp_max < 65536, "grouped_list: at most 65535 expert slots");
+    return grouped_impl(X0, X1, TP0, TP1, B0, B1, C0, C1, uids, nexp_max, ucount, members, maxm, Z, z_numel, mats, K,
+                        N, P, SK, slots, warps, lo, hi, tiles, stream);
 }
 
 static int grouped_launch_gateup(const GroupedArgs& a, int64_t nexp_max, int64_t warps, size_t smem, hipStream_t st) {

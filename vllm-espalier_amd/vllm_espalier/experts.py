@@ -382,6 +382,7 @@ class PrefillScratch:
             "z": ((P * max(2 * I * PREFILL_SK_GU, D),), f32, 0),     # the gate/up splits' partials, or down's sums
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0), "members": ((maxu * rows,), i32, -1),
+            "tiles": ((1 + tile_list_cap(maxu, rows, P),), i32, 0),
             "logits": ((rows * E,), f32, 0),
         }
         for name, (shape, dtype, fill) in layout.items():
@@ -393,6 +394,12 @@ class PrefillScratch:
 
 
 _PREFILL: dict = {}
+TILE_LIST_PAIRS = 32768      # esp_tile_list's limit on (expert slot, member tile) pairs
+
+
+def tile_list_cap(maxu: int, maxm: int, P: int) -> int:
+    """Entries esp_tile_list may write for a grouping of P picks over maxu expert slots, maxm members a row."""
+    return min(maxu * -(-maxm // 32), -(-P // 32) + maxu)
 
 
 def prefill_scratch(layer: Layer, rows: int, slots: int, device) -> PrefillScratch:
@@ -431,12 +438,22 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
                        L.E)
     e.rot_in(x, x.stride(0), pick_p, L.suh_g, L.suh_u, s.xg, s.xu, T, L.D, slots, L.E)
     sk = PREFILL_SK_GU
-    e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
-              L.D, L.I, P, sk, slots, 8, PREFILL_WAVES, 2, *L.k2_gu)
-    e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
     t, b, c = L.ptr[2], L.k2[2], L.cb[2]
-    e.grouped(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.z, 1, L.I, L.D, P, 1, slots, 8, PREFILL_WAVES,
-              2, *L.k2_d)
+    # the grouped launches over the grouping's non-empty (expert, member tile) pairs only: a grid of every expert slot
+    # times every member tile is mostly empty workgroups (the same programs either way, the same bits)
+    if ids.numel() * -(-T // 32) <= TILE_LIST_PAIRS:
+        e.tile_list(s.count, members, ids.numel(), P, s.tiles)
+        e.grouped_list(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members,
+                       s.tiles, s.z, 2, L.D, L.I, P, sk, slots, PREFILL_WAVES, *L.k2_gu)
+        e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
+        e.grouped_list(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.tiles, s.z, 1, L.I, L.D, P, 1, slots,
+                       PREFILL_WAVES, *L.k2_d)
+    else:
+        e.grouped(s.xg, s.xu, L.ptr[0], L.ptr[1], L.k2[0], L.k2[1], L.cb[0], L.cb[1], ids, s.count, members, s.z, 2,
+                  L.D, L.I, P, sk, slots, 8, PREFILL_WAVES, 2, *L.k2_gu)
+        e.gateup_epilogue(s.z, pick_p, L.svh_g, L.svh_u, L.suh_d, s.xd, T, P, L.I, sk, slots, L.E, math.inf, ACT_F32)
+        e.grouped(s.xd, s.xd, t, t, b, b, c, c, ids, s.count, members, s.z, 1, L.I, L.D, P, 1, slots, 8,
+                  PREFILL_WAVES, 2, *L.k2_d)
     out = torch.empty((T, L.D), dtype=x.dtype, device=x.device) if out is None else out
     if has_shared and out_shared is None:
         out_shared = torch.empty((T, L.D), dtype=x.dtype, device=x.device)
