@@ -648,6 +648,86 @@ def phase_trace(dev) -> dict:
     return res
 
 
+TILE_PHASE_NAMES = ("first stage landed", "K loop (wave 0)", "of which stage waits", "sums in shared memory",
+                    "stored and arrived", "finisher")
+
+
+def tile_phase_trace(dev) -> dict:
+    """Where a prompt launch (esp_dense_tile) spends its time, from the same timing build (dense_tile.hip: thread 0 of
+    every workgroup records the real-time counter at each phase, and sums its waits for the later stages). Config 2's
+    four matrices at 512 rows and the LM head at one row, each in a graph of 8 back-to-back prompt launches (the
+    rotation launch included in the time a launch), then one more replay whose last launch's records are read back.
+    Each phase is the median (and 90th percentile) over workgroups of the ns since the previous phase; the
+    finisher's over the finishers (the last split of each column block and row tile to arrive)."""
+    import ctypes
+    import numpy as np
+    import torch
+    import vllm_espalier
+    from vllm_espalier import dense as D, workloads as WL
+    pkg = Path(vllm_espalier.__file__).resolve().parent
+    if pkg.parent != PHASE_ROOT.resolve():
+        raise RuntimeError(f"--phase-trace needs the timing build (csrc/build.py --phase-trace); imported {pkg}")
+    lib = ctypes.CDLL(str(pkg / "libespalier_hip.so"))
+    lib.esp_tile_phase_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    words = 8192 * 8
+    buf = np.zeros(words, dtype=np.uint64)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    block = dense_block(gen, dev)
+    head = D.Dense([WL.matrix(2048, 151936, 6, "mcg", gen, dev)])
+    cases = [(d, nm, 512) for d, nm in zip(block, ("qkv", "o", "shared gate/up", "shared down"))] + [(head, "head", 1)]
+    res = {}
+    for d, nm, T in cases:
+        x = torch.randn((T, d.K), generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty((T, d.n_out), dtype=torch.bfloat16, device=dev)
+        d.reserve_prompt(T)
+        reps = 8
+        g = graph_of(lambda: [d.forward_tile(x, out=y) for _ in range(reps)])
+        us = time_graph(g, 10) * 1000 / reps
+        if lib.esp_tile_phase_clear() != 0:
+            raise RuntimeError("esp_tile_phase_clear failed")
+        g.replay()
+        torch.cuda.synchronize()
+        if lib.esp_tile_phase_read(buf.ctypes.data, words) != 0:
+            raise RuntimeError("esp_tile_phase_read failed")
+        del g
+        t = buf.reshape(-1, 8).astype(np.int64)
+        wg = np.nonzero(t[:, 0] > 0)[0]
+        R = t[wg]
+        rel = (R[:, [0, 1, 3, 4, 5, 6]] - R[:, 0].min()) * 10
+        waits = R[:, 2] * 10
+        fin = (R[:, 7] >> 8) & 1 == 1
+
+        def stat(v):
+            return {"p50": float(np.median(v)), "p90": float(np.percentile(v, 90))}
+        ph = {"first stage landed": stat(rel[:, 1] - rel[:, 0]), "K loop (wave 0)": stat(rel[:, 2] - rel[:, 1]),
+              "of which stage waits": stat(waits), "sums in shared memory": stat(rel[:, 3] - rel[:, 2]),
+              "stored and arrived": stat(rel[:, 4] - rel[:, 3])}
+        if fin.any():
+            ph["finisher"] = stat(rel[fin, 5] - rel[fin, 4])
+            span = float(rel[fin, 5].max())
+        else:
+            span = float(rel[:, 4].max())
+        res[f"{nm}, T={T}"] = {"us_per_launch": round(us, 2), "workgroups": int(len(wg)),
+                               "stages": int(np.median((R[:, 7] >> 16) & 0xFFFF)), "span_us": round(span / 1000, 2),
+                               "phases_ns": ph}
+        log(f"tile phase trace {nm} T={T}: {us:.2f} us a launch, span {span / 1000:.2f} us")
+    return res
+
+
+def tile_phase_table(res: dict) -> str:
+    """The markdown table of tile_phase_trace's result (medians, ns)."""
+    head = ["prompt launch", "us a launch (graph, with its rotation)", "workgroups", "stages", *TILE_PHASE_NAMES,
+            "last done (us)"]
+    lines = ["| " + " | ".join(head) + " |", "|" + "---|" * len(head)]
+    for k, r in res.items():
+        ph = r["phases_ns"]
+        cells = [k, f"{r['us_per_launch']:.2f}", f"{r['workgroups']}", f"{r['stages']}",
+                 *(f"{ph[n]['p50']:.0f} ({ph[n]['p90']:.0f})" if n in ph else "-" for n in TILE_PHASE_NAMES),
+                 f"{r['span_us']:.2f}"]
+        lines.append("| " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
 def phase_table(res: dict) -> str:
     """The markdown table of phase_trace's result (medians, ns)."""
     head = ["launch", "us a launch (graph)", "workgroups", *PHASE_NAMES[1:], "last finisher done (us)"]
@@ -679,8 +759,8 @@ def main() -> int:
                     "passes over the expert kernels and the LM head, and exit")
     ap.add_argument("--probes", action="store_true", help="measure the ceilings the kernels are held to (graph "
                     "launch floor, streaming read bandwidth, VALU issue rates) and exit")
-    ap.add_argument("--phase-trace", action="store_true", help="time the phases of config 2's batch-1 launches with "
-                    "the timing build (csrc/build.py --phase-trace) and exit")
+    ap.add_argument("--phase-trace", action="store_true", help="time the phases of config 2's batch-1 launches and "
+                    "of its prompt launches at 512 rows with the timing build (csrc/build.py --phase-trace) and exit")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
@@ -717,8 +797,10 @@ def main() -> int:
         return 0
     if a.phase_trace:
         res = phase_trace(dev)
+        tres = tile_phase_trace(dev)
         print(phase_table(res), flush=True)
-        print(json.dumps({"phase_trace": res, "device": name}), flush=True)
+        print(tile_phase_table(tres), flush=True)
+        print(json.dumps({"phase_trace": res, "tile_phase_trace": tres, "device": name}), flush=True)
         return 0
 
     # ---- config 2 dense block, cold stack

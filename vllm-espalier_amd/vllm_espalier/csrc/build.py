@@ -8,8 +8,8 @@
 All land in the vllm_espalier package directory. Usage: python build.py [--jobs N] [--only lib|ext|probe]
 
 --phase-trace builds, instead, a timing copy of the package under csrc/_phase/vllm_espalier (its Python files and both
-libraries, compiled with ESP_PHASE_TRACE): esp_dense's workgroups record when each phase of the launch starts
-(dense.hpp), which bench.py --phase-trace reads. The product package is left as it is.
+libraries, compiled with ESP_PHASE_TRACE): esp_dense's and esp_dense_tile's workgroups record when each phase of the
+launch starts (dense.hpp, dense_tile.hip), which bench.py --phase-trace reads. The product package is left as it is.
 """
 from __future__ import annotations
 

@@ -13,6 +13,8 @@
 //
 // Row invariance: a row's sums depend only on its own A rows, the K split (a function of the caller's plan) and the
 // fixed step order, never on the other rows of the prompt or its place in a tile.
+#include <type_traits>
+
 #include "dense.hpp"
 
 namespace esp {
@@ -25,6 +27,42 @@ constexpr int TILE_STEPS = 4;                   // 32-k steps a stage
 constexpr int TILE_FRAG = 512;                  // halves a (row group, step) block: 64 lanes x 8
 constexpr int RED_STRIDE = 132;                 // floats between two rows of the block's sums (banks apart)
 constexpr int RED_BYTES = TILE_ROWS * RED_STRIDE * 4;
+
+#ifdef ESP_PHASE_TRACE
+// Timing build only (build.py --phase-trace): thread 0 of each workgroup records the 100 MHz real-time counter into
+// g_tile_phase[workgroup][8]: 0 start, 1 the first stage landed, 2 the ticks spent in the later stage waits (a sum),
+// 3 its own wave's K loop done, 4 the block's sums in shared memory, 5 partials stored and arrived (or y stored at one
+// split), 6 the finisher done; slot 7 holds the XCD (bits 0-3), 1 << 8 for a finisher and the stage count << 16.
+constexpr int TILE_PHASE_WGS = 8192;
+static __device__ unsigned long long g_tile_phase[TILE_PHASE_WGS * 8];
+__device__ __forceinline__ int tile_phase_wg() {
+    return (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+}
+__device__ __forceinline__ void tile_phase_set(int slot, unsigned long long v) {
+    if (threadIdx.x == 0 && tile_phase_wg() < TILE_PHASE_WGS) g_tile_phase[tile_phase_wg() * 8 + slot] = v;
+}
+__device__ __forceinline__ void tile_phase_info(int finisher, int nst) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    tile_phase_set(7, (unsigned long long)(xcc & 0xFu) | ((unsigned long long)finisher << 8) |
+                          ((unsigned long long)nst << 16));
+}
+#define TILE_PHASE(slot) tile_phase_set(slot, __builtin_amdgcn_s_memrealtime())
+#define TILE_PHASE_SET(slot, v) tile_phase_set(slot, v)
+#define TILE_PHASE_INFO(finisher, nst) tile_phase_info(finisher, nst)
+#define TILE_PHASE_DRAIN()              \
+    do {                                \
+        __builtin_amdgcn_s_waitcnt(0);  \
+        __syncthreads();                \
+    } while (0)
+#define TILE_NOW() __builtin_amdgcn_s_memrealtime()
+#else
+#define TILE_PHASE(slot) ((void)0)
+#define TILE_PHASE_SET(slot, v) ((void)0)
+#define TILE_PHASE_INFO(finisher, nst) ((void)0)
+#define TILE_PHASE_DRAIN() ((void)0)
+#define TILE_NOW() 0ull
+#endif
 
 struct TileArgs {
     Shard s[MAX_SHARDS];
@@ -67,6 +105,49 @@ __global__ __launch_bounds__(256) void tile_rot_kernel(const void* __restrict__ 
 
 typedef __attribute__((address_space(3))) const f16x8* lds_f16x8_ptr;
 
+// The finisher's rows of one half-wave (rows rbase, rbase + 16, ...): RPB rows at a time with the other splits'
+// partials of those rows in flight together (RPB * OM loads, OM >= SK - 1), its own split's sums read from shared
+// memory (own: the block's [128][RED_STRIDE] sums), each row's splits added in split order, then the output transform
+// and y. zp0 is the half-wave's column slice of split 0's row 0 in Z. The loads take no branch (a load under a
+// lane-dependent branch is waited on before the next one): a row past Mt still lies in Z's 128 rows of the tile and is
+// read but not used, and a slot past SK - 1 reads split 0 again.
+template <int RPB, int OM>
+__device__ __forceinline__ void tile_finish_rows(const DevBuf& zb, const float* zp0, size_t zrow, size_t zsplit,
+                                                 const float* own, int wave, int rbase, int Mt, int SK, int split,
+                                                 int l32, uint2 sv, float scale, void* y, int y_dtype, size_t ybase,
+                                                 int y_stride) {
+    constexpr int RSTEP = 2 * TILE_WAVES, ITERS = TILE_ROWS / RSTEP;
+    for (int i0 = 0; i0 < ITERS && 2 * wave + i0 * RSTEP < Mt; i0 += RPB) {
+        float4 u[RPB][OM];
+#pragma unroll
+        for (int i = 0; i < RPB; ++i) {
+            const int r = rbase + (i0 + i) * RSTEP;
+#pragma unroll
+            for (int o = 0; o < OM; ++o) {
+                const int q = o >= SK - 1 ? 0 : o < split ? o : o + 1;    // the o-th split other than its own
+                u[i][o] = zb.load4(zp0 + r * zrow + q * zsplit);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPB; ++i) {
+            const int r = rbase + (i0 + i) * RSTEP;
+            if (r < Mt) {
+                const float4 mine = *reinterpret_cast<const float4*>(own + r * RED_STRIDE + 4 * l32);
+                float4 s = split == 0 ? mine : u[i][0];
+#pragma unroll
+                for (int q = 1; q <= OM; ++q)
+                    if (q < SK) {
+                        const float4 t = q == split ? mine : q < split ? u[i][q < OM ? q : OM - 1] : u[i][q - 1];
+                        s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+                    }
+                float v[4] = {s.x, s.y, s.z, s.w};
+                finish(v, l32, sv, scale);
+                store4(y, y_dtype, ybase + (size_t)r * y_stride, v);
+            }
+        }
+    }
+}
+
 template <int CB, int K2>
 __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -78,6 +159,7 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
     constexpr int B_BUF = TILE_STEPS * 2 * ROW_WORDS;              // words a B stage
     constexpr int A_BUF = TILE_RG * TILE_STEPS * TILE_FRAG;        // halves an A stage
     const int nbg = blockIdx.x, split = blockIdx.y, mt = blockIdx.z;
+    TILE_PHASE(0);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, half = lane >> 5, pair = wave & 3, kw = wave >> 2, G = lane >> 4;
 
@@ -134,35 +216,62 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
     const int nst = (steps + TILE_STEPS - 1) / TILE_STEPS;
     const uint2 sv = *reinterpret_cast<const uint2*>(svh + cb_local * 128 + 4 * l32);
 
-    issue(0, 0);
-    for (int st = 0; st < nst; ++st) {
-        wait_stage();                           // stage st landed; every wave is done with buffer (st + 1) & 1
-        if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
-        const int first = st * TILE_STEPS, n = steps - first < TILE_STEPS ? steps - first : TILE_STEPS;
-        const uint32_t* bb = sb + (st & 1) * B_BUF + lane_base;
-        const uint16_t* ab = sa + (st & 1) * A_BUF + lane * 8;
-        for (int ls = kw; ls < n; ls += TILE_KW) {
-            // the trellis words, then every row group's A fragment, all in flight while the words are decoded (LDS
-            // reads return in order). A row group past the tile's rows reads whatever its slot holds: row i of an
-            // MFMA result depends on row i of A alone, and those rows' sums are never stored.
-            uint32_t w[2][6];
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 6; ++i) w[j][i] = bb[ls * 2 * ROW_WORDS + j * TW + lw.off[i]];
-            f16x8 av[TILE_RG];
-#pragma unroll
-            for (int g = 0; g < TILE_RG; ++g) av[g] = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
-            f16x8 b[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = decode_b<CB, K2>(w[j], lp);
-#pragma unroll
-            for (int g = 0; g < TILE_RG; ++g)
+    // a tile of fewer than 128 rows (the prompt's last, or a short prompt) reads and multiplies only its row groups;
+    // a full tile keeps the loop free of those tests
+    auto run = [&](auto full) __attribute__((always_inline)) {
+        constexpr bool FULL = decltype(full)::value;
+        issue(0, 0);
+        unsigned long long waited = 0;
+        (void)waited;
+        for (int st = 0; st < nst; ++st) {
+            const unsigned long long t0 = TILE_NOW();
+            (void)t0;
+            wait_stage();                           // stage st landed; every wave is done with buffer (st + 1) & 1
+#ifdef ESP_PHASE_TRACE
+            if (st == 0)
+                TILE_PHASE(1);
+            else
+                waited += TILE_NOW() - t0;
+#endif
+            if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
+            const int first = st * TILE_STEPS, n = steps - first < TILE_STEPS ? steps - first : TILE_STEPS;
+            const uint32_t* bb = sb + (st & 1) * B_BUF + lane_base;
+            const uint16_t* ab = sa + (st & 1) * A_BUF + lane * 8;
+            for (int ls = kw; ls < n; ls += TILE_KW) {
+                // the trellis words, then every row group's A fragment, all in flight while the words are decoded (LDS
+                // reads return in order). Rows of the tile's last row group past T are zeros of xh, and their sums
+                // are never stored.
+                uint32_t w[2][6];
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b[j], acc[j][g], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 6; ++i) w[j][i] = bb[ls * 2 * ROW_WORDS + j * TW + lw.off[i]];
+                f16x8 av[TILE_RG];
+                if (FULL) {
+#pragma unroll
+                    for (int g = 0; g < TILE_RG; ++g) av[g] = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
+                }
+                f16x8 b[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) b[j] = decode_b<CB, K2>(w[j], lp);
+#pragma unroll
+                for (int g = 0; g < TILE_RG; ++g)
+                    if (FULL || g < rgt) {
+                        // a partial tile reads each row group's fragment where it uses it (fewer live registers)
+                        if (!FULL) av[g] = *(lds_f16x8_ptr)(ab + (g * TILE_STEPS + ls) * TILE_FRAG);
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b[j], acc[j][g], 0, 0, 0);
+                    }
+            }
         }
-    }
+        TILE_PHASE_SET(2, waited);
+        TILE_PHASE(3);
+    };
+    if (rgt == TILE_RG)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 
     // the block's [Mt][128] sums: k slot 0's accumulators into shared memory, then slot 1's added to them
     __syncthreads();
@@ -184,6 +293,7 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         }
         __syncthreads();
     }
+    TILE_PHASE(4);
     const int ycol = col0 + cb_local * 128 + 4 * l32;
     const size_t yrow0 = (size_t)m0 * a.y_stride;
     if (a.SK == 1) {
@@ -193,6 +303,9 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
             finish(v, l32, sv, scale);
             store4(a.y, a.y_dtype, yrow0 + (size_t)r * a.y_stride + ycol, v);
         }
+        TILE_PHASE_DRAIN();
+        TILE_PHASE(5);
+        TILE_PHASE_INFO(0, nst);
         return;
     }
     // K splits: partials to Z, the last split of the (row tile, column block) to arrive adds them in split order
@@ -203,8 +316,23 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         zb.store4(Zt + split * zsplit + r * zrow + nbg * 128 + 4 * l32,
                   *reinterpret_cast<const float4*>(red + r * RED_STRIDE + 4 * l32));
     int* const cnt_p = a.counters + ((size_t)mt * a.NBT + nbg) * CNT_STRIDE;
-    if (!arrive_last(cnt_p, a.SK, last)) return;
-    for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES) {
+    const bool finisher = arrive_last(cnt_p, a.SK, last);
+    TILE_PHASE(5);
+    TILE_PHASE_INFO(finisher ? 1 : 0, nst);
+    if (!finisher) return;
+    // the other splits' partials, up to 16 loads in flight a lane (the rows' device-scope round trips overlap instead
+    // of following one another, eight rows a half-wave); its own split's sums are still in shared memory
+    const float* zp0 = Zt + nbg * 128 + 4 * l32;
+    if (a.SK <= 3) {
+        tile_finish_rows<8, 2>(zb, zp0, zrow, zsplit, red, wave, wave * 2 + half, Mt, a.SK, split, l32, sv,
+                               scale, a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+    } else if (a.SK <= 4) {
+        tile_finish_rows<4, 3>(zb, zp0, zrow, zsplit, red, wave, wave * 2 + half, Mt, a.SK, split, l32, sv,
+                               scale, a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+    } else if (a.SK <= 8) {
+        tile_finish_rows<2, 7>(zb, zp0, zrow, zsplit, red, wave, wave * 2 + half, Mt, a.SK, split, l32, sv,
+                               scale, a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+    } else for (int r = wave * 2 + half; r < Mt; r += 2 * TILE_WAVES) {
         const float* zp = Zt + r * zrow + nbg * 128 + 4 * l32;
         float4 s;
         for (int q0 = 0; q0 < a.SK; q0 += 8) {              // up to eight splits' loads in flight at once
@@ -226,6 +354,8 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         store4(a.y, a.y_dtype, yrow0 + (size_t)r * a.y_stride + ycol, v);
     }
     if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every split of the block arrived
+    TILE_PHASE_DRAIN();
+    TILE_PHASE(6);
 }
 
 template <int KCB, int K2>
@@ -241,6 +371,23 @@ static int launch_tile(const TileArgs& a, dim3 grid, size_t smem, hipStream_t st
 }  // namespace esp
 
 using namespace esp;
+
+#ifdef ESP_PHASE_TRACE
+// The timing build's phase records of esp_dense_tile's workgroups: copy n words out, or clear them all
+extern "C" int esp_tile_phase_read(unsigned long long* host, int64_t n) {
+    ESP_REQUIRE(host && n >= 0 && n <= (int64_t)esp::TILE_PHASE_WGS * 8, "tile_phase_read: 0 to %d words",
+                esp::TILE_PHASE_WGS * 8);
+    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(esp::g_tile_phase), (size_t)n * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "tile_phase_read: copy failed");
+    return esp_host::ok();
+}
+extern "C" int esp_tile_phase_clear(void) {
+    static unsigned long long zero[esp::TILE_PHASE_WGS * 8];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(esp::g_tile_phase), zero, sizeof(zero), 0, hipMemcpyHostToDevice) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "tile_phase_clear: copy failed");
+    return esp_host::ok();
+}
+#endif
 
 extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
                               const void* const* trellis, const void* const* suh, const void* const* svh,
