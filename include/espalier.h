@@ -153,7 +153,7 @@ int esp_grouped(const void* X0, const void* X1, const int64_t* TP0, const int64_
  * ~400 have members). esp_tile_list writes the non-empty (expert slot u, member tile t) pairs of a grouping (uids,
  * ucount, members as esp_group writes them) into tiles: tiles[0] = their number, tiles[1 + i] = u << 16 | t in (u, t)
  * order; tiles needs 1 + min(nexp_max * ceil(maxm / 32), ceil(P / 32) + nexp_max) ints, and nexp_max *
- * ceil(maxm / 32) <= 32768. esp_grouped_list then runs esp_grouped's programs for the listed pairs only, with the same
+ * ceil(maxm / 32) <= 32768. Every slot of members [nexp_max][maxm] is read (slots past *ucount are masked). esp_grouped_list then runs esp_grouped's programs for the listed pairs only, with the same
  * arguments (less the tile hints) and the same bits. One list serves every launch over the same grouping. */
 int esp_tile_list(const int32_t* ucount, const int32_t* members, int64_t nexp_max, int64_t maxm, int64_t P,
                   int32_t* tiles, int64_t tiles_numel, void* stream);

@@ -1145,24 +1145,30 @@ __global__ __launch_bounds__(TL_THREADS) void tile_list_kernel(const int* __rest
                                                               int mt, int* __restrict__ tiles, int cap) {
     __shared__ int wave_tot[TL_THREADS / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int cnt = ucount[0];
-    cnt = cnt < maxu ? cnt : maxu;
-    const int pairs = cnt * mt, per = (maxu * mt + TL_THREADS - 1) / TL_THREADS, q0 = tid * per;
+    // the count and the first eight pairs' first members in flight together: every slot of the member table lies
+    // inside it, and slots past the count are masked once it has arrived
+    const int cnt_raw = ucount[0];
+    const int per = (maxu * mt + TL_THREADS - 1) / TL_THREADS, q0 = tid * per;
     unsigned flags = 0u;
+    int pairs = -1;
     for (int i0 = 0; i0 < per; i0 += 8) {                  // eight pairs' first members in flight at a time
         int v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int q = q0 + i0 + i;
             v[i] = -1;
-            if (i0 + i < per && q < pairs) {
+            if (i0 + i < per && q < maxu * mt) {
                 const int u = q / mt, t = q - u * mt;
                 v[i] = members[(size_t)u * maxm + t * 32];
             }
         }
+        if (pairs < 0) {
+            const int cnt = cnt_raw < maxu ? cnt_raw : maxu;
+            pairs = cnt * mt;
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (v[i] >= 0) flags |= 1u << (i0 + i);
+            if (v[i] >= 0 && q0 + i0 + i < pairs) flags |= 1u << (i0 + i);
     }
     const int n = __builtin_popcount(flags);
     int incl = n;                                          // inclusive prefix of n over the wave
@@ -1332,13 +1338,15 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
 
 // ------------------------------------------------------------------------------------------------------------------
 // esp_route_rows: a whole prompt's routing in two launches. The router logits on the fp64 matrix cores: a workgroup is
-// RL_WAVES waves on one tile of 16 rows x 16 router columns (column E is the shared gate), wave w summing the products
-// of K range w with v_mfma_f64_16x16x4f64. Lane (i, q) of a wave feeds row i's and column i's elements at the same k;
+// RL_WAVES waves on one tile of 16 rows x 16 expert columns, wave w summing the products of K range w with
+// v_mfma_f64_16x16x4f64 (the shared gate's column is the top-k launch's: as a 17th column tile of E = 256 it would take
+// 32 more workgroups than the 512 two a CU hold at 512 rows, a second round for one column). Lane (i, q) of a wave feeds row i's and column i's elements at the same k;
 // a step of 32 k gives lane group q the 8 from 8 q (one 16-byte load a lane, 64 contiguous bytes a row), so each MFMA
 // adds 4 products and the steps cover every k once.
 // bf16 x bf16 products are exact in fp64 and so are their sums for ordinary data, so after the one rounding (bf16 for
 // the experts, fp32 for the shared gate) the logits equal route_group's, whose sums run in another order. The waves'
-// partials are added in wave order. Then route_topk_kernel: one wave a row (topk_row).
+// partials are added in wave order. Then route_topk_kernel: one wave a row, the shared gate's fp64 dot (as
+// shared_slots_kernel's: the same exact sum) and topk_row.
 // ------------------------------------------------------------------------------------------------------------------
 constexpr int RL_WAVES = 8;
 constexpr int RL_BATCH = 4;
@@ -1359,17 +1367,16 @@ __device__ __forceinline__ f64x4 route_mfma8(uint4 xv, uint4 gv, f64x4 acc) {
 
 template <int BF16>
 __global__ __launch_bounds__(RL_WAVES * 64) void route_logits_kernel(const uint16_t* __restrict__ x, int x_stride,
-                                                                     const uint16_t* __restrict__ gate,
-                                                                     const uint16_t* __restrict__ sgate, int R, int H,
+                                                                     const uint16_t* __restrict__ gate, int R, int H,
                                                                      int E, int C, float* __restrict__ logits) {
     __shared__ double part[RL_WAVES - 1][4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, q = lane >> 4;
     const int r0 = blockIdx.y * 16, c0 = blockIdx.x * 16;
     const int r = r0 + i < R ? r0 + i : R - 1;                 // rows and columns past the ends: their sums unused
-    const int c = c0 + i < C ? c0 + i : C - 1;
+    const int c = c0 + i < E ? c0 + i : E - 1;
     const uint16_t* xr = x + (size_t)r * x_stride;
-    const uint16_t* gr = c < E ? gate + (size_t)c * H : sgate;
+    const uint16_t* gr = gate + (size_t)c * H;
     const int kw = H / RL_WAVES;                                // elements of a wave, a multiple of 64
     const int kb = wave * kw + 8 * q;                           // a row's 4 lane groups read 64 contiguous bytes
     f64x4 acc = {0.0, 0.0, 0.0, 0.0};
@@ -1399,21 +1406,52 @@ __global__ __launch_bounds__(RL_WAVES * 64) void route_logits_kernel(const uint1
         double sum = acc[v];
         for (int w = 1; w < RL_WAVES; ++w) sum += part[w - 1][v][lane];
         const int row = r0 + q + 4 * v, col = c0 + i;
-        if (row < R && col < C) logits[(size_t)row * C + col] = col < E ? bf2f(f64_to_bf16(sum)) : (float)sum;
+        if (row < R && col < E) logits[(size_t)row * C + col] = bf2f(f64_to_bf16(sum));
     }
 }
 
-__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int R, int E, int k,
-                                                         int shared_id, int* __restrict__ pick_out,
-                                                         float* __restrict__ wts_out) {
+__global__ __launch_bounds__(256) void route_topk_kernel(float* __restrict__ logits, int R, int E, int k,
+                                                         int shared_id, const uint16_t* __restrict__ x, int x_stride,
+                                                         int bf16, const uint16_t* __restrict__ sgate, int H,
+                                                         int* __restrict__ pick_out, float* __restrict__ wts_out) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= R) return;                                        // wave-uniform
     const bool has = shared_id >= 0;
     const int C = E + has, slots = k + has;
+    float ls = 0.f;
+    if (has) {                                                 // the shared gate's logit: x . sgate, one rounding
+        double acc = 0.0;                                      // 2048 k at a time, all their loads in flight
+        for (int h0 = 0; h0 < H; h0 += 2048) {
+            uint2 xu[8], wu[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int h = h0 + 4 * lane + 256 * j;
+                if (h < H) {
+                    xu[j] = *reinterpret_cast<const uint2*>(x + (size_t)r * x_stride + h);
+                    wu[j] = *reinterpret_cast<const uint2*>(sgate + h);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (h0 + 4 * lane + 256 * j >= H) break;
+                const uint16_t xh[4] = {(uint16_t)(xu[j].x & 0xFFFFu), (uint16_t)(xu[j].x >> 16),
+                                        (uint16_t)(xu[j].y & 0xFFFFu), (uint16_t)(xu[j].y >> 16)};
+                const uint16_t wh[4] = {(uint16_t)(wu[j].x & 0xFFFFu), (uint16_t)(wu[j].x >> 16),
+                                        (uint16_t)(wu[j].y & 0xFFFFu), (uint16_t)(wu[j].y >> 16)};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc = __builtin_fma((double)(bf16 ? bf2f(xh[q]) : h2f(xh[q])),
+                                        (double)(bf16 ? bf2f(wh[q]) : h2f(wh[q])), acc);
+            }
+        }
+        ls = (float)wave_sum_f64_dpp(acc);
+        if (lane == 0) logits[(size_t)r * C + E] = ls;
+    }
     int e_mine;
     float w_mine, w_shared;
-    topk_row<false>(logits + (size_t)r * C, E, k, has, lane, e_mine, w_mine, w_shared);
+    topk_row<false>(logits + (size_t)r * C, E, k, false, lane, e_mine, w_mine, w_shared);
+    if (has) w_shared = 1.f / (1.f + expf(-ls));             // topk_row's sigmoid of the shared logit
     if (lane < k) {
         pick_out[(size_t)r * slots + lane] = e_mine;
         wts_out[(size_t)r * slots + lane] = w_mine;
@@ -1545,18 +1583,19 @@ extern "C" int esp_route_rows(const void* x, int x_dtype, int64_t x_stride, int6
                 "route_rows: x / gate must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     const int C = (int)(E + has);
-    const dim3 grid((unsigned)((C + 15) / 16), (unsigned)((R + 15) / 16));
+    const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((R + 15) / 16));
     const uint16_t *xp = static_cast<const uint16_t*>(x), *gp = static_cast<const uint16_t*>(gate),
                    *sp = static_cast<const uint16_t*>(sgate);
     if (x_dtype == ESP_BF16)
-        route_logits_kernel<1><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, sp, (int)R, (int)H, (int)E, C,
+        route_logits_kernel<1><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, (int)R, (int)H, (int)E, C,
                                                                logits);
     else
-        route_logits_kernel<0><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, sp, (int)R, (int)H, (int)E, C,
+        route_logits_kernel<0><<<grid, RL_WAVES * 64, 0, st>>>(xp, (int)x_stride, gp, (int)R, (int)H, (int)E, C,
                                                                logits);
     int rc = esp_host::launch_check("route_rows logits");
     if (rc) return rc;
-    route_topk_kernel<<<(unsigned)((R + 3) / 4), 256, 0, st>>>(logits, (int)R, (int)E, (int)k, (int)shared_id,
+    route_topk_kernel<<<(unsigned)((R + 3) / 4), 256, 0, st>>>(logits, (int)R, (int)E, (int)k, (int)shared_id, xp,
+                                                               (int)x_stride, x_dtype == ESP_BF16 ? 1 : 0, sp, (int)H,
                                                                pick_out, wts_out);
     return esp_host::launch_check("route_rows");
 }
