@@ -248,9 +248,12 @@ def test_group_shared(dev, ext, R):
     assert np.array_equal(uids[:cnt].cpu().numpy(), u) and np.array_equal(members[:cnt].cpu().numpy(), m)
 
 
-def test_rot_in_bit_exact(dev, ext):
-    gen = torch.Generator().manual_seed(3)
-    R, slots, E, K = 5, 3, 6, 512
+@pytest.mark.parametrize("R,slots,K", [(5, 3, 512), (70, 9, 1024), (64, 17, 384)])
+def test_rot_in_bit_exact(dev, ext, R, slots, K):
+    """rot_in against the oracle's rotation, invalid picks left untouched, from a decode window's few rows to a
+    prompt's (more slots than 16, K of 3 and 8 blocks)."""
+    gen = torch.Generator().manual_seed(3 + R)
+    E = 6
     x = torch.randn((R, K), generator=gen).to(torch.bfloat16)
     pick = torch.randint(-1, E + 1, (R, slots), generator=gen).to(torch.int32)       # includes invalid picks
     suh0 = (torch.randint(0, 2, (E, K), generator=gen) * 2 - 1).half()
