@@ -427,7 +427,8 @@ def counter_probe(dev) -> None:
     at 1 token (route_group, the fused gate/up launch, the grouped down launch, down_combine2) and at 32 tokens
     (route_group, rot_in, the grouped gate/up launch, its epilogue, the grouped down launch, down_combine2), one
     replay each, then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row, then two cold config-2 blocks
-    as prompt launches over 512 rows (esp_dense_tile)."""
+    as prompt launches over 512 rows (esp_dense_tile), then two cold 256-expert layers over a 512-token prompt
+    (experts.prefill)."""
     import torch
     from vllm_espalier import dense as D, experts as G, workloads as WL
     gen = torch.Generator(device=dev).manual_seed(4)
@@ -451,8 +452,22 @@ def counter_probe(dev) -> None:
     del heads
     g = run_dense_prompt(dense_stack(2, 12, dev), 512, dev)
     g.replay()
+    del g
+    # two cold 256-expert layers over a whole 512-token prompt (experts.prefill: route_rows, one grouping, the tile
+    # list, the grouped launches over it, the epilogues)
+    stack = [moe_layer(gen, dev) for _ in range(2)]
+    ps = G.prefill_scratch(stack[0][0], 512, 9, dev)
+    xs = [torch.randn((512, 2048), device=dev).to(torch.bfloat16) for _ in stack]
+    o = (torch.empty((512, 2048), dtype=torch.bfloat16, device=dev),
+         torch.empty((512, 2048), dtype=torch.bfloat16, device=dev))
+
+    def fp():
+        for (L, experts, shared, router), x in zip(stack, xs):
+            G.prefill(x, None, None, L, ps, 8, gate=router, out=o[0], out_shared=o[1])
+    graph_of(fp).replay()
     torch.cuda.synchronize()
-    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row, 2 dense blocks over 512 rows")
+    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row, 2 dense blocks over 512 rows, "
+        "2 MoE layers over a 512-token prompt")
 
 
 # ---------------------------------------------------------------------------------------------------------------
