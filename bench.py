@@ -478,7 +478,7 @@ VALU_OPS = ["v_add_u32", "v_mul_lo_u32", "v_bfe_u32", "v_perm_b32", "v_fma_mix_f
 
 
 def probes(dev) -> dict:
-    """The device ceilings DESIGN.md's kernel notes refer to, measured here: (1) the launch floor, an empty kernel of
+    """The device ceilings the kernels are held to, measured here: (1) the launch floor, an empty kernel of
     256 workgroups, as us a launch in a graph of 1000; (2) the streaming read rate of a 2 GiB buffer (16-byte
     nontemporal loads, 8 workgroups of 256 threads a CU); (3) each decode instruction's issue rate, 8 independent
     chains a lane, one and four waves a SIMD, as lane operations a CU a clock (at the reported peak clock)."""
