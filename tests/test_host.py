@@ -168,3 +168,24 @@ def test_int6_index_through_magic_sum():
         direct = fl + 1 if e - fl > F(1, 2) else fl                     # no ties: the distance check above
         via_f32 = int(np.float16(np.float32(float(e + 1536)))) - 1536
         assert direct == q and via_f32 == q, (a, q, direct, via_f32)
+
+
+@pytest.mark.parametrize("E,k,T", [(16, 8, 517), (256, 8, 512), (256, 9, 2048), (64, 2, 33)])
+def test_tile_list_cap_bounds_every_grouping(E, k, T):
+    """tile_list_cap(maxu, T, P) bounds the non-empty 32-row member tiles of any grouping of P = T * k picks: the sum
+    over experts of ceil(members / 32) is at most ceil(P / 32) + the experts used, and at most maxu * ceil(T / 32).
+    Checked on random picks, on picks piled onto a few experts, and on every expert given one member more than a
+    multiple of 32 (the worst case of the first bound)."""
+    rng = np.random.default_rng(E * 1000 + T)
+    P = T * k
+    maxu = min(P, E)
+    cap = X.tile_list_cap(maxu, T, P)
+    cases = [rng.integers(0, E, size=P), rng.integers(0, min(E, 3), size=P)]
+    skew = np.concatenate([np.full(33, e) for e in range(E)] * (P // (33 * E) + 1))[:P]
+    cases.append(skew)
+    for picks in cases:
+        counts = np.bincount(picks, minlength=E)
+        counts = np.minimum(counts, T)               # a token picks an expert once: at most T members an expert
+        tiles = int(sum(-(-int(c) // 32) for c in counts if c > 0))
+        assert tiles <= cap, (tiles, cap)
+    assert cap <= maxu * -(-T // 32)
