@@ -1,9 +1,12 @@
 """The vLLM methods' apply on the GPU, driven through stand-in layers (vLLM is not importable here): EspLinearMethod
-(linear.py:100-117) against the library calls it stands for, bit for bit, in each prefill mode, and against the oracle
-on the per-matrix path; EspMoEMethod.apply / apply_monolithic (moe.py:123-212) against experts.routed2 / windows /
-prefill on the same tables, bit for bit, with the shared expert folded into the launch (its output stored where
-vLLM's runner reads it) or left to the runner.
+(the reference's linear.py:100-117) against the library calls it stands for, bit for bit, in each prefill mode, and
+against the oracle on the per-matrix path; EspMoEMethod.apply / apply_monolithic (moe.py:123-212) against
+experts.routed2 / windows / prefill on the same tables, bit for bit, with the shared expert folded into the launch
+(its output stored where vLLM's runner reads it) or left to the runner; apply_monolithic's first call (the runner's
+gate still in place, real logits) through the router's select_experts, the later ones routed inside.
 """
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -47,7 +50,7 @@ def test_linear_apply_equals_dense(dev, monkeypatch, mode, T):
     print(f"linear apply {mode} T={T}", flush=True)
     monkeypatch.setattr(ops, "PREFILL", mode)
     method, layer = _linear_layer(dev, "model.layers.0.self_attn.qkv_proj", QKV, D, 31)
-    d = ops.DENSE_LAYERS[layer._esp_dense]
+    d = ops.DENSE_LAYERS[layer.espalier.dense_key]
     x = torch.randn((1, T, D), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).to(dev)
     bias = torch.randn((5120,), generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
     y = method.apply(layer, x)
@@ -71,7 +74,7 @@ def test_linear_apply_per_matrix_path(dev, monkeypatch):
     method, layer = _linear_layer(dev, "lm_head", [(None, 1024, "mcg")], 1024, 32)
     x = torch.randn((3, 1024), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
     y = method.apply(layer, x)
-    m = layer._esp_mats[0]
+    m = layer.espalier.mats[0]
     W = O.dequant_f32(m.trellis.cpu().numpy(), 2 * m.K, G.KERNEL_CB[m.cb])
     ref = O.linear_ref(O.bf16_to_f32(bits(x)), W, bits(m.suh), bits(m.svh))
     assert O.rel_l2(y.float().cpu().numpy(), ref) < 2e-2
@@ -85,9 +88,9 @@ class _MLP(torch.nn.Module):
     def __init__(self, gate, up, down, gate_w):
         super().__init__()
         self.gate_up_proj = torch.nn.Module()
-        self.gate_up_proj._esp_mats = [gate, up]
+        self.gate_up_proj.espalier = types.SimpleNamespace(mats=[gate, up])
         self.down_proj = torch.nn.Module()
-        self.down_proj._esp_mats = [down]
+        self.down_proj.espalier = types.SimpleNamespace(mats=[down])
         self.expert_gate = torch.nn.Linear(D, 1, bias=False)
         self.expert_gate.weight.data = gate_w.reshape(1, D)
 
@@ -108,7 +111,12 @@ class _Shared:
 
 
 class _Router:
+    """vLLM's router as the method calls it: softmax top-k with renormalisation, in fp32."""
     top_k, renormalize, scoring_func = 8, True, "softmax"
+
+    def select_experts(self, hidden_states, router_logits, topk_indices_dtype=None, input_ids=None):
+        w, ids = torch.topk(torch.softmax(router_logits.float(), -1), self.top_k, dim=-1)
+        return w / w.sum(-1, keepdim=True), ids.to(topk_indices_dtype)
 
 
 class _Runner:
@@ -151,13 +159,13 @@ def _moe_layer(dev, moe16, order):
     list(layer.load_weights(iter(named)))
     method.process_weights_after_loading(layer)
     sh = _Shared(_MLP(*shared, gate_w), order)
-    layer._esp_runner = _Runner(router, sh)
+    layer.espalier_runner = _Runner(router, sh)
     return method, layer, sh
 
 
 def _direct(layer, x, pick, wts, shared, gate_w, mode, gate=None):
     """The same layer through experts.py directly: its own tables with the shared expert folded in."""
-    L = G.prepare(layer._esp_experts, tuple(shared), gate_w)
+    L = G.prepare(layer.espalier.experts, tuple(shared), gate_w)
     T = x.shape[0]
     if T <= 32:
         s = G.scratch(L, 32, 9, x.device)
@@ -199,7 +207,7 @@ def test_moe_apply_external_shared_and_expert_loop(dev, moe16, monkeypatch):
     wts = torch.softmax(torch.randn((4, 8), generator=gen), -1).to(dev)
     out = method.apply(layer, x, wts, ids, shared_experts=sh, shared_experts_input=x).clone()
     assert sh._output == [None, None] and sh.calls == []
-    L = G.prepare(layer._esp_experts)                                    # no shared slot
+    L = G.prepare(layer.espalier.experts)                                # no shared slot
     wo, _ = G.routed2(x, ids.to(torch.int32).contiguous(), wts.float().contiguous(), L, G.scratch(L, 32, 8, dev),
                       k=8)
     assert torch.equal(out.view(torch.int16), wo.view(torch.int16))
@@ -214,10 +222,14 @@ def test_moe_apply_monolithic_routes_inside(dev, moe16, monkeypatch, mode, T):
     print(f"moe apply_monolithic {mode} T={T}", flush=True)
     monkeypatch.setattr(ops, "PREFILL", mode)
     method, layer, sh = _moe_layer(dev, moe16, Moe.SharedExpertsOrder.MK_INTERNAL_OVERLAPPED)
-    runner = layer._esp_runner
+    runner = layer.espalier_runner
     x = torch.randn((T, D), generator=torch.Generator().manual_seed(40 + T)).to(torch.bfloat16).to(dev)
-    out = method.apply_monolithic(layer, x, x).clone()                   # the pass-through hands x on as logits
-    assert isinstance(runner.gate, Moe._PassThroughGate) and runner.gate(x)[0] is x
+    logits = runner.gate(x)                                              # the first call: the runner's own gate
+    first = method.apply_monolithic(layer, x, logits).clone()
+    w, ids = runner.router.select_experts(x, logits, torch.int32)
+    assert torch.equal(first.view(torch.int16), method.apply(layer, x, w, ids, sh, x).view(torch.int16))
+    assert isinstance(runner.gate, Moe.HiddenStatesGate) and runner.gate(x)[0] is x
+    out = method.apply_monolithic(layer, x, x).clone()                   # from now on the gate hands x on
     wo, ws = _direct(layer, x, None, None, moe16[1], moe16[2], mode, gate=moe16[3])
     assert torch.equal(out.view(torch.int16), wo.view(torch.int16))
     assert torch.equal(sh._output[1].view(torch.int16), ws.view(torch.int16))

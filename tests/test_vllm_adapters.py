@@ -1,7 +1,7 @@
 """The vLLM-facing surface without vLLM (it is not importable in this image): the quantisation config's checkpoint
-scan and per-layer decisions (config.py:33-133), the linear and MoE methods' loaders and checks (linear.py:45-99,
-moe.py:82-122) on stand-in layers, and the plugin's patches of vLLM classes (__init__.py:12-112) on stand-in
-classes and modules. The GPU side of the methods (apply) is tests/test_gpu_adapters.py.
+scan and per-layer decisions (the reference's config.py:33-133), the linear and MoE methods' loaders and checks
+(linear.py:45-99, moe.py:82-122) on stand-in layers, and the plugin's patches of vLLM classes (__init__.py:12-112)
+on stand-in classes and modules. The GPU side of the methods (apply) is tests/test_gpu_adapters.py.
 """
 import gc
 import json
@@ -135,13 +135,15 @@ def test_linear_loader_orders_shards_and_registers():
             p = getattr(layer, suffix)
             p.weight_loader(p, v, shard)
     method.process_weights_after_loading(layer)
-    assert [m.out_features for m in layer._esp_mats] == [256, 128, 128]
+    assert [m.out_features for m in layer.espalier.mats] == [256, 128, 128]
     for i, s in enumerate("qkv"):
-        assert torch.equal(layer._esp_mats[i].trellis, want[s])
-        assert getattr(layer, f"_esp_t{i}") is layer._esp_mats[i].trellis
-    key = layer._esp_dense
+        assert torch.equal(layer.espalier.mats[i].trellis, want[s])
+        assert getattr(layer.espalier, f"trellis_{i}") is layer.espalier.mats[i].trellis
+    assert [n for n, _ in layer.espalier.named_buffers()][:3] == ["trellis_0", "suh_0", "svh_0"]
+    assert layer.espalier.state_dict() == {}                             # buffers, not checkpoint state
+    key = layer.espalier.dense_key
     assert key is not None and ops.DENSE_LAYERS[key].N == 512 and ops.DENSE_LAYERS[key].K == 256
-    assert layer._esp_pad == 0
+    assert layer.espalier.pad == 0
     del layer, p                                                         # p: a placeholder whose loader holds layer
     gc.collect()
     assert key not in ops.DENSE_LAYERS                                   # dropped with its layer
@@ -163,12 +165,14 @@ def test_linear_checks_and_head_padding():
     h = Lin.EspLinearMethod("lm_head")
     h.create_weights(head, 256, [384], 256, 384, torch.bfloat16)
     h.process_weights_after_loading(head)                                # a drafter's head: nothing loaded, fine
-    assert head._esp_mats == [] and head._esp_dense is None
+    assert head.espalier.mats == [] and head.espalier.dense_key is None
+    with pytest.raises(RuntimeError, match="never loaded"):
+        h.apply(head, torch.zeros((1, 256)))
     padded = torch.nn.Module()
     h.create_weights(padded, 256, [512], 256, 512, torch.bfloat16)       # vocabulary padded past the matrix
     _load_linear(h, padded, [(None, 384)], gen)
     h.process_weights_after_loading(padded)
-    assert padded._esp_pad == 128 and ops.DENSE_LAYERS[padded._esp_dense].n_out == 512
+    assert padded.espalier.pad == 128 and ops.DENSE_LAYERS[padded.espalier.dense_key].n_out == 512
 
 
 def _expert_weights(E, gen, D=256, I=128):
@@ -190,8 +194,8 @@ def test_moe_loader_and_checks():
     assert names[:6] == ["w13_esp_trellis", "w13_suh", "w13_svh", "w13_mcg", "w13_esp_grid", "w13_esp_trellis"]
     assert "w2_esp_trellis" in names
     method.process_weights_after_loading(layer)
-    assert len(layer._esp_experts) == 3
-    g, u, d = layer._esp_experts[2]
+    assert len(layer.espalier.experts) == 3
+    g, u, d = layer.espalier.experts[2]
     assert (g.in_features, g.out_features, d.in_features, d.out_features) == (256, 128, 128, 256)
     assert method.get_fused_moe_quant_config(layer) is None
     short = torch.nn.Module()

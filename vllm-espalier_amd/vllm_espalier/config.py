@@ -95,7 +95,7 @@ class EspalierConfig(_Base):
         self.packed_modules_mapping = {k: list(v) for k, v in PACKED.items()}
         self.checkpoint: Path | None = None
 
-    # ---- QuantizationConfig surface (config.py:56-90)
+    # ---- QuantizationConfig surface (the reference's config.py:56-90)
     def get_name(self) -> str:
         return NAME
 
@@ -122,7 +122,7 @@ class EspalierConfig(_Base):
         method = str((hf_quant_cfg or {}).get("quant_method", "")).lower()
         return NAME if method == NAME else None
 
-    # ---- the checkpoint scan (config.py:92-104)
+    # ---- the checkpoint scan (the reference's config.py:92-104)
     def maybe_update_config(self, model_name: str, hf_config=None, revision: str | None = None) -> None:
         d = checkpoint_dir(model_name, revision)
         index = json.loads((d / "model.safetensors.index.json").read_text())
@@ -131,31 +131,22 @@ class EspalierConfig(_Base):
 
     def scan(self, weight_map) -> None:
         """Record every trellis-coded matrix of a weight map (its keys)."""
-        for key in weight_map:
-            if key.endswith(TRELLIS_SUFFIX):
-                t = text_key(key[:-len(TRELLIS_SUFFIX)])
-                if t is not None:
-                    self.coded.add(t)
+        self.coded |= coded_matrices(weight_map)
         if not self.coded:
             raise ValueError("the checkpoint holds no .esp_trellis tensors")
 
-    # ---- per-layer decisions (config.py:106-133)
+    # ---- per-layer decisions (the reference's config.py:106-133)
     def is_exl3(self, prefix: str) -> bool:
-        """Whether the vLLM layer at `prefix` is trellis-coded: every checkpoint matrix it fuses is (an error when
+        """Whether the vLLM layer at `prefix` is trellis-coded: every checkpoint matrix it fuses is (ValueError when
         only some are)."""
-        t = text_key(prefix)
-        if t is None:
-            return False
-        if t == "lm_head":
-            return t in self.coded
-        parent, _, leaf = t.rpartition(".")
-        parts = [f"{parent}.{m}" if parent else m for m in PACKED.get(leaf, [leaf])]
-        found = {p: p in self.coded for p in parts}
-        if any(found.values()) and not all(found.values()):
-            raise ValueError(f"{prefix}: a fused layer only partly trellis-coded: {found}")
-        return all(found.values())
+        members = fused_members(text_key(prefix))
+        coded = [m for m in members if m in self.coded]
+        if coded and len(coded) != len(members):
+            raise ValueError(f"{prefix}: a fused layer only partly trellis-coded: coded {coded} of {members}")
+        return bool(members) and len(coded) == len(members)
 
     def experts_exl3(self, prefix: str) -> bool:
+        """Whether any matrix under the routed experts at `prefix` is trellis-coded."""
         t = text_key(prefix)
         return t is not None and any(k.startswith(t + ".") for k in self.coded)
 
@@ -163,12 +154,28 @@ class EspalierConfig(_Base):
         from .linear import EspLinearMethod
         from .moe import EspMoEMethod
         kind = _layer_kind(layer)
+        if kind is None:
+            return None
         if kind == "experts":
             if not self.experts_exl3(prefix):
                 raise ValueError(f"{prefix}: routed experts without trellis-coded tensors")
             return EspMoEMethod(getattr(layer, "moe_config", None))
-        if kind == "lm_head":
-            return EspLinearMethod(prefix) if self.is_exl3(prefix) else None
-        if kind == "linear":
-            return EspLinearMethod(prefix) if self.is_exl3(prefix) else _unquantized_linear()
-        return None
+        if self.is_exl3(prefix):
+            return EspLinearMethod(prefix)
+        # an uncoded head keeps vLLM's default; an uncoded linear layer runs unquantised
+        return None if kind == "lm_head" else _unquantized_linear()
+
+
+def coded_matrices(weight_map) -> set[str]:
+    """Text keys of the trellis-coded matrices a checkpoint's weight map names (keys ending in .esp_trellis)."""
+    keys = (text_key(k[:-len(TRELLIS_SUFFIX)]) for k in weight_map if k.endswith(TRELLIS_SUFFIX))
+    return {k for k in keys if k is not None}
+
+
+def fused_members(text: str | None) -> list[str]:
+    """The checkpoint matrices a vLLM layer holds, by text key: the PACKED members of a fused layer, else the layer
+    itself; none outside the text model."""
+    if text is None:
+        return []
+    parent, _, leaf = text.rpartition(".")
+    return [f"{parent}.{m}" if parent else m for m in PACKED.get(leaf, [leaf])]

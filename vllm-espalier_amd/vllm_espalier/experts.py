@@ -411,6 +411,9 @@ def prefill_scratch(layer: Layer, rows: int, slots: int, device) -> PrefillScrat
     return found
 
 
+PREFILL_MAX_ROWS = 16384    # tokens one whole-prompt grouping takes (the wide grouping's members an expert)
+
+
 def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None, L: Layer, s: PrefillScratch,
             k: int, gate: torch.Tensor | None = None, out: torch.Tensor | None = None,
             out_shared: torch.Tensor | None = None):
@@ -418,7 +421,22 @@ def prefill(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     over the whole prompt, the bits decode's route_group gives them), ONE grouping of all of them, and the expert GEMMs
     over that grouping with one K split, so each picked expert's weights are decoded once for all its member rows
     (in tiles of 32) instead of once a 32-token window. Returns (routed sum, shared output or None), [T, D] in x's
-    dtype; a token's output depends on its own picks and rows only (the K split is fixed), not on the other tokens."""
+    dtype; a token's output depends on its own picks and rows only (the K split is fixed), not on the other tokens.
+    A prompt of more than PREFILL_MAX_ROWS tokens runs as consecutive chunks of that many (the same bits a row)."""
+    T = x.shape[0]
+    if T <= PREFILL_MAX_ROWS:
+        return _prefill(x, pick, wts, L, s, k, gate, out, out_shared)
+    out = torch.empty((T, L.D), dtype=x.dtype, device=x.device) if out is None else out
+    if L.shared_id >= 0 and out_shared is None:
+        out_shared = torch.empty((T, L.D), dtype=x.dtype, device=x.device)
+    for r0 in range(0, T, PREFILL_MAX_ROWS):
+        rows = slice(r0, r0 + PREFILL_MAX_ROWS)
+        _prefill(x[rows], None if pick is None else pick[rows], None if wts is None else wts[rows], L, s, k, gate,
+                 out[rows], None if out_shared is None else out_shared[rows])
+    return out, (out_shared if L.shared_id >= 0 else None)
+
+
+def _prefill(x, pick, wts, L: Layer, s: PrefillScratch, k: int, gate, out, out_shared):
     e = ext()
     T = x.shape[0]
     has_shared = L.shared_id >= 0
