@@ -33,7 +33,7 @@ extern "C" {
 /* Bits of the device status word (esp_status). */
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
-#define ESP_STATUS_WAIT_TIMEOUT 4 /* a dense_multi group gave up waiting for its producer group (~20 ms) */
+#define ESP_STATUS_WAIT_TIMEOUT 4 /* a chained launch (dense_multi, moe_chain) gave up waiting for a producer (~20 ms) */
 #define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table) */
 
 /* Message of the last failed call on this host thread ("" if none). */
@@ -207,6 +207,27 @@ int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh
                    int64_t counters_numel, const void* svh_g, const void* svh_u, const void* suh_d, void* xd, int64_t K,
                    int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps, int64_t lo, int64_t hi,
                    double limit, int64_t act_mode, void* stream);
+
+/* The decode MoE layer after its routing as ONE launch: esp_moe_gateup's fused gate/up programs, the down programs
+ * (esp_grouped's, K split into the I / 128 gate/up column blocks) and esp_down_combine2's combine, as three program
+ * groups of one grid, each consumer waiting inside the launch for the units it reads (bounded waits: past ~20 ms a
+ * wait sets ESP_STATUS_WAIT_TIMEOUT instead of hanging). A down program lands and decodes its weights before it waits
+ * for its xd slice. Bit-identical to esp_moe_gateup + esp_grouped (mats 1, SK = I / 128) + esp_down_combine2. No
+ * counterpart in the reference, which launches them apart (experts.py:231-261). The tables as esp_moe_gateup's (TP0,
+ * B0, C0 gate; TP1, B1, C1 up) and esp_grouped's down launch (TP2, B2, C2, K2 range [lo_d, hi_d]); members [nexp_max]
+ * [rows]; 1 <= rows <= 4; Z >= 2 * SK * P * I floats (gate/up partials), Zd >= (I / 128) * P * D floats (down partials,
+ * apart from Z), P = rows * slots; y fp32 [P][D] per-slot outputs; out / out_shared [rows][D] in out_dtype;
+ * counters >= nexp_max * (I / 128) * 32 ints and flags >= 32 * 2 * (nexp_max * I / 128 + D / 128) ints, both zero on
+ * entry and left zero. */
+int esp_moe_chain(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                  const int64_t* TP0, const int64_t* TP1, const int64_t* TP2, const int32_t* B0, const int32_t* B1,
+                  const int32_t* B2, const int32_t* C0, const int32_t* C1, const int32_t* C2, const int32_t* uids,
+                  int64_t nexp_max, const int32_t* ucount, const int32_t* members, int64_t rows, const int32_t* pick,
+                  const float* wts, const void* svh_g, const void* svh_u, const void* suh_d, const void* svh_d,
+                  void* xd, float* Z, int64_t z_numel, float* Zd, int64_t zd_numel, float* y, void* out,
+                  int out_dtype, void* out_shared, int32_t* counters, int64_t counters_numel, int32_t* flags,
+                  int64_t flags_numel, int64_t D, int64_t I, int64_t SK, int64_t slots, int64_t E, int64_t n_routed,
+                  int64_t lo, int64_t hi, int64_t lo_d, int64_t hi_d, double limit, int64_t act_mode, void* stream);
 
 /* esp_dense with the input rows normalised in the launch: x = RMSNorm(h + d1 + d2) * norm_w (d1, d2 may be NULL),
  * bit-identical to esp_add_rmsnorm followed by esp_dense; the residual h + d1 + d2 is stored to h_out (not h: other

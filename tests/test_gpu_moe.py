@@ -571,6 +571,7 @@ def test_moe_fused_launches_equal_unfused(dev, layer16, R, invalid, monkeypatch)
         pick[R - 1, 0] = 17                                  # past every table entry (16 routed + shared)
     pick = pick.to(dev)
     wts = torch.softmax(torch.randn((R, 8), generator=gen), -1).to(dev)
+    monkeypatch.setattr(G, "CHAIN", False)                  # esp_moe_gateup itself (the chain: test_gpu_moe_chain)
     monkeypatch.setattr(G, "FUSED", False)
     uo, us = (t.clone() for t in G.routed2(x, pick, wts, L, s))
     monkeypatch.setattr(G, "FUSED", True)
@@ -594,6 +595,7 @@ def test_moe_fused_sixteen_splits(dev, layer16, monkeypatch):
     x = torch.randn((R, D), generator=gen).to(torch.bfloat16).to(dev)
     pick = distinct_picks(R, 16, 8, gen).to(dev)
     wts = torch.softmax(torch.randn((R, 8), generator=gen), -1).to(dev)
+    monkeypatch.setattr(G, "CHAIN", False)
     monkeypatch.setattr(G, "FUSED", False)
     uo, us = (t.clone() for t in G.routed2(x, pick, wts, L, s))
     monkeypatch.setattr(G, "FUSED", True)

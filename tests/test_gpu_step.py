@@ -179,12 +179,14 @@ def test_decoder_graph_replay_equals_eager(small_decoder):
         torch.randn((64, 64), device=b.h.device).sum()        # eager work between replays
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 2])
 def test_decoder_fused_norms_equal_separate(small_decoder, T, monkeypatch):
     """The norms inside the qkv, routing and head launches (dense_rmsnorm, route_group_rmsnorm) against add_rmsnorm
-    launches of their own: logits and the residual stream bit for bit."""
+    launches of their own: logits and the residual stream bit for bit. The qkv launch normalises four waves a row, so
+    at ATTN_W = 8 waves a workgroup the norms run inside the launches for up to 2 rows (beyond, apart)."""
     dec = small_decoder
     ids = [7, 1234, 4000][:T]
+    assert not dec.fused_norms(S.ATTN_W // 4 + 1)
     res = {}
     for fused in (False, True):
         monkeypatch.setattr(S, "FUSE_NORMS", fused)

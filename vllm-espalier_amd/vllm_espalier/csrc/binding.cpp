@@ -494,6 +494,45 @@ void moe_gateup(const at::Tensor& x, int64_t x_stride, const at::Tensor& suh_g, 
                         lo, hi, limit, act_mode, cur_stream()));
 }
 
+// the chained decode MoE layer (no reference counterpart; esp_moe_chain)
+void moe_chain(const at::Tensor& x, int64_t x_stride, const at::Tensor& suh_g, const at::Tensor& suh_u,
+               const at::Tensor& TP0, const at::Tensor& TP1, const at::Tensor& TP2, const at::Tensor& B0,
+               const at::Tensor& B1, const at::Tensor& B2, const at::Tensor& C0, const at::Tensor& C1,
+               const at::Tensor& C2, const at::Tensor& uids, const at::Tensor& ucount, const at::Tensor& members,
+               const at::Tensor& pick, const at::Tensor& wts, const at::Tensor& svh_g, const at::Tensor& svh_u,
+               const at::Tensor& suh_d, const at::Tensor& svh_d, at::Tensor xd, at::Tensor Z, at::Tensor Zd,
+               at::Tensor y, at::Tensor out, std::optional<at::Tensor> out_shared, at::Tensor counters,
+               at::Tensor flags, int64_t D, int64_t I, int64_t SK, int64_t slots, int64_t E, int64_t n_routed,
+               int64_t lo, int64_t hi, int64_t lo_d, int64_t hi_d, double limit, int64_t act_mode) {
+    TORCH_CHECK(x.is_cuda() && (x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf) && x.stride(-1) == 1,
+                "x: bf16/fp16 rows with unit column stride");
+    using TL = std::initializer_list<const at::Tensor*>;
+    for (const at::Tensor* t : TL{&suh_g, &suh_u, &svh_g, &svh_u, &suh_d, &svh_d, &xd}) check(*t, at::kHalf, "fp16 table");
+    for (const at::Tensor* t : TL{&TP0, &TP1, &TP2}) check(*t, at::kLong, "pointer table");
+    for (const at::Tensor* t : TL{&B0, &B1, &B2, &C0, &C1, &C2, &uids, &ucount, &members, &pick, &counters, &flags})
+        check(*t, at::kInt, "int table");
+    for (const at::Tensor* t : TL{&wts, &Z, &Zd, &y}) check(*t, at::kFloat, "fp32 buffer");
+    TORCH_CHECK(members.dim() == 2 && members.size(0) >= uids.numel(), "members: [nexp_max, rows]");
+    const int64_t rows = members.size(1), P = rows * slots;
+    TORCH_CHECK(pick.numel() >= P && wts.numel() >= P && xd.numel() >= P * I && y.numel() >= P * D,
+                "pick / wts / xd / y too small");
+    TORCH_CHECK(out.is_cuda() && out.is_contiguous() && out.numel() >= rows * D, "out: [rows, D] contiguous");
+    if (out_shared.has_value())
+        TORCH_CHECK(out_shared->is_cuda() && out_shared->is_contiguous() && out_shared->scalar_type() == out.scalar_type() &&
+                        out_shared->numel() >= rows * D,
+                    "out_shared: out's dtype, [rows, D] contiguous");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    call(esp_moe_chain(x.data_ptr(), dtype_code(x), x_stride, suh_g.data_ptr(), suh_u.data_ptr(), cptr<int64_t>(TP0),
+                       cptr<int64_t>(TP1), cptr<int64_t>(TP2), cptr<int32_t>(B0), cptr<int32_t>(B1), cptr<int32_t>(B2),
+                       cptr<int32_t>(C0), cptr<int32_t>(C1), cptr<int32_t>(C2), cptr<int32_t>(uids), uids.numel(),
+                       cptr<int32_t>(ucount), cptr<int32_t>(members), rows, cptr<int32_t>(pick), cptr<float>(wts),
+                       svh_g.data_ptr(), svh_u.data_ptr(), suh_d.data_ptr(), svh_d.data_ptr(), xd.data_ptr(),
+                       mptr<float>(Z), Z.numel(), mptr<float>(Zd), Zd.numel(), mptr<float>(y), out.data_ptr(),
+                       dtype_code(out), out_shared.has_value() ? out_shared->data_ptr() : nullptr,
+                       mptr<int32_t>(counters), counters.numel(), mptr<int32_t>(flags), flags.numel(), D, I, SK, slots,
+                       E, n_routed, lo, hi, lo_d, hi_d, limit, act_mode, cur_stream()));
+}
+
 // decode-step glue (no reference counterpart; csrc/step.hip)
 void embed(const at::Tensor& ids, const at::Tensor& table, at::Tensor h) {
     check(ids, at::kInt, "ids");
@@ -649,6 +688,7 @@ PYBIND11_MODULE(espalier_ext, m) {
     m.def("combine", &combine);
     m.def("down_combine", &down_combine);
     m.def("moe_gateup", &moe_gateup);
+    m.def("moe_chain", &moe_chain);
     m.def("dense_rmsnorm", &dense_rmsnorm);
     m.def("status", &status, py::arg("clear") = false);
     m.def("dense_multi", &dense_multi, py::arg("xs"), py::arg("T"), py::arg("suh"), py::arg("svh"), py::arg("col0"),

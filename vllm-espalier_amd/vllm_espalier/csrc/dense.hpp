@@ -85,8 +85,12 @@ struct DenseArgs {
     int wait_off;                          // consumer: x's first column in the producer's y, in 128-column blocks
     int wp_n;                              // consumer: the producer's shards, as y column blocks [wp_c0, + wp_nb)
     int wp_c0[4], wp_nb0[4], wp_nb[4];     //   holding the producer's column blocks wp_nb0 ...
+    int ahead;                             // consumer: decode its B operands before the wait (dense_program)
     int case_id;             // cb * 32 + k2 of the group (the multi kernel's instance)
 };
+
+// A consumer's waves hold at most this many steps' B operands decoded ahead (8 VGPRs a step)
+constexpr int AHEAD_STEPS = 4;
 
 // y rows of one lane (4 values at i) in y's dtype: device-coherent stores when another workgroup of the same launch
 // reads them (a consumer group of a multi launch)
@@ -246,6 +250,7 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     ESP_PHASE(1);
 
     // 1. input rows, rotated, for this K range: shared memory (fused) or the rot launch's xh
+    AheadB<AHEAD_STEPS> pb;   // a consumer's B operands decoded ahead (MULTI, a.ahead)
     RowsA<MG, true> al;       // fused: the rotated rows in shared memory
     RowsA<MG, false> ag;      // else the rot launch's xh
     if (a.fused) {
@@ -282,7 +287,15 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
                 if (idx < M * chunks) weights(idx);
             }
         } else if (MULTI && a.wait_done) {
-            // x is the output of the producer group of this launch: wait for it, then read it device-coherently
+            // x is the output of the producer group of this launch. With `ahead` the K range is one stage: it is
+            // landed and decoded into registers first, so the wait overlaps the producer with this decode. Then wait
+            // for x and read it device-coherently.
+            if constexpr (MULTI) {
+                if (a.ahead) {
+                    wait_stage();
+                    decode_ahead<CB, K2, AHEAD_STEPS>(stage, kr, KW, pb);
+                }
+            }
             dense_wait_producer<MULTI>(a, ticket, c0, chunks);
             for (int idx = wave * 2 + half; idx < M * chunks; idx += 2 * NW) {
                 const int r = idx / chunks, ch = idx % chunks;
@@ -315,13 +328,22 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
         ag.kbase = 0;
     }
 
-    // 2. the K loop (its first wait is a workgroup barrier, after which the rotated rows are visible)
+    // 2. the K loop (its first wait is a workgroup barrier, after which the rotated rows are visible); a consumer
+    // that decoded ahead only runs the MFMAs, after a barrier for the rows
     ESP_PHASE(2);
     f32x4 acc[2][MG];
-    if (a.fused)
+    bool decoded = false;
+    if constexpr (MULTI) decoded = a.ahead && a.wait_done;
+    if (decoded) {
+        if constexpr (MULTI) {
+            __syncthreads();
+            mfma_ahead<MG, AHEAD_STEPS>(pb, k0, kr, KW, al, acc);
+        }
+    } else if (a.fused) {
         block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, al, acc, true);
-    else
+    } else {
         block_gemm<CB, K2, MG>(S.T, NTILES, cb_local * 8, k0, kr, KW, stage, ag, acc, true);
+    }
 
     ESP_PHASE(3);
     // 3. the block's [M][128] sums: every wave's partials in shared memory (the stages are no longer read), the KW

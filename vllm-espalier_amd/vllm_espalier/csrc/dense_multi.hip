@@ -178,6 +178,9 @@ extern "C" int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, 
         }
         A.wait_done = m.g[g - 1].done;
         A.pass = link + (size_t)(lb + nbs[g]) * DONE_STRIDE;
+        // decode ahead of the wait when the longest split is one stage and a wave's steps fit the registers
+        const int steps_max = A.SQ + (A.SR > 0), kw = (int)W / 4;
+        A.ahead = steps_max <= stage_max_steps((int)C.k2) && (steps_max + kw - 1) / kw <= AHEAD_STEPS;
     }
     hipStream_t st = (hipStream_t)stream;
     const int rc = mg == 1 ? launch_multi<1>(m, (int)W, smem, st) : launch_multi<2>(m, (int)W, smem, st);

@@ -167,6 +167,69 @@ __device__ __forceinline__ void block_gemm(const uint32_t* __restrict__ T, int N
     }
 }
 
+// Decode ahead of the A rows: for a K range held whole in one landed stage, the B operands of this wave's steps (those
+// block_gemm gives it: steps kw, kw + KW, ... of the range), decoded into registers before the rows exist. A consumer
+// of a chained launch does this while its producer is still running, then mfma_ahead runs the MFMAs in block_gemm's
+// order, so the sums are bit-identical. MAXS bounds the wave's steps (the caller checks it).
+template <int MAXS>
+struct AheadB {
+    u32x4 b[MAXS][2];
+};
+
+template <int CB, int K2, int MAXS>
+__device__ __forceinline__ void decode_ahead(const uint32_t* stage_lds, int kr, int KW, AheadB<MAXS>& pb) {
+    constexpr int TW = 4 * K2;
+    constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int pair = wave & 3, kw = wave >> 2;
+    const int G = lane >> 4;
+    const int steps = kr >> 5;
+    const LanePlan<K2> lp(lane);
+    const LdsWords<K2> lw(lp);
+    const uint32_t* buf = stage_lds + ((G >> 1) * 8 + 2 * pair) * TW;
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+        const int st = kw + i * KW;
+        if (st < steps) {
+            const uint32_t* tl = buf + st * 2 * ROW_WORDS;
+            uint32_t w[2][6];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 6; ++q) w[j][q] = tl[j * TW + lw.off[q]];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) pb.b[i][j] = decode_words<CB, K2>(w[j], lp);
+        }
+    }
+}
+
+template <int MG, int MAXS, typename AL>
+__device__ __forceinline__ void mfma_ahead(const AheadB<MAXS>& pb, int k0, int kr, int KW, const AL& aload,
+                                           f32x4 (&acc)[2][MG]) {
+    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2;
+    const int steps = kr >> 5;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[j][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < MAXS; ++i) {
+        const int st = kw + i * KW;
+        if (st < steps) {
+            f16x8 av[MG];
+#pragma unroll
+            for (int g = 0; g < MG; ++g) aload(g, k0 + 32 * st, av[g]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const f16x8 b = __builtin_bit_cast(f16x8, pb.b[i][j]);
+#pragma unroll
+                for (int g = 0; g < MG; ++g)
+                    acc[j][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[g], b, acc[j][g], 0, 0, 0);
+            }
+        }
+    }
+}
+
 // The [M][128] sums of the block in red (fp32, [KW][M][128]) from every wave's accumulators; the caller adds the KW
 // slices in order after a barrier.
 template <int MG>

@@ -648,6 +648,8 @@ struct GroupedArgs {
     const int* tiles;              // esp_grouped_list: the non-empty (expert slot, member tile) pairs (tile_list_kernel);
                                    // null: grid x is the expert slot and grid z holds the member tile
     int staged;                    // MODE 0: the member rows staged through shared memory (grouped_body_staged)
+    int* xd_ready;                 // MODE 1 in the chained MoE launch: flags of the (expert slot, 128-column block)
+                                   // units whose xd is stored (CNT_STRIDE apart); null otherwise
 };
 
 // Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
@@ -665,12 +667,12 @@ template <int CB, int K2, int MG, bool LDS>
 __device__ __forceinline__ void grouped_body(const GroupedArgs& a, const uint32_t* __restrict__ T,
                                              const uint16_t* abase, int astride, int kbase, bool by_member,
                                              const int* rows_sh, int nrows, int mat, int split, float scale,
-                                             uint32_t* stage, bool issued, bool dev) {
+                                             uint32_t* stage, bool issued, bool dev, int yb) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
     const int c = lane & 15, G = lane >> 4;
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
     const int NTILES = a.N >> 4;
-    const int nt0 = blockIdx.y * 8;
+    const int nt0 = yb * 8;
     const int kr = a.K / a.SK, k0 = split * kr;
     RowsA<MG, LDS> al;
 #pragma unroll
@@ -718,7 +720,7 @@ __host__ __device__ constexpr int staged_buf_bytes(int k2) { return AST_STEPS * 
 template <int CB, int K2, int MG>
 __device__ __forceinline__ void grouped_body_staged(const GroupedArgs& a, const uint32_t* __restrict__ T,
                                                     const uint16_t* abase, const int* rows_sh, int nrows, int mat,
-                                                    int split, float scale, uint32_t* stage) {
+                                                    int split, float scale, uint32_t* stage, int yb) {
     constexpr int TW = 4 * K2;
     constexpr int ROW_WORDS = StagePlan<K2>::ROW_WORDS;
     constexpr int B_WORDS = AST_STEPS * 2 * ROW_WORDS;
@@ -726,7 +728,7 @@ __device__ __forceinline__ void grouped_body_staged(const GroupedArgs& a, const 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l32 = lane & 31, half = lane >> 5, c = lane & 15, G = lane >> 4;
     const int NW = (int)(blockDim.x >> 6), KW = NW >> 2, pair = wave & 3, kw = wave >> 2;
-    const int NTILES = a.N >> 4, nt0 = blockIdx.y * 8;
+    const int NTILES = a.N >> 4, nt0 = yb * 8;
     const int kr = a.K / a.SK, k0 = split * kr, steps = kr >> 5;
     const int nst = (steps + AST_STEPS - 1) / AST_STEPS;
     unsigned char* const sbase = reinterpret_cast<unsigned char*>(stage);
@@ -886,6 +888,13 @@ __device__ __forceinline__ void sum_splits4x2(const float* __restrict__ pg, cons
         }
 }
 
+// 4 values as fp16 (f2h, as store4) in one device-scope 8-byte store: a workgroup of the same launch reads them
+__device__ __forceinline__ void store4_dev16(uint16_t* p, size_t i, const float (&v)[4]) {
+    const unsigned long long u = (unsigned long long)f2h(v[0]) | ((unsigned long long)f2h(v[1]) << 16) |
+                                 ((unsigned long long)f2h(v[2]) << 32) | ((unsigned long long)f2h(v[3]) << 48);
+    store_dev(reinterpret_cast<unsigned long long*>(p + i), u);
+}
+
 __device__ __forceinline__ void load4_f16(const uint16_t* p, float (&v)[4]) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);
     v[0] = h2f((uint16_t)(u.x & 0xFFFFu)); v[1] = h2f((uint16_t)(u.x >> 16));
@@ -994,7 +1003,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // shared slot's gated output (experts.cu:340-393); n_routed == slots and out_shared == nullptr give down_combine. At
 // least 256 threads; every thread calls it. y == nullptr: no slot's output is stored, and an invalid pick adds zero
 // (where it would reuse y's stored row).
-template <int OUT_DTYPE>
+template <int OUT_DTYPE, bool DEV = false>
 __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, const int* __restrict__ pick,
                                                   const uint16_t* __restrict__ svh_d, float* __restrict__ y,
                                                   const float* __restrict__ wts, void* __restrict__ out,
@@ -1008,7 +1017,7 @@ __device__ __forceinline__ void down_combine_unit(const float* __restrict__ Z, c
         const int p = r * slots + k;
         const int n = n0 + 4 * l32;
         float v[4];
-        sum_splits4(Z + (size_t)p * D + n, (size_t)P * D, SK, v);            // in flight with the pick
+        sum_splits4<DEV>(Z + (size_t)p * D + n, (size_t)P * D, SK, v, Z);   // in flight with the pick
         const int e = pick[p];
         float o[4];
         if (e >= 0 && e < E) {
@@ -1205,23 +1214,26 @@ __global__ __launch_bounds__(TL_THREADS) void tile_list_kernel(const int* __rest
 // into shared memory in the launch (rot_in's arithmetic), and the last of the 2 * SK programs of an (expert,
 // 128-column block) to arrive runs gateup_epilogue for its member rows.
 // ------------------------------------------------------------------------------------------------------------------
+// The program of workgroup (bx, by, bz) of a grid whose y extent is ny (by is the 128-column block): the kernel's
+// whole body, a function of its indices so that the chained MoE launch (moe_chain_kernel) runs the same gate/up
+// program under indices of its own.
 template <int MODE>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void grouped_kernel_t(GroupedArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void grouped_program(const GroupedArgs& a, int bx, int by, int bz, int ny,
+                                                unsigned char* smem) {
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
     // program: expert slot u, member tile (32 members of the expert's list), K split, matrix; with a work list, the
-    // slot and tile are the list's entry blockIdx.x (workgroups past the list's length exit: workgroup-uniform)
+    // slot and tile are the list's entry bx (workgroups past the list's length exit: workgroup-uniform)
     int u, mtile, zz;
     if (MODE != 1 && a.tiles != nullptr) {
-        if ((int)blockIdx.x >= a.tiles[0]) return;
-        const int ent = a.tiles[1 + blockIdx.x];
+        if (bx >= a.tiles[0]) return;
+        const int ent = a.tiles[1 + bx];
         u = ent >> 16;
         mtile = ent & 0xFFFF;
-        zz = blockIdx.z;
+        zz = bz;
     } else {
-        u = blockIdx.x;
-        mtile = blockIdx.z % a.mt;
-        zz = blockIdx.z / a.mt;
+        u = bx;
+        mtile = bz % a.mt;
+        zz = bz / a.mt;
     }
     const int split = zz % a.SK, mat = zz / a.SK;
     const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
@@ -1256,7 +1268,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
         const float qn = __builtin_nanf("");
         const float4 nan4 = make_float4(qn, qn, qn, qn);
         for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
-            float* zp = Zm + (size_t)rows_sh[m] * a.N + blockIdx.y * 128 + 4 * l32;
+            float* zp = Zm + (size_t)rows_sh[m] * a.N + by * 128 + 4 * l32;
             if (MODE == 1)
                 DevBuf(a.Z).store4(zp, nan4);
             else
@@ -1271,8 +1283,8 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
     if (MODE == 1 && runs) {
         // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory; the
         // epilogue's scales (the expert's, for this lane's 4 columns) ride along, for the workgroup that runs it
-        issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), blockIdx.y * 8, stage);
-        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + blockIdx.y * 128 + 4 * l32);
+        issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), by * 8, stage);
+        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + by * 128 + 4 * l32);
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const uint16_t* suh = (mat ? a.suh1 : a.suh0) + (size_t)e * a.K;
         const int chunks = kr >> 7;
@@ -1287,7 +1299,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
         astride = a.xs_stride;
         kbase = k0;
     } else if (MODE == 1) {                                 // not run, but it may still be the last to arrive
-        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + blockIdx.y * 128 + 4 * l32);
+        sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + by * 128 + 4 * l32);
     }
     const bool two = nrows > 16;
     switch (runs ? cb * 32 + k2 : -1) {
@@ -1297,15 +1309,15 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
         const float scale = gemm_scale(CB_);                                                                  \
         if constexpr (MODE == 2) {                                                                            \
             if (two)                                                                                          \
-                grouped_body_staged<KCB, K2_, 2>(a, T, abase, rows_sh, nrows, mat, split, scale, stage);      \
+                grouped_body_staged<KCB, K2_, 2>(a, T, abase, rows_sh, nrows, mat, split, scale, stage, by);      \
             else                                                                                              \
-                grouped_body_staged<KCB, K2_, 1>(a, T, abase, rows_sh, nrows, mat, split, scale, stage);      \
+                grouped_body_staged<KCB, K2_, 1>(a, T, abase, rows_sh, nrows, mat, split, scale, stage, by);      \
         } else if (two) {                                                                                     \
             grouped_body<KCB, K2_, 2, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
-                                      scale, stage, MODE == 1, MODE == 1);                                    \
+                                      scale, stage, MODE == 1, MODE == 1, by);                                    \
         } else {                                                                                              \
             grouped_body<KCB, K2_, 1, MODE == 1>(a, T, abase, astride, kbase, MODE == 1, rows_sh, nrows, mat, split,     \
-                                      scale, stage, MODE == 1, MODE == 1);                                    \
+                                      scale, stage, MODE == 1, MODE == 1, by);                                    \
         }                                                                                                     \
         break;                                                                                                \
     }
@@ -1316,9 +1328,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
     }
     if constexpr (MODE == 1) {
         __shared__ int last;
-        int* cnt_p = a.counters + ((size_t)u * gridDim.y + blockIdx.y) * CNT_STRIDE;
+        int* cnt_p = a.counters + ((size_t)u * ny + by) * CNT_STRIDE;
         if (!arrive_last(cnt_p, 2 * a.SK, &last)) return;
-        const int n = blockIdx.y * 128 + 4 * l32;
+        const int n = by * 128 + 4 * l32;
         for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
             const int p = rows_sh[m];
             float gv[4], uv[4], v[4];
@@ -1330,11 +1342,203 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
                 sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv, a.Z);
             }
             gateup_unit(gv, uv, sc, a.limit, a.act_mode, l32, v);
-            store4(a.xd, F16, (size_t)p * a.N + n, v);
+            if (a.xd_ready != nullptr)                      // read in the same launch: device-coherent stores
+                store4_dev16(a.xd, (size_t)p * a.N + n, v);
+            else
+                store4(a.xd, F16, (size_t)p * a.N + n, v);
         }
         if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every program of the block arrived
+        if (a.xd_ready != nullptr) {                        // the chained launch: xd of (u, by) is ready
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (threadIdx.x == 0) store_dev(a.xd_ready + ((size_t)u * ny + by) * CNT_STRIDE, 1);
+        }
     }
 }
+
+template <int MODE>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void grouped_kernel_t(GroupedArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    grouped_program<MODE>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.y, smem);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// esp_moe_chain: the decode MoE layer after its routing as ONE launch of three program groups (no counterpart in the
+// reference, whose experts.py:231-261 runs them as separate launches). Workgroups of 4 waves, ids in dependency order:
+//   [0, n_gu)           the fused gate/up programs (esp_moe_gateup's grouped_program<1>); the epilogue of each
+//                       (expert slot, 128-column block) stores xd device-coherently, then raises the unit's flag;
+//   [n_gu, + n_dn)      the down programs (expert slot u, output block yb, K split s = gate/up column block s): the
+//                       split's trellis tiles land and are decoded into registers (decode_ahead) before the program
+//                       waits for flag (u, s); then it reads its member rows' xd slice, runs the MFMAs in block_gemm's
+//                       order, stores its partials device-coherently and counts block yb arrived;
+//   [.., + R * D/128)   the combine programs (row r, block yb): they wait for every down program of block yb
+//                       (ucount * SK arrivals), then run down_combine_unit with device-coherent partial loads.
+// Each program's arithmetic is that of the separate launches, in the same order, so the results are bit-identical.
+// Waits are bounded (~20 ms of s_memrealtime, then ESP_STATUS_WAIT_TIMEOUT) and end: producers have lower ids and
+// never wait, so an XCD dispatches every producer before any consumer. A flag or count is reset in the launch by the
+// last of its readers, so the flag buffer is zero between launches.
+// ------------------------------------------------------------------------------------------------------------------
+struct ChainArgs {
+    GroupedArgs gu;                // the fused gate/up group (xd_ready set)
+    GroupedArgs dn;                // the down group: X0 = xd, Z = the down partials, K = I, N = D, SK = I / 128
+    const int* pick;
+    const float* wts;
+    const uint16_t* svh_d;
+    float* y;
+    void* out;
+    void* out_shared;
+    int R, E, n_routed;
+    int* xd_seen;                  // per gate/up unit: down programs past its flag (CNT_STRIDE apart)
+    int* dn_done;                  // per output block: down programs arrived
+    int* dn_seen;                  // per output block: combine programs past the arrivals
+    int nexp, n_gu, n_dn;
+};
+
+// Thread 0 waits until *flag >= target (bounded: ~20 ms, then ESP_STATUS_WAIT_TIMEOUT) and counts the workgroup past
+// it on *seen; the last of n_seen resets both to zero. Every thread calls it.
+__device__ __forceinline__ void chain_wait(int* flag, int target, int* seen, int n_seen) {
+    if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();         // 100 MHz
+        while (load_dev(flag) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
+                raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                break;
+            }
+        }
+        if (__hip_atomic_fetch_add(seen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_seen - 1) {
+            store_dev(flag, 0);
+            store_dev(seen, 0);
+        }
+    }
+    __syncthreads();
+}
+
+constexpr int CHAIN_ROWS = 4;      // rows the chained launch takes (its member rows: one 16-row MFMA group)
+constexpr int CHAIN_AHEAD = 4;     // steps of a down program (128 k) a wave decodes ahead: 32 VGPRs
+
+// One down program's GEMM after its prologue: the split's stage (4 steps of 32 k: kr = 128) decoded ahead, the wait
+// for its xd slice, the MFMAs, the scaled partials to Z
+template <int KCB, int K2>
+__device__ __forceinline__ void chain_down_body(const ChainArgs& c, const uint32_t* __restrict__ T, const int* rows_sh,
+                                                int nrows, int yb, int s, float scale, int* flag, int* seen,
+                                                unsigned char* smem) {
+    const GroupedArgs& a = c.dn;
+    uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, half = lane >> 5;
+    const int cl = lane & 15, G = lane >> 4;
+    const int NW = (int)(blockDim.x >> 6), KW = NW >> 2;
+    const int kr = a.K / a.SK, k0 = s * kr;
+    issue_stage<K2>(T, a.N >> 4, k0 >> 4, kr >> 4, yb * 8, stage);
+    wait_stage();
+    AheadB<CHAIN_AHEAD> pb;
+    decode_ahead<KCB, K2, CHAIN_AHEAD>(stage, kr, KW, pb);
+    chain_wait(flag, 1, seen, a.N >> 7);
+    // the member rows' xd slice, a 32-lane half a row (4 halves a lane), into shared memory past the stage
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
+    for (int m = wave * 2 + half; m < nrows; m += 2 * NW)
+        for (int q = 4 * l32; q < kr; q += 128)
+            *reinterpret_cast<unsigned long long*>(xs + m * a.xs_stride + q) =
+                load_dev(reinterpret_cast<const unsigned long long*>(a.X0 + (size_t)rows_sh[m] * a.K + k0 + q));
+    __syncthreads();
+    RowsA<1, true> al;
+    al.set(0, xs + (cl < nrows ? cl : 0) * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1));   // absent rows read row 0
+    al.kbase = k0;
+    f32x4 acc[2][1];
+    mfma_ahead<1, CHAIN_AHEAD>(pb, k0, kr, KW, al, acc);
+    // the k slots' partials added in order, scaled, one member row a 32-lane half (grouped_body's)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(stage);
+    store_partials<1>(red, nrows, acc);
+    __syncthreads();
+    float* Zm = a.Z + (size_t)s * a.P * a.N;
+    const DevBuf zb(a.Z);
+    for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+        float4 s4 = *reinterpret_cast<const float4*>(red + (size_t)m * 128 + 4 * l32);
+        for (int q = 1; q < KW; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(red + ((size_t)q * nrows + m) * 128 + 4 * l32);
+            s4.x += u.x; s4.y += u.y; s4.z += u.z; s4.w += u.w;
+        }
+        s4.x *= scale; s4.y *= scale; s4.z *= scale; s4.w *= scale;
+        zb.store4(Zm + (size_t)rows_sh[m] * a.N + yb * 128 + 4 * l32, s4);
+    }
+}
+
+__device__ __forceinline__ void chain_down(const ChainArgs& c, int local, unsigned char* smem) {
+    const GroupedArgs& a = c.dn;
+    const int nyd = a.N >> 7, nb_gu = c.gu.N >> 7;
+    const int u = local % c.nexp, yb = (local / c.nexp) % nyd, s = local / (c.nexp * nyd);
+    __shared__ int rows_sh[32];
+    __shared__ int nrows;
+    const int cnt = a.ucount[0];
+    const int e = a.uids[u];
+    if (threadIdx.x < 64) {
+        const int m = threadIdx.x;
+        const int code = m < a.maxm ? a.members[(size_t)u * a.maxm + m] : -1;
+        const int rp = code >= 0 ? (code >> 5) * a.slots + (code & 31) : -1;
+        if (m < 32) rows_sh[m] = rp;
+        const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
+        if (m == 0) nrows = __builtin_popcountll(valid);
+    }
+    if (u >= cnt) return;                                   // no gate/up unit of this slot: nothing waits for it
+    const uint32_t* T = reinterpret_cast<const uint32_t*>(a.TP0[e]);
+    const int k2 = a.B0[e], cb = a.C0[e];
+    __syncthreads();
+    int* flag = c.gu.xd_ready + ((size_t)u * nb_gu + s) * CNT_STRIDE;
+    int* seen = c.xd_seen + ((size_t)u * nb_gu + s) * CNT_STRIDE;
+    const bool runs = supported(cb, k2) && k2 >= a.lo && k2 <= a.hi;
+    switch (runs ? cb * 32 + k2 : -1) {
+#define ESP_CHAIN_CASE(CB_, K2_)                                                                              \
+    case CB_ * 32 + K2_:                                                                                      \
+        chain_down_body<gemm_cb(CB_), K2_>(c, T, rows_sh, nrows, yb, s, gemm_scale(CB_), flag, seen, smem);   \
+        break;
+        ESP_CASES(ESP_CHAIN_CASE)
+#undef ESP_CHAIN_CASE
+        default: {                          // no kernel for the expert's table entry: NaN partials, as grouped's
+            chain_wait(flag, 1, seen, nyd);
+            if (threadIdx.x == 0) raise_status(supported(cb, k2) ? ESP_STATUS_WIDTH_RANGE : ESP_STATUS_NO_KERNEL);
+            const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
+            const float qn = __builtin_nanf("");
+            for (int m = wave * 2 + half; m < nrows; m += 2 * (int)(blockDim.x >> 6))
+                DevBuf(a.Z).store4(a.Z + (size_t)s * a.P * a.N + (size_t)rows_sh[m] * a.N + yb * 128 + 4 * l32,
+                                   make_float4(qn, qn, qn, qn));
+            break;
+        }
+    }
+    // every partial of the program stored: count block yb arrived
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(c.dn_done + (size_t)yb * CNT_STRIDE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int OUT_DTYPE>
+__device__ __forceinline__ void chain_combine(const ChainArgs& c, int local, unsigned char* smem) {
+    const int nyd = c.dn.N >> 7;
+    const int r = local / nyd, yb = local % nyd;
+    const int cnt = c.dn.ucount[0];
+    chain_wait(c.dn_done + (size_t)yb * CNT_STRIDE, cnt * c.dn.SK, c.dn_seen + (size_t)yb * CNT_STRIDE, c.R);
+    down_combine_unit<OUT_DTYPE, true>(c.dn.Z, c.pick, c.svh_d, c.y, c.wts, c.out, c.out_shared, c.dn.P, c.dn.N,
+                                       c.dn.SK, c.E, c.dn.slots, c.n_routed, r, yb,
+                                       reinterpret_cast<float (*)[128]>(smem));
+}
+
+template <int OUT_DTYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void moe_chain_kernel(ChainArgs c) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int id = blockIdx.x;
+    if (id < c.n_gu) {
+        const int ny = c.gu.N >> 7;
+        const int rest = id / c.nexp;
+        grouped_program<1>(c.gu, id % c.nexp, rest % ny, rest / ny, ny, smem);
+    } else if (id < c.n_gu + c.n_dn) {
+        chain_down(c, id - c.n_gu, smem);
+    } else {
+        chain_combine<OUT_DTYPE>(c, id - c.n_gu - c.n_dn, smem);
+    }
+}
+
+
 
 // ------------------------------------------------------------------------------------------------------------------
 // esp_route_rows: a whole prompt's routing in two launches. The router logits on the fp64 matrix cores: a workgroup is
@@ -1790,13 +1994,14 @@ static int grouped_launch_gateup(const GroupedArgs& a, int64_t nexp_max, int64_t
     return esp_host::launch_check("moe_gateup");
 }
 
-extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
-                              const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1,
-                              const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
-                              const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel,
-                              int32_t* counters, int64_t counters_numel, const void* svh_g, const void* svh_u,
-                              const void* suh_d, void* xd, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
-                              int64_t warps, int64_t lo, int64_t hi, double limit, int64_t act_mode, void* stream) {
+// esp_moe_gateup's checks and arguments without the launch (also the chained launch's gate/up group)
+static int gateup_args(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                       const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1, const int32_t* C0,
+                       const int32_t* C1, const int32_t* uids, int64_t nexp_max, const int32_t* ucount,
+                       const int32_t* members, int64_t maxm, float* Z, int64_t z_numel, int32_t* counters,
+                       int64_t counters_numel, const void* svh_g, const void* svh_u, const void* suh_d, void* xd,
+                       int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots, int64_t warps, int64_t lo,
+                       int64_t hi, double limit, int64_t act_mode, GroupedArgs& a, size_t& smem_out) {
     ESP_REQUIRE(x && suh_g && suh_u && TP0 && TP1 && B0 && B1 && C0 && C1 && uids && ucount && members && Z &&
                     counters && svh_g && svh_u && suh_d && xd,
                 "moe_gateup: null pointer");
@@ -1814,8 +2019,7 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
     ESP_REQUIRE(lo >= 2 && hi <= 16 && lo <= hi, "K2 range must lie in [2, 16]");
     ESP_REQUIRE(warps == 4 || warps == 8 || warps == 16, "warps (waves a workgroup) must be 4, 8 or 16");
     ESP_REQUIRE(counters_numel >= nexp_max * (N / 128) * CNT_STRIDE, "counters: 32 ints per (expert, 128 columns)");
-    if (nexp_max <= 0) return esp_host::ok();
-    GroupedArgs a{};
+    a = GroupedArgs{};
     a.mt = 1;
     a.X0 = a.X1 = nullptr;
     a.TP0 = TP0;
@@ -1852,11 +2056,123 @@ extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, cons
     const size_t stage = (size_t)host_stage_words((int)hi, (int)kr) * 4;   // the widest expert's stages
     a.stage_bytes = (int)stage;
     a.xs_stride = (int)kr + 8;                                             // pad rows across the LDS banks
-    const size_t xs = (size_t)32 * a.xs_stride * 2;
-    const size_t red = (size_t)(warps / 4) * 32 * 128 * 4;
-    const size_t smem = stage + xs > red ? stage + xs : red;
-    ESP_REQUIRE(smem <= 160 * 1024, "moe_gateup: shared memory exceeds 160 KiB");
+    // the rotated rows and the k slots' partials of at most maxm member rows (a program's members are <= maxm)
+    const size_t xs = (size_t)maxm * a.xs_stride * 2;
+    const size_t red = (size_t)(warps / 4) * maxm * 128 * 4;
+    smem_out = stage + xs > red ? stage + xs : red;
+    ESP_REQUIRE(smem_out <= 160 * 1024, "moe_gateup: shared memory exceeds 160 KiB");
+    return ESP_OK;
+}
+
+extern "C" int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                              const int64_t* TP0, const int64_t* TP1, const int32_t* B0, const int32_t* B1,
+                              const int32_t* C0, const int32_t* C1, const int32_t* uids, int64_t nexp_max,
+                              const int32_t* ucount, const int32_t* members, int64_t maxm, float* Z, int64_t z_numel,
+                              int32_t* counters, int64_t counters_numel, const void* svh_g, const void* svh_u,
+                              const void* suh_d, void* xd, int64_t K, int64_t N, int64_t P, int64_t SK, int64_t slots,
+                              int64_t warps, int64_t lo, int64_t hi, double limit, int64_t act_mode, void* stream) {
+    GroupedArgs a{};
+    size_t smem = 0;
+    const int rc = gateup_args(x, x_dtype, x_stride, suh_g, suh_u, TP0, TP1, B0, B1, C0, C1, uids, nexp_max, ucount,
+                               members, maxm, Z, z_numel, counters, counters_numel, svh_g, svh_u, suh_d, xd, K, N, P,
+                               SK, slots, warps, lo, hi, limit, act_mode, a, smem);
+    if (rc) return rc;
+    if (nexp_max <= 0) return esp_host::ok();
     return grouped_launch_gateup(a, nexp_max, warps, smem, (hipStream_t)stream);
+}
+
+extern "C" int esp_moe_chain(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
+                             const int64_t* TP0, const int64_t* TP1, const int64_t* TP2, const int32_t* B0,
+                             const int32_t* B1, const int32_t* B2, const int32_t* C0, const int32_t* C1,
+                             const int32_t* C2, const int32_t* uids, int64_t nexp_max, const int32_t* ucount,
+                             const int32_t* members, int64_t rows, const int32_t* pick, const float* wts,
+                             const void* svh_g, const void* svh_u, const void* suh_d, const void* svh_d, void* xd,
+                             float* Z, int64_t z_numel, float* Zd, int64_t zd_numel, float* y, void* out,
+                             int out_dtype, void* out_shared, int32_t* counters, int64_t counters_numel,
+                             int32_t* flags, int64_t flags_numel, int64_t D, int64_t I, int64_t SK, int64_t slots,
+                             int64_t E, int64_t n_routed, int64_t lo, int64_t hi, int64_t lo_d, int64_t hi_d,
+                             double limit, int64_t act_mode, void* stream) {
+    ESP_REQUIRE(rows >= 1 && rows <= CHAIN_ROWS, "moe_chain: 1 to 4 rows");
+    const int64_t P = rows * slots;
+    GroupedArgs gu{};
+    size_t smem_gu = 0;
+    int rc = gateup_args(x, x_dtype, x_stride, suh_g, suh_u, TP0, TP1, B0, B1, C0, C1, uids, nexp_max, ucount, members,
+                         rows, Z, z_numel, counters, counters_numel, svh_g, svh_u, suh_d, xd, D, I, P, SK, slots, 4,
+                         lo, hi, limit, act_mode, gu, smem_gu);
+    if (rc) return rc;
+    ESP_REQUIRE(TP2 && B2 && C2 && pick && wts && svh_d && Zd && y && out && flags, "moe_chain: null pointer");
+    ESP_REQUIRE(out_dtype >= 0 && out_dtype <= 2, "moe_chain: out dtype");
+    ESP_REQUIRE(n_routed >= 0 && n_routed <= slots && E >= 1, "moe_chain: n_routed <= slots");
+    ESP_REQUIRE(I % 128 == 0 && I / 128 <= 64 && D % 128 == 0, "moe_chain: I and D multiples of 128");
+    ESP_REQUIRE(lo_d >= 2 && hi_d <= 16 && lo_d <= hi_d, "moe_chain: down K2 range must lie in [2, 16]");
+    ESP_REQUIRE((((uintptr_t)Zd | (uintptr_t)y) & 15) == 0 && ((uintptr_t)xd & 7) == 0 && ((uintptr_t)svh_d & 7) == 0,
+                "moe_chain: Zd and y 16-byte aligned, xd and svh_d 8-byte aligned");
+    const int64_t SKd = I / 128;                         // a down split a gate/up column block
+    ESP_REQUIRE(zd_numel >= SKd * P * D, "moe_chain: Zd needs I / 128 * P * D floats");
+    ESP_REQUIRE(SKd * P * D <= (int64_t(1) << 30), "moe_chain: the down partials must fit in 4 GiB");
+    const int64_t nb_gu = I / 128, nyd = D / 128;
+    const int64_t lines = 2 * nexp_max * nb_gu + 2 * nyd;
+    ESP_REQUIRE(flags_numel >= lines * CNT_STRIDE, "moe_chain: flags need 32 ints a line, 2 * (nexp * I + D) / 128 lines");
+    ESP_REQUIRE(((uintptr_t)flags & 3) == 0, "moe_chain: flags 4-byte aligned");
+    if (nexp_max <= 0) return esp_host::ok();
+    ChainArgs c{};
+    c.gu = gu;
+    c.gu.xd_ready = flags;
+    c.xd_seen = flags + nexp_max * nb_gu * CNT_STRIDE;
+    c.dn_done = flags + 2 * nexp_max * nb_gu * CNT_STRIDE;
+    c.dn_seen = c.dn_done + nyd * CNT_STRIDE;
+    GroupedArgs& dn = c.dn;
+    dn.mt = 1;
+    dn.X0 = dn.X1 = static_cast<const uint16_t*>(xd);
+    dn.TP0 = dn.TP1 = TP2;
+    dn.B0 = dn.B1 = B2;
+    dn.C0 = dn.C1 = C2;
+    dn.uids = uids;
+    dn.ucount = ucount;
+    dn.members = members;
+    dn.Z = Zd;
+    dn.K = (int)I;
+    dn.N = (int)D;
+    dn.P = (int)P;
+    dn.SK = (int)SKd;
+    dn.maxm = (int)rows;
+    dn.slots = (int)slots;
+    dn.lo = (int)lo_d;
+    dn.hi = (int)hi_d;
+    dn.stage_bytes = host_stage_words((int)hi_d, 128) * 4;
+    dn.xs_stride = 128 + 8;
+    c.pick = pick;
+    c.wts = wts;
+    c.svh_d = static_cast<const uint16_t*>(svh_d);
+    c.y = y;
+    c.out = out;
+    c.out_shared = out_shared;
+    c.R = (int)rows;
+    c.E = (int)E;
+    c.n_routed = (int)n_routed;
+    c.nexp = (int)nexp_max;
+    c.n_gu = (int)(nexp_max * nb_gu * 2 * SK);
+    c.n_dn = (int)(nexp_max * nyd * SKd);
+    const int n_cb = (int)(rows * nyd);
+    const size_t smem_dn = (size_t)dn.stage_bytes + (size_t)16 * dn.xs_stride * 2;
+    const size_t smem_cb = (size_t)slots * 128 * 4;
+    size_t smem = smem_gu > smem_dn ? smem_gu : smem_dn;
+    smem = smem > smem_cb ? smem : smem_cb;
+    hipStream_t st = (hipStream_t)stream;
+    const void* kern = out_dtype == ESP_BF16 ? (const void*)moe_chain_kernel<BF16>
+                       : out_dtype == ESP_F16 ? (const void*)moe_chain_kernel<F16>
+                                              : (const void*)moe_chain_kernel<F32>;
+    if (smem > 64 * 1024 &&
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
+        return esp_host::fail(ESP_ERR_HIP, "moe_chain: cannot raise the shared memory limit to %zu bytes", smem);
+    const unsigned grid = (unsigned)(c.n_gu + c.n_dn + n_cb);
+    if (out_dtype == ESP_BF16)
+        moe_chain_kernel<BF16><<<grid, 256, smem, st>>>(c);
+    else if (out_dtype == ESP_F16)
+        moe_chain_kernel<F16><<<grid, 256, smem, st>>>(c);
+    else
+        moe_chain_kernel<F32><<<grid, 256, smem, st>>>(c);
+    return esp_host::launch_check("moe_chain");
 }
 
 extern "C" int esp_gateup_epilogue(const float* Z, const int32_t* pick, const void* svh_g, const void* svh_u,

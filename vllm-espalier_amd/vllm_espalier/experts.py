@@ -45,6 +45,10 @@ ACT_F32 = 1
 # ESPALIER_MOE_FUSED=0 turns it off.
 FUSED = env("ESPALIER_MOE_FUSED", "1") != "0"
 FUSED_ROWS = 4
+# up to CHAIN_ROWS tokens the fused gate/up launch, the down launch and the combine run as one chained launch
+# (esp_moe_chain: the down programs decode their weights while gate/up runs; the same bits); ESPALIER_MOE_CHAIN=0 off
+CHAIN = env("ESPALIER_MOE_CHAIN", "1") != "0"
+CHAIN_ROWS = 4
 PREFILL_WAVES = 4          # waves a workgroup of the whole-prompt (prefill) grouped launches
 PREFILL_SK_GU = 1          # K splits of the whole-prompt gate/up launch
 PKG = Path(__file__).resolve().parent
@@ -230,6 +234,9 @@ class Scratch:
             "members": ((maxu * rows,), i32, -1),                     # their member rows, -1 padded
             # esp_moe_gateup's arrival counters, one a (expert, 128 columns) on its own 128-byte line
             "counters": ((maxu * (I // 128) * 32,), i32, 0),
+            # esp_moe_chain: the down partials (apart from the gate/up ones) and its hand-off flags (zero between uses)
+            "zd": ((P * D * (I // 128),), f32, 0),
+            "flags": ((2 * (maxu * (I // 128) + D // 128) * 32,), i32, 0),
         }
         for name, (shape, dtype, fill) in layout.items():
             setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
@@ -342,12 +349,19 @@ def routed2(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
     if pick is not None:
         e.group_shared(pick, wts, x, x.stride(0), L.gate_w, L.shared_id, pick_p, wts_p, ids, s.count, members, R, k,
                        L.E)
-    _gate_up(e, x, L, s, R, P, slots, pick_p, ids, members)
-    sk_d = _down(e, L, s, P, slots, ids, members)
     out = torch.empty((R, L.D), dtype=x.dtype, device=x.device) if out is None else out
     if has_shared and out_shared is None:
         out_shared = torch.empty((R, L.D), dtype=x.dtype, device=x.device)
     shared_out = out_shared if has_shared else None
+    sk_gu, sk_d = s.cfg_gu[2], s.cfg_d[2]
+    if CHAIN and FUSED and R <= CHAIN_ROWS and (L.D // sk_gu) % 128 == 0 and sk_d * 128 == L.I:
+        (tg, tu, td), (bg, bu, bd), (cg, cu, cd) = L.ptr, L.k2, L.cb
+        e.moe_chain(x, x.stride(0), L.suh_g, L.suh_u, tg, tu, td, bg, bu, bd, cg, cu, cd, ids, s.count, members,
+                    pick_p, wts_p, L.svh_g, L.svh_u, L.suh_d, L.svh_d, s.xd, s.z, s.zd, s.y, out, shared_out,
+                    s.counters, s.flags, L.D, L.I, sk_gu, slots, L.E, k, *L.k2_gu, *L.k2_d, math.inf, ACT_F32)
+        return out, shared_out
+    _gate_up(e, x, L, s, R, P, slots, pick_p, ids, members)
+    sk_d = _down(e, L, s, P, slots, ids, members)
     e.down_combine2(s.z, pick_p, L.svh_d, s.y, wts_p, out, shared_out, R, P, L.D, sk_d, slots, L.E, k)
     return out, shared_out
 

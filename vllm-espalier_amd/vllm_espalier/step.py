@@ -15,8 +15,11 @@ package, nothing allocates after construction, so a HIP graph holds a whole step
 For up to 4 rows (decode) each norm runs inside its consumer's launch instead (dense_rmsnorm for qkv and the head,
 route_group_rmsnorm for the router), with the same arithmetic in the same order, so the bits do not change: the qkv
 launch stores the residual to a second buffer, which the routing launch reads and adds o to, back into h. qkv and o
-run as one chained launch (dense.DenseMulti: o's workgroups issue their weight copies, then wait for qkv's column
-blocks), with the bits of the two launches apart (MULTI_ATTN = False runs them apart).
+run as one chained launch (dense.DenseMulti: o's workgroups land and decode their weights, then wait for qkv's column
+blocks), with the bits of the two launches apart (MULTI_ATTN = False runs them apart). Both run at ATTN_W waves a
+workgroup: at 8, a CU holds a qkv and an o workgroup at once, so o's decode overlaps qkv (decode step 2,152 -> 2,122
+us on MI355X; at 16 waves the chain was slower than the launches apart, 2,214 against 2,146 us). Up to 4 rows the
+MoE after the routing is one chained launch too (experts.routed2: esp_moe_chain).
 
 Rows never interact (the dense and grouped kernels keep rows apart, norms are per row), so a window of T rows
 gives each row the bits it gets alone.
@@ -39,7 +42,8 @@ VOCAB = 151936
 TOPK = 8
 EPS = 1e-6
 FUSE_NORMS = True            # the norms inside their consumers' launches for up to 4 rows (same bits)
-MULTI_ATTN = False            # qkv and o as one chained launch (same bits)
+MULTI_ATTN = True             # qkv and o as one chained launch (same bits)
+ATTN_W = 8                    # waves a workgroup of the qkv and o launches, chained or apart (the same bits either way)
 
 
 @dataclass
@@ -72,8 +76,10 @@ def build_layer(gen: torch.Generator, dev, E: int = 256, D: int = D_MODEL, I: in
     gate_w = (torch.randn((D,), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
     router = (torch.randn((E, D), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
     moe = G.prepare(experts, shared, gate_w)
-    # both launches at 16 waves (their plans' own width at these shapes), so the chained launch keeps their bits
-    attn = Dn.DenseMulti([qkv, o], after=[False, True], W=16)
+    # both launches at ATTN_W waves, so the chained launch keeps the bits of the launches apart
+    for d in (qkv, o):
+        d.plans = [(sk, ATTN_W, pf) for sk, _, pf in d.plans]
+    attn = Dn.DenseMulti([qkv, o], after=[False, True], W=ATTN_W)
     return DecoderLayer(_norm_weight(gen, dev, D), qkv, o, attn, _norm_weight(gen, dev, D), router, moe, experts,
                         shared)
 
