@@ -663,6 +663,116 @@ def phase_trace(dev) -> dict:
     return res
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# --sweep: the measurements behind the shape rules dense.plan, dense.tile_plan and experts.tile_config (the
+# reference's --sweep / --cold, tests/gpu_dense.py:127-202, and tests/gpu_grouped_sweep.py, with its --force-cb)
+# ---------------------------------------------------------------------------------------------------------------
+def sweep(dev, force_cb: int = -1) -> dict:
+    """Cold sweeps on the BASELINE shapes, each candidate timed as a graph over >= 1 GiB of distinct weights (so
+    nothing is served from the 256 MB MALL):
+      * dense decode plan (dense.plan): config 2's four launches at 1 and 32 rows, every K split SK (uneven splits
+        allowed) and 4 / 8 / 16 waves a workgroup;
+      * prompt K splits (dense.tile_plan): the same launches as prompt launches over 128, 512 and 2048 rows;
+      * grouped tile config (experts.tile_config): the config-4 MoE layer (8 cold 256-expert layers, fused routing)
+        at 1, 4 and 32 tokens, gate/up and down each at 4 / 8 waves and every power-of-two K split. force_cb >= 0
+        decodes every expert with that kernel codebook (the same bytes, wrong values), to see what share of the time
+        is decode arithmetic.
+    Each line gives the best candidates and the rule's choice; the rules themselves depend on the shape alone, so a
+    row's bits never depend on the batch."""
+    import torch
+    from vllm_espalier import dense as D, experts as G
+    sms = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {"dense_plan": {}, "tile_plan": {}, "tile_config": {}}
+    probe = dense_stack(1, 1, dev)
+    copies = max(2, -(-COLD_BYTES // block_bytes(probe[0])))
+    del probe
+    stack = dense_stack(copies, 5, dev)
+    names = ("qkv", "o", "shared gate/up", "shared down")
+    for M in (1, 32):
+        for i, nm in enumerate(names):
+            ds = [blk[i] for blk in stack]
+            K, N = ds[0].K, ds[0].N
+            x = torch.randn((M, K), device=dev).to(torch.bfloat16)
+            ys = [torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev) for d in ds]
+            keep = [d.plans for d in ds]
+            res = []
+            for sk in sorted({1, 2, 3, 4, 6, 8, 12, 16, 24, 32} & set(range(1, K // 128 + 1))):
+                for w in (4, 8, 16):
+                    for d in ds:
+                        d.plans = [(sk, w, 2)] * len(d.launches)
+                    D.scratch(dev, sk * D.MAX_ROWS * N, 0)
+                    g = graph_of(lambda: [d.forward(x, out=y) for d, y in zip(ds, ys)])
+                    res.append((round(time_graph(g, 10, 2) * 1000 / len(ds), 3), sk, w))
+                    del g
+            for d, p in zip(ds, keep):
+                d.plans = p
+            res.sort()
+            rule = D.plan(K, N, sms)[:2]
+            t_rule = next(t for t, sk, w in res if (sk, w) == rule)
+            out["dense_plan"][f"{nm}, M={M}"] = {"rule": list(rule), "rule_us": t_rule,
+                                                "best": [list(r) for r in res[:6]]}
+            log(f"sweep dense plan {nm} M={M}: rule {rule} {t_rule} us; best " +
+                ", ".join(f"{t}({sk},{w})" for t, sk, w in res[:6]))
+    for T in (128, 512, 2048):
+        for i, nm in enumerate(names):
+            ds = [blk[i] for blk in stack[:8]]
+            K, N = ds[0].K, ds[0].N
+            x = torch.randn((T, K), device=dev).to(torch.bfloat16)
+            ys = [torch.empty((T, d.n_out), dtype=torch.bfloat16, device=dev) for d in ds]
+            res = []
+            for sk in sorted({1, 2, 3, 4, 6, 8, 12, 16} & set(range(1, K // 128 + 1))):
+                os.environ["ESPALIER_DENSE_PROMPT_SK"] = str(sk)
+                for d in ds:
+                    d.reserve_prompt(T)
+                g = graph_of(lambda: [d.forward_tile(x, out=y) for d, y in zip(ds, ys)])
+                res.append((round(time_graph(g, 5, 1) * 1000 / len(ds), 2), sk))
+                del g
+            os.environ.pop("ESPALIER_DENSE_PROMPT_SK", None)
+            res.sort()
+            rule = D.tile_plan(K, N)
+            t_rule = next(t for t, sk in res if sk == rule)
+            out["tile_plan"][f"{nm}, T={T}"] = {"rule": rule, "rule_us": t_rule, "best": [list(r) for r in res[:5]]}
+            log(f"sweep prompt SK {nm} T={T}: rule {rule} {t_rule} us; best " +
+                ", ".join(f"{t}({sk})" for t, sk in res[:5]))
+    del stack
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device=dev).manual_seed(4)
+    layers = [moe_layer(gen, dev) for _ in range(8)]
+    if force_cb >= 0:
+        for L, *_ in layers:
+            for c in L.cb:
+                c.fill_(force_cb)
+    for T in (1, 4, 32):
+        xg = torch.Generator(device=dev).manual_seed(40 + T)
+        xs = [torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16) for _ in range(16 * len(layers))]
+        o = (torch.empty((T, 2048), dtype=torch.bfloat16, device=dev),
+             torch.empty((T, 2048), dtype=torch.bfloat16, device=dev))
+        res = []
+        for wgu, skgu in ((4, 2), (4, 4), (4, 8), (4, 16), (8, 4), (8, 8)):
+            for wd, skd in ((4, 1), (4, 2), (4, 4), (8, 2), (8, 4)):
+                os.environ["ESPALIER_GROUPED_TILE_PLAN"] = f"{wgu},{skgu};{wd},{skd}"
+                s = G.Scratch(256 + 1, 2048, 512, 32, 9, dev)
+                calls = [(xs[i], layers[i % len(layers)]) for i in range(len(xs))]
+
+                def fn():
+                    for x, (L, _, _, router) in calls:
+                        G.route(x, router, 8, L, s)
+                        G.routed2(x, None, None, L, s, out=o[0], out_shared=o[1], k=8)
+                g = graph_of(fn)
+                res.append((round(time_graph(g, 5, 1) * 1000 / len(calls), 2), wgu, skgu, wd, skd))
+                del g, s
+        os.environ.pop("ESPALIER_GROUPED_TILE_PLAN", None)
+        res.sort()
+        rule = (G.tile_config(2048, 512, True)[1:3], G.tile_config(512, 2048, False)[1:3])
+        key = (rule[0][0], rule[0][1], rule[1][0], rule[1][1])
+        t_rule = next(r[0] for r in res if tuple(r[1:]) == key)
+        out["tile_config"][f"T={T}"] = {"rule": list(key), "rule_us": t_rule, "best": [list(r) for r in res[:6]],
+                                        "force_cb": force_cb}
+        log(f"sweep grouped tile config T={T}: rule (w,sk gate/up; w,sk down) {key} {t_rule} us; best " +
+            ", ".join(f"{r[0]}{tuple(r[1:])}" for r in res[:6]))
+    return out
+
+
 TILE_PHASE_NAMES = ("first stage landed", "K loop (wave 0)", "of which stage waits", "sums in shared memory",
                     "stored and arrived", "finisher")
 
@@ -776,6 +886,10 @@ def main() -> int:
                     "launch floor, streaming read bandwidth, VALU issue rates) and exit")
     ap.add_argument("--phase-trace", action="store_true", help="time the phases of config 2's batch-1 launches and "
                     "of its prompt launches at 512 rows with the timing build (csrc/build.py --phase-trace) and exit")
+    ap.add_argument("--sweep", action="store_true", help="cold sweeps behind dense.plan, dense.tile_plan and "
+                    "experts.tile_config (one JSON line), and exit")
+    ap.add_argument("--force-cb", type=int, default=-1, help="with --sweep: decode every expert with this kernel "
+                    "codebook (same bytes, wrong values) to see the decode arithmetic's share")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
@@ -809,6 +923,9 @@ def main() -> int:
         return 0
     if a.probes:
         print(json.dumps({"probes": probes(dev), "device": name}), flush=True)
+        return 0
+    if a.sweep:
+        print(json.dumps({"sweep": sweep(dev, a.force_cb), "device": name}), flush=True)
         return 0
     if a.phase_trace:
         res = phase_trace(dev)

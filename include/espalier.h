@@ -34,7 +34,8 @@ extern "C" {
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
 #define ESP_STATUS_WAIT_TIMEOUT 4 /* a chained launch (dense_multi, moe_chain) gave up waiting for a producer (~20 ms) */
-#define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table) */
+#define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table),
+                                   * or esp_grouped_list's grid (sized from its P and maxm) is shorter than the list */
 
 /* Message of the last failed call on this host thread ("" if none). */
 const char* esp_last_error(void);
@@ -294,9 +295,10 @@ int esp_dense_multi(int64_t n_groups, const esp_dense_group* groups, int64_t M, 
  * same kernels, the same bits); the arrival counters, the split-K partials Z and the unfused rotation's rows live in a
  * 16 MiB device array of the library, one per GPU, held until the process ends. A launch needing more than that
  * (64 KiB of counters, then SK * M * sum(n_cols) * 4 bytes of partials rounded to 256, then n_shards * M * K * 2 bytes
- * when the rotation is not fused) fails with ESP_ERR_ARG. Nothing is allocated: the array's address is looked up,
- * and its counters cleared by a kernel on `stream`, on a device's first call. Calls on one GPU share the array, so
- * calls that overlap in time (on different streams, or from different threads) race. */
+ * when the rotation is not fused) fails with ESP_ERR_ARG. Nothing is allocated and nothing but the GEMM is launched:
+ * the array's address is looked up on a device's first call; its counters start zero (the array has no initializer, so
+ * it is zero-filled where the library's code is loaded) and every launch leaves them zero. Calls on one GPU share the
+ * array, so calls that overlap in time (on different streams, or from different threads) race. */
 int esp_dense_noalloc(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
                       const void* const* trellis, const void* const* suh, const void* const* svh,
                       const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,

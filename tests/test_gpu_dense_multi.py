@@ -148,3 +148,24 @@ def test_multi_rejects_bad_groups(dev, ext):
         with pytest.raises(RuntimeError, match="previous group"):
             chain.forward([x, xo_bad], [a, b])
     _clean(ext, chain)
+
+
+def test_multi_refuses_a_changed_plan(dev, ext):
+    """A chain's hand-off maps a consumer's ticket to its launch through the consumer's K splits: a layer whose plan
+    changes after the multi launch was built is refused before any launch, and a new DenseMulti over the changed plan
+    keeps the bits of the launches apart."""
+    qkv, o = _layers(BLOCK[:2], 5, dev)
+    x = torch.randn((1, 2048), generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(dev)
+    chain = Dn.DenseMulti([qkv, o], after=[False, True], W=W)
+    a = torch.empty((1, 5120), dtype=torch.bfloat16, device=dev)
+    b = torch.empty((1, 2048), dtype=torch.bfloat16, device=dev)
+    sk, w, pf = o.plans[0]
+    o.plans = [(sk // 2, w, pf)]
+    with pytest.raises(ValueError, match="plan changed"):
+        chain.forward([x, a[:, :4096]], [a, b])
+    fresh = Dn.DenseMulti([qkv, o], after=[False, True], W=W)
+    fresh.forward([x, a[:, :4096]], [a, b])
+    _clean(ext, fresh)
+    y1 = qkv.forward(x)
+    assert torch.equal(a.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(b.view(torch.int16), o.forward(y1[:, :4096]).view(torch.int16))

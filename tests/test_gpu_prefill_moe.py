@@ -239,3 +239,52 @@ def test_tile_list_over_its_bound_raises_status(dev, ext):
     torch.cuda.synchronize()
     assert int(tiles[0].item()) == cap == 17
     assert int(ext.status(True)) & 8
+
+
+def test_grouped_list_short_grid_raises_status(dev, ext, layer16):
+    """esp_grouped_list launched for fewer picks than its tile list was built for (P given as 32 for a 517-token
+    grouping): its grid, the bound for 32 picks, is shorter than the list, so listed tiles would be left undone; the
+    status word reports ESP_STATUS_TILE_LIST (8). The down projection (one matrix, one split) keeps every access inside
+    the full-size buffers."""
+    L = layer16[0]
+    E, T, slots = 16, 517, 8
+    ext.status(True)
+    gen = torch.Generator().manual_seed(711)
+    pick = torch.stack([torch.randperm(E, generator=gen)[:8] for _ in range(T)]).to(torch.int32).to(dev)
+    P = T * slots
+    maxu = min(P, E)
+    uids = torch.zeros(maxu, dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    members = torch.full((maxu, T), -1, dtype=torch.int32, device=dev)
+    ext.group(pick.reshape(-1), uids, count, members, T, slots, E)
+    tiles = torch.zeros((1 + G.tile_list_cap(maxu, T, P),), dtype=torch.int32, device=dev)
+    ext.tile_list(count, members, maxu, P, tiles)
+    torch.cuda.synchronize()
+    assert int(tiles[0].item()) > G.tile_list_cap(maxu, T, 32)
+    xs = torch.randn((P, I), generator=gen).half().to(dev)
+    z = torch.zeros((P * D,), dtype=torch.float32, device=dev)
+    t, b, c = L.ptr[2], L.k2[2], L.cb[2]
+    ext.grouped_list(xs, xs, t, t, b, b, c, c, uids, count, members, tiles, z, 1, I, D, 32, 1, slots,
+                     G.PREFILL_WAVES, *L.k2_d)
+    torch.cuda.synchronize()
+    assert int(ext.status(True)) & 8
+
+
+def test_prefill_past_the_grouping_limit(dev, layer16):
+    """A prompt of PREFILL_MAX_ROWS + 1 tokens (the shared expert alone then has more members than one whole-prompt
+    grouping takes) runs as chunks: its first and last rows equal the same rows run alone, bit for bit."""
+    L = layer16[0]
+    T = G.PREFILL_MAX_ROWS + 1
+    print(f"prefill moe past the grouping limit T={T}", flush=True)
+    gen = torch.Generator().manual_seed(16385)
+    x = torch.randn((T, D), generator=gen).to(torch.bfloat16).to(dev)
+    pick = torch.stack([torch.randperm(16, generator=gen)[:8] for _ in range(T)]).to(torch.int32).to(dev)
+    wts = torch.softmax(torch.randn((T, 8), generator=gen), -1).to(dev)
+    s = G.prefill_scratch(L, G.PREFILL_MAX_ROWS, 9, dev)
+    out, osh = (t.clone() for t in G.prefill(x, pick, wts, L, s, 8))
+    torch.cuda.synchronize()
+    assert int(ext_status(G)) == 0
+    for r in (0, T - 1):
+        o1, s1 = G.prefill(x[r:r + 1], pick[r:r + 1], wts[r:r + 1], L, s, 8)
+        assert torch.equal(o1[0].view(torch.int16), out[r].view(torch.int16)), r
+        assert torch.equal(s1[0].view(torch.int16), osh[r].view(torch.int16)), r

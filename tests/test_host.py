@@ -189,3 +189,19 @@ def test_tile_list_cap_bounds_every_grouping(E, k, T):
         tiles = int(sum(-(-int(c) // 32) for c in counts if c > 0))
         assert tiles <= cap, (tiles, cap)
     assert cap <= maxu * -(-T // 32)
+
+
+def test_shared_scratch_keeps_outgrown_buffers_only_when_captured():
+    """dense._SharedScratch: a pair outgrown outside any capture is dropped (the allocator reuses it); one handed out
+    during a capture is kept, since a graph may still write to it."""
+    from vllm_espalier import dense as Dn
+    s = Dn._SharedScratch()
+    dev = torch.device("cpu")
+    a = s.reserve(dev, 10, 10)
+    b = s.reserve(dev, 20, 10)
+    assert s.retired == [] and s.reserve(dev, 5, 5) is b and b[0].numel() == 20 and b[1].numel() == 10
+    s.captured.add(dev)                          # as if b had been handed out inside a stream capture
+    c = s.reserve(dev, 40, 10)
+    assert len(s.retired) == 1 and s.retired[0] is b and c[0].numel() == 40
+    assert dev not in s.captured                 # the new pair has not been captured yet
+    del a

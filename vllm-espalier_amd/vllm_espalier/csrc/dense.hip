@@ -353,8 +353,10 @@ extern "C" int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, 
 // file-scope device array instead of caller buffers, for callers that cannot allocate. Layout of the array:
 //   [0, NOALLOC_COUNTER_BYTES)       arrival counters, one a 128-column block, as far apart as fit (up to 32 ints)
 //   [NOALLOC_COUNTER_BYTES, ...)     Z, SK * M * sum(n_cols) floats, then xh (n_shards * M * K halves) if unfused
-// The counters start zero (cleared once per device when the array is first used) and every launch leaves the ones
-// it used zero, so no call needs to clear them. Calls overlapping on one GPU share the array and race.
+// The counters start zero: the array has no initializer, so it lives in the code object's zero-filled segment, which
+// the loader allocates zeroed on each device it loads the library's code onto; every launch leaves the counters it used
+// zero, so no call clears them, and nothing is launched besides the GEMM (a first call inside stream capture records
+// only the GEMM). Calls overlapping on one GPU share the array and race.
 // ======================================================================================================================
 constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
 constexpr size_t NOALLOC_COUNTER_BYTES = size_t(64) << 10;
@@ -366,14 +368,8 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 std::mutex g_noalloc_mu;
 void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];     // the array's device address, per device
 
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int n) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-
-// The array's address on the current device: looked up (and its counter region cleared, by a kernel on `stream`)
-// the first time the device uses it.
-int noalloc_scratch(hipStream_t stream, unsigned char** out) {
+// The array's address on the current device, looked up the first time the device uses it (no device work).
+int noalloc_scratch(unsigned char** out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES)
         return esp_host::fail(ESP_ERR_HIP, "dense_noalloc: no current device");
@@ -384,10 +380,6 @@ int noalloc_scratch(hipStream_t stream, unsigned char** out) {
         if (e != hipSuccess || p == nullptr)
             return esp_host::fail(ESP_ERR_HIP, "dense_noalloc: cannot resolve the scratch array: %s",
                                   hipGetErrorString(e));
-        const int words = (int)(NOALLOC_COUNTER_BYTES / 4);
-        zero_words_kernel<<<(unsigned)((words + 255) / 256), 256, 0, stream>>>(static_cast<uint32_t*>(p), words);
-        const int rc = esp_host::launch_check("dense_noalloc: counter clear");
-        if (rc) return rc;
         g_noalloc_ptr[dev] = p;
     }
     *out = static_cast<unsigned char*>(g_noalloc_ptr[dev]);
@@ -429,9 +421,8 @@ extern "C" int esp_dense_noalloc(const void* x, int x_dtype, int64_t x_stride, i
                               "dense_noalloc: this launch needs %zu bytes of scratch, the array holds %zu "
                               "(use esp_dense with caller buffers)",
                               need, NOALLOC_SCRATCH_BYTES);
-    hipStream_t st = (hipStream_t)stream;
     unsigned char* base = nullptr;
-    const int rc = noalloc_scratch(st, &base);
+    const int rc = noalloc_scratch(&base);
     if (rc) return rc;
     int32_t* counters = reinterpret_cast<int32_t*>(base);
     float* Z = reinterpret_cast<float*>(base + NOALLOC_COUNTER_BYTES);

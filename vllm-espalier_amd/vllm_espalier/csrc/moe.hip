@@ -1225,6 +1225,9 @@ __device__ __forceinline__ void grouped_program(const GroupedArgs& a, int bx, in
     // slot and tile are the list's entry bx (workgroups past the list's length exit: workgroup-uniform)
     int u, mtile, zz;
     if (MODE != 1 && a.tiles != nullptr) {
+        // a grid smaller than the list (a caller that sized the launch for fewer picks or members than esp_tile_list
+        // was given) would leave listed tiles' partials stale: say so in the status word
+        if (bx == 0 && threadIdx.x == 0 && a.tiles[0] > (int)gridDim.x) raise_status(ESP_STATUS_TILE_LIST);
         if (bx >= a.tiles[0]) return;
         const int ent = a.tiles[1 + bx];
         u = ent >> 16;

@@ -75,23 +75,32 @@ TILE_ROWS = 128              # rows a prompt-launch workgroup
 
 class _SharedScratch:
     """The split-K partials Z (fp32) and the unfused rotation's rows xh (fp16), one pair a device, shared by every
-    layer (layers run one after another). Sizes only grow, and only while layers are being built; a pair a growth
-    replaces stays allocated for good, because a graph captured before the growth still writes to it."""
+    layer (layers run one after another). Sizes only grow. A pair that a growth replaces is kept for good only when a
+    graph may write to it (it was handed out during a stream capture); otherwise it is dropped, and the caching
+    allocator reuses its memory, so a series of growing prompts outside capture keeps only the current pair."""
 
     def __init__(self):
         self.current: dict = {}
+        self.captured: set = set()          # devices whose current pair was handed out during a capture
         self.retired: list = []
 
     def reserve(self, device, z_floats: int, xh_halves: int):
         have = self.current.get(device)
+        capturing = device.type == "cuda" and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
         if have is not None and have[0].numel() >= z_floats and have[1].numel() >= xh_halves:
+            if capturing:
+                self.captured.add(device)
             return have
         if have is not None:
-            self.retired.append(have)
+            if device in self.captured:
+                self.retired.append(have)
             z_floats, xh_halves = max(z_floats, have[0].numel()), max(xh_halves, have[1].numel())
+        self.captured.discard(device)
         pair = (torch.empty(max(z_floats, 1), dtype=torch.float32, device=device),
                 torch.empty(max(xh_halves, 1), dtype=torch.float16, device=device))
         self.current[device] = pair
+        if capturing:
+            self.captured.add(device)
         return pair
 
 
@@ -110,10 +119,11 @@ _PROMPT_COUNTERS: dict = {}
 def prompt_scratch(device, z_floats: int, xh_halves: int, counters: int):
     """(Z, xh, counters) of the device for prompt launches, grown to at least the given sizes (the counters zero, and
     left zero by every launch)."""
+    was_captured = device in _PROMPT.captured            # before reserve: a growth there resets the mark
     z, xh = _PROMPT.reserve(device, z_floats, xh_halves)
     cnt = _PROMPT_COUNTERS.get(device)
     if cnt is None or cnt.numel() < counters:
-        if cnt is not None:
+        if cnt is not None and (was_captured or device in _PROMPT.captured):
             _PROMPT.retired.append((cnt,))
         cnt = _PROMPT_COUNTERS[device] = torch.zeros(max(counters, 1), dtype=torch.int32, device=device)
     return z, xh, cnt
@@ -270,6 +280,9 @@ class DenseMulti:
         if any(len(d.launches) != 1 for d in self.layers):
             raise ValueError("every layer of a multi launch must be a single launch group")
         self.W = W
+        # a chain's hand-off maps a consumer's ticket to a launch through its K splits, over counts that only grow: the
+        # plans are fixed here, and forward refuses a layer whose plan has changed since
+        self.plans = [d.launches[0] for d in self.layers]
         device = self.layers[0].mats[0].trellis.device
         blocks = sum(d.launches[0].n // 128 for d in self.layers)
         # the split-K arrival counters (left zero by every launch), then a chain's 64-bit running hand-off counts (a
@@ -285,6 +298,8 @@ class DenseMulti:
         * w, made in the launch, with the residual stored to h_out (xs[0] is then unused)."""
         z, _ = scratch(outs[0].device, 0, 0)
         launches = [d.launches[0] for d in self.layers]
+        if launches != self.plans:
+            raise ValueError("a layer's plan changed after its multi launch was built: build a new DenseMulti")
         h, d1, d2, w, eps, h_out = norm if norm is not None else (None, None, None, None, 0.0, None)
         x0 = h if norm is not None else xs[0]
         ext().dense_multi([x0] + list(xs[1:]), [[d.mats[i].trellis for i in l.members] for d, l in zip(self.layers, launches)],
