@@ -24,7 +24,7 @@ def test_dense_plan_is_valid(K, N):
     sk, w, pf = D.plan(K, N, 256)
     assert w in (4, 8, 16) and 1 <= sk <= K // 32         # splits of whole 32-k steps
     steps = -(-(K // 32) // sk)                           # the longest split
-    assert steps >= w // 4 * (2 if w > 4 else 1)          # every k slot of the workgroup has work
+    assert steps >= w // 4                                # every k slot of the workgroup has a step
     assert (N // 128) * sk <= max(N // 128, 256)          # the splits keep to a workgroup a CU
 
 

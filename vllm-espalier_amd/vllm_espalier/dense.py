@@ -33,9 +33,11 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
     steps, SK need not divide them. The decode of a workgroup's share is bound by its CU's VALU, so the plan spreads
     the layer over the CUs, SK = CUs // blocks (one workgroup a CU), but keeps 4 steps a split: below that the
     fixed costs (rotation, hand-off) outweigh the shorter decode, and 32-row windows lose more to the extra partials
-    than single rows gain (cold sweeps on MI355X). Then 16 waves when a split has 8 steps or more, 8 from 4, else 4,
-    but at most 8 when the launch has more workgroups than CUs (the LM head: 97 us against 113 at 16 waves).
-    ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
+    than single rows gain. Then 16 waves when a split has 4 steps or more, else 4, but at most 8 when the launch has
+    more workgroups than CUs (the LM head: 97 us against 113 at 16 waves). bench.py --sweep (cold, MI355X) confirms the
+    K splits of config 2's four launches at 1 and 32 rows, and the 16 waves also for the 4-step splits of the shared
+    gate/up and down (1 row 6.95 -> 6.91 and 6.49 -> 6.46 us, 32 rows 12.1 -> 10.2 and 8.7 -> 8.0 us against 8
+    waves). ESPALIER_DENSE_TILE_PLAN="sk,w,pf" forces."""
     forced = env("ESPALIER_DENSE_TILE_PLAN")
     if forced:
         sk, w, pf = (int(v) for v in forced.split(","))
@@ -44,7 +46,7 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
     steps_all = K // 32
     sk = max(1, min(steps_all // 4, sms // nb))
     steps = -(-steps_all // sk)
-    w = 16 if steps >= 8 else 8 if steps >= 4 else 4
+    w = 16 if steps >= 4 else 4
     if nb * sk > sms:
         w = min(w, 8)            # more workgroups than CUs: two of 8 waves share a CU and hide each other's waits
     return sk, w, 2
