@@ -244,17 +244,31 @@ __device__ __forceinline__ float bf16_unorder(uint32_t k) {
 // One row's routing from its logits, by one wave: lr holds the E bf16-rounded router logits, then the shared gate's
 // logit. The k largest (one order-preserving 32-bit key an expert: the logit's bf16 bits, then 0xFFFF - id, so ties go
 // to the lowest id), their softmax weights (exponentials of the k maxima at once, the sum in pick order), and the
-// shared slot's sigmoid weight. Lane t < k returns pick t; every lane returns the shared weight (when has). DEV: the
-// logits were stored by other workgroups of the same launch (device-coherent loads).
-template <bool DEV>
+// shared slot's sigmoid weight. Lane t < k returns pick t; every lane returns the shared weight (when has). LOAD 0:
+// plain loads; 1: device-coherent loads (the logits were stored by other workgroups of the same launch), a lane
+// holding experts lane + 64 q; 2: as 1, with one 16-byte load a lane of experts 4 lane + q (E == 256, lr 16-byte
+// aligned). Every load, the shared logit's too, is issued before any is used (one round trip).
+template <int LOAD>
 __device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has, int lane, int& e_out, float& w_out,
                                          float& w_shared) {
+    auto expert = [lane](int q) __attribute__((always_inline)) { return LOAD == 2 ? 4 * lane + q : lane + 64 * q; };
+    float l4[4];
+    if constexpr (LOAD == 2) {
+        const float4 v = DevBuf(lr).load4(lr + 4 * lane);
+        l4[0] = v.x; l4[1] = v.y; l4[2] = v.z; l4[3] = v.w;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = expert(q);
+            l4[q] = e < E ? (LOAD ? load_dev(lr + e) : lr[e]) : 0.f;
+        }
+    }
+    const float ls = has ? (LOAD ? load_dev(lr + E) : lr[E]) : 0.f;
     uint32_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int e = lane + 64 * q;
-        const float l = e < E ? (DEV ? load_dev(lr + e) : lr[e]) : 0.f;
-        key[q] = e < E ? (bf16_order(l) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
+        const int e = expert(q);
+        key[q] = e < E ? (bf16_order(l4[q]) << 16) | (0xFFFFu - (uint32_t)e) : 0u;
     }
     float l_mine = 0.f;
     int e_mine = -1;
@@ -270,7 +284,7 @@ __device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (lane + 64 * q == e) key[q] = 0u;
+            if (expert(q) == e) key[q] = 0u;
     }
     const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_mine), 0));   // pick 0's
     const float p_mine = expf(l_mine - mx);
@@ -279,11 +293,7 @@ __device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has
         psum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_mine), t));
     e_out = e_mine;
     w_out = p_mine / psum;
-    w_shared = 0.f;
-    if (has) {
-        const float ls = DEV ? load_dev(lr + E) : lr[E];
-        w_shared = 1.f / (1.f + expf(-ls));
-    }
+    w_shared = has ? 1.f / (1.f + expf(-ls)) : 0.f;
 }
 
 template <int BF16>
@@ -409,12 +419,52 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     }
     if (!arrive_last(counter, (int)gridDim.x, &last)) return;
 
+    // one row (a decode step): wave 0 takes the top-k and groups its picks itself -- the ids are distinct (top-k picks and
+    // the shared id), so a pick's place is the number of smaller ids and its member rank 0 -- with no shared-memory
+    // round trip or barrier; the tables are group_wave's
+    if (R == 1 && a.uids != nullptr && slots <= 64) {
+        if (wave == 0) {
+            int e_mine;
+            float w_mine, w_shared;
+            if (a.E == 256 && ((uintptr_t)logits & 15) == 0)
+                topk_row<2>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+            else
+                topk_row<1>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+            int id = -1;
+            if (lane < a.k) {
+                pick_out[lane] = e_mine;
+                wts_out[lane] = w_mine;
+                id = e_mine;
+            }
+            if (has && lane == a.k) {
+                pick_out[a.k] = a.shared_id;
+                wts_out[a.k] = w_shared;
+                id = a.shared_id;
+            }
+            const bool valid = lane < slots && id >= 0 && id < C;
+            int place = 0;
+            for (int j = 0; j < slots; ++j) {
+                const int ej = __builtin_amdgcn_readlane(id, j);
+                place += ej >= 0 && ej < C && ej < id;
+            }
+            const uint64_t vm = __ballot(valid);
+            if (lane == 0) *a.ucount = __builtin_popcountll(vm);
+            if (valid) {
+                a.uids[place] = id;
+                a.members[(size_t)place * a.maxm] = lane;                        // row 0, slot lane
+                for (int m = 1; m < a.maxm; ++m) a.members[(size_t)place * a.maxm + m] = -1;
+            }
+        }
+        if (tid == 0) store_dev(counter, 0);
+        return;
+    }
+
     // 2. per row (one wave a row): k maxima of the keys, softmax weights over the picks, the shared gate's sigmoid
     const int NW = RT / 64;
     for (int r = wave; r < R; r += NW) {
         int e_mine;
         float w_mine, w_shared;
-        topk_row<true>(logits + (size_t)r * C, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+        topk_row<1>(logits + (size_t)r * C, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
         if (lane < a.k) {
             pick_out[r * slots + lane] = e_mine;
             wts_out[r * slots + lane] = w_mine;
@@ -1657,7 +1707,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(float* __restrict__ log
     }
     int e_mine;
     float w_mine, w_shared;
-    topk_row<false>(logits + (size_t)r * C, E, k, false, lane, e_mine, w_mine, w_shared);
+    topk_row<0>(logits + (size_t)r * C, E, k, false, lane, e_mine, w_mine, w_shared);
     if (has) w_shared = 1.f / (1.f + expf(-ls));             // topk_row's sigmoid of the shared logit
     if (lane < k) {
         pick_out[(size_t)r * slots + lane] = e_mine;
