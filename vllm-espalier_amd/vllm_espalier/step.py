@@ -178,6 +178,24 @@ class SyntheticDecoder:
             self._bufs[key] = Buffers(T, self.vocab, self.dev)
         return self._bufs[key]
 
+    def prefill_scratch(self, T: int) -> G.PrefillScratch:
+        """The MoE prefill scratch for prompts of T tokens, with the dense layers' prompt scratch grown to match."""
+        L0 = self.layers[0]
+        L0.qkv.reserve_prompt(T)
+        L0.o.reserve_prompt(T)
+        return G.prefill_scratch(L0.moe, T, TOPK + 1, self.dev)
+
+    def prefill_layer(self, L: DecoderLayer, b: Buffers, first: bool, ps: G.PrefillScratch):
+        """One layer of prefill over the rows of b: the dense layers as prompt launches, the MoE over the whole prompt
+        (its picks left in ps.pick, slots a row)."""
+        e = ext()
+        d1, d2 = (None, None) if first else (b.moe, b.moe_shared)
+        e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
+        L.qkv.forward_tile(b.a, out=b.qkv)
+        L.o.forward_tile(b.qkv[:, :Q_OUT], out=b.o)
+        e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
+        G.prefill(b.a, None, None, L.moe, ps, TOPK, gate=L.router, out=b.moe, out_shared=b.moe_shared)
+
     def prefill(self, T: int, head_rows: int = 1) -> Buffers:
         """A whole prompt of T tokens (prefill_buffers(T).ids_in) in the tile mode: the dense layers as prompt launches
         (Dense.forward_tile: each weight decoded once for every 128 rows), every layer's MoE over the whole prompt
@@ -187,19 +205,10 @@ class SyntheticDecoder:
         b = self.prefill_buffers(T)
         e = ext()
         e.embed(b.ids_in, self.embedding, b.h)
-        L0 = self.layers[0]
-        ps = G.prefill_scratch(L0.moe, T, TOPK + 1, self.dev)
-        L0.qkv.reserve_prompt(T)
-        L0.o.reserve_prompt(T)
+        ps = self.prefill_scratch(T)
         self.head.reserve_prompt(head_rows)
-        q = b.qkv[:, :Q_OUT]
         for i, L in enumerate(self.layers):
-            d1, d2 = (None, None) if i == 0 else (b.moe, b.moe_shared)
-            e.add_rmsnorm(b.h, d1, d2, L.norm1, b.a, EPS)
-            L.qkv.forward_tile(b.a, out=b.qkv)
-            L.o.forward_tile(q, out=b.o)
-            e.add_rmsnorm(b.h, b.o, None, L.norm2, b.a, EPS)
-            G.prefill(b.a, None, None, L.moe, ps, TOPK, gate=L.router, out=b.moe, out_shared=b.moe_shared)
+            self.prefill_layer(L, b, i == 0, ps)
         e.add_rmsnorm(b.h, b.moe, b.moe_shared, self.final_norm, b.a, EPS)
         tail = slice(T - head_rows, T)
         self.head.forward_tile(b.a[tail], out=b.logits[tail])
