@@ -168,6 +168,25 @@ def test_dense_row_invariance(dev, name, M):
     assert torch.equal(y, ya)
 
 
+@pytest.mark.parametrize("name", ["qkv", "o", "shared_gate_up", "shared_down"])
+@pytest.mark.parametrize("M", [4, 9, 32])
+def test_dense_split_finish_rows(dev, ext, name, M):
+    """config 2's four launches over 4-32 rows, all with K splits: each row equals its bits alone, every arrival
+    counter is left zero and the status word stays 0. o and gate/up take 16 splits (two rounds of partial loads in
+    the finisher)."""
+    assert int(ext.status(True)) == 0
+    mats = _mats(CONFIGS[name], 17, dev)
+    d = D.Dense(mats)
+    assert all(sk > 1 for sk, _, _ in d.plans)
+    x = torch.randn((M, d.K), generator=torch.Generator().manual_seed(40 + M)).to(torch.bfloat16).to(dev)
+    y = d.forward(x).clone()
+    torch.cuda.synchronize()
+    assert int(d.counters.abs().sum()) == 0
+    assert int(ext.status(True)) == 0
+    for r in (0, M // 2, M - 1):
+        assert torch.equal(d.forward(x[r:r + 1]).view(torch.int16), y[r:r + 1].view(torch.int16)), r
+
+
 @pytest.mark.parametrize("M", [1, 8, 32])
 def test_dense_graph_replay_equals_eager(dev, M):
     mats = _mats(CONFIGS["qkv"], 14, dev)
