@@ -136,18 +136,21 @@ def run_dense(stack, M: int, dev, which=None):
     return graph_of(fn)
 
 
-def run_dense_multi(stack, M: int, dev, chain: bool):
-    """A graph over every copy of the block as ONE esp_dense_multi launch a copy (W = 16 for every group): the four
-    groups side by side on their own inputs ("in one launch per layer"), or chained, each group
-    reading the previous group's output (o reads q, gate/up reads o's output, down reads the gate half), every
-    consumer waiting for its producer inside the launch."""
+CHAIN_W = 8                 # waves a workgroup of the chained block (step.ATTN_W, the decoder's qkv -> o launch)
+
+
+def run_dense_multi(stack, M: int, dev, chain: bool, W: int = 16):
+    """A graph over every copy of the block as ONE esp_dense_multi launch a copy (W waves a workgroup for every
+    group): the four groups side by side on their own inputs ("in one launch per layer"), or
+    chained, each group reading the previous group's output (o reads q, gate/up reads o's output, down reads the gate
+    half), every consumer waiting for its producer inside the launch."""
     import torch
     from vllm_espalier import dense as D
     gen = torch.Generator(device=dev).manual_seed(2000 + M)
     xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for K in (512, 2048, 4096)}
     multis, ios = [], []
     for block in stack:
-        m = D.DenseMulti(block, after=[False, chain, chain, chain], W=16)
+        m = D.DenseMulti(block, after=[False, chain, chain, chain], W=W)
         outs = [torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev) for d in block]
         if chain:
             ins = [xs[2048], outs[0][:, :4096], outs[1], outs[2][:, :512]]
@@ -424,9 +427,9 @@ def traffic_record(fetch_dir: str, write_dir: str) -> dict:
 
 def counter_probe(dev) -> None:
     """The workload of the shader-counter passes over the expert kernels and the LM head: 8 cold 256-expert layers
-    at 1 token (route_group, the fused gate/up launch, the grouped down launch, down_combine2) and at 32 tokens
-    (route_group, rot_in, the grouped gate/up launch, its epilogue, the grouped down launch, down_combine2), one
-    replay each, then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row, then two cold config-2 blocks
+    at 1 token (route_group, then the chained layer, esp_moe_chain) and at 32 tokens (route_group, rot_in, the
+    grouped gate/up launch, its epilogue, the grouped down launch, down_combine2), one replay each, then 8 cold
+    chained config-2 blocks at one row (esp_dense_multi), then two cold LM-head launches (2048 x 151936, 6-bit mcg) at one row, then two cold config-2 blocks
     as prompt launches over 512 rows (esp_dense_tile), then two cold 256-expert layers over a 512-token prompt
     (experts.prefill)."""
     import torch
@@ -445,6 +448,9 @@ def counter_probe(dev) -> None:
                 G.routed2(x, None, None, L, s, out=o[0], out_shared=o[1], k=8)
         graph_of(fn).replay()
     del stack
+    # the chained config-2 block at one row as the decoder runs it (esp_dense_multi, CHAIN_W waves: qkv -> o ->
+    # shared gate/up -> down in one launch, consumers decoding ahead), 8 cold copies
+    run_dense_multi(dense_stack(8, 13, dev), 1, dev, True, CHAIN_W).replay()
     heads = [D.Dense([WL.matrix(2048, 151936, 6, "mcg", gen, dev)]) for _ in range(2)]
     x = torch.randn((1, 2048), device=dev).to(torch.bfloat16)
     y = torch.empty((1, 151936), dtype=torch.bfloat16, device=dev)
@@ -466,8 +472,8 @@ def counter_probe(dev) -> None:
             G.prefill(x, None, None, L, ps, 8, gate=router, out=o[0], out_shared=o[1])
     graph_of(fp).replay()
     torch.cuda.synchronize()
-    log("counter probe: 8 MoE layers at 1 and 32 tokens, 2 LM-head launches at one row, 2 dense blocks over 512 rows, "
-        "2 MoE layers over a 512-token prompt")
+    log("counter probe: 8 MoE layers at 1 and 32 tokens, 8 chained dense blocks at one row, 2 LM-head launches at "
+        "one row, 2 dense blocks over 512 rows, 2 MoE layers over a 512-token prompt")
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -539,7 +545,7 @@ def probes(dev) -> dict:
 # ---------------------------------------------------------------------------------------------------------------
 # rocprofv3 summaries (the text kept under profiles/)
 # ---------------------------------------------------------------------------------------------------------------
-def rocprof_summary(d: str, top: int = 30) -> str:
+def rocprof_summary(d: str, top: int = 80) -> str:
     """Markdown from a `rocprofv3 --kernel-trace --stats --output-format csv -o run` directory: the --stats table
     of this library's kernels, then per-dispatch durations grouped by kernel and launch shape (grid and workgroup, in
     threads), from the kernel trace. Durations in microseconds."""
@@ -955,13 +961,14 @@ def main() -> int:
             g1 = g
         else:
             del g
-    # the same block as one esp_dense_multi launch a layer: side by side, and chained
-    multi = {}
+    # the same block as one esp_dense_multi launch a layer: side by side (16 waves a workgroup), and chained (8, the
+    # decoder's: two workgroups a CU, so a consumer that decoded ahead and waits leaves the other slot to a producer)
+    multi = {"waves": {"independent": 16, "chain": CHAIN_W}}
     for chain in (False, True):
         key = "chain" if chain else "independent"
         multi[key] = {}
         for M in (1, 8, 32):
-            g = run_dense_multi(stack, M, dev, chain)
+            g = run_dense_multi(stack, M, dev, chain, CHAIN_W if chain else 16)
             us = time_graph(g, a.steps if M == 1 else max(5, a.steps // 2), a.warmup) * 1000 / copies
             del g
             multi[key][str(M)] = {"us_per_layer": round(us, 3), "GBps": round(bpl / (us * 1e-6) / 1e9, 1)}
