@@ -211,15 +211,16 @@ int esp_moe_gateup(const void* x, int x_dtype, int64_t x_stride, const void* suh
 
 /* The decode MoE layer after its routing as ONE launch: esp_moe_gateup's fused gate/up programs, the down programs
  * (esp_grouped's, K split into the I / 128 gate/up column blocks) and esp_down_combine2's combine, as three program
- * groups of one grid, each consumer waiting inside the launch for the units it reads (bounded waits: past ~20 ms a
- * wait sets ESP_STATUS_WAIT_TIMEOUT instead of hanging). A down program lands and decodes its weights before it waits
- * for its xd slice. Bit-identical to esp_moe_gateup + esp_grouped (mats 1, SK = I / 128) + esp_down_combine2. No
- * counterpart in the reference, which launches them apart (experts.py:231-261). The tables as esp_moe_gateup's (TP0,
- * B0, C0 gate; TP1, B1, C1 up) and esp_grouped's down launch (TP2, B2, C2, K2 range [lo_d, hi_d]); members [nexp_max]
- * [rows]; 1 <= rows <= 4; Z >= 2 * SK * P * I floats (gate/up partials), Zd >= (I / 128) * P * D floats (down partials,
- * apart from Z), P = rows * slots; y fp32 [P][D] per-slot outputs; out / out_shared [rows][D] in out_dtype;
- * counters >= nexp_max * (I / 128) * 32 ints and flags >= 32 * 2 * (nexp_max * I / 128 + D / 128) ints, both zero on
- * entry and left zero. */
+ * groups of one grid, each consumer reading inside the launch the pieces it needs as soon as they are stored
+ * (bounded waits: past ~20 ms a wait sets ESP_STATUS_WAIT_TIMEOUT instead of hanging). A down program lands and
+ * decodes its weights before it reads its xd slice. Bit-identical to esp_moe_gateup + esp_grouped (mats 1, SK =
+ * I / 128) + esp_down_combine2. No counterpart in the reference, which launches them apart (experts.py:231-261). The
+ * tables as esp_moe_gateup's (TP0, B0, C0 gate; TP1, B1, C1 up) and esp_grouped's down launch (TP2, B2, C2, K2 range
+ * [lo_d, hi_d]); members [nexp_max][rows]; 1 <= rows <= 4; I <= 1024; Z >= 2 * SK * P * I floats (gate/up partials),
+ * Zd >= (I / 128) * P * D floats (down partials, apart from Z), P = rows * slots; xd fp16 [P][I]; y fp32 [P][D]
+ * per-slot outputs; out / out_shared [rows][D] in out_dtype; counters >= nexp_max * (I / 128) * 32 ints and flags >=
+ * 32 * 2 * (nexp_max * I / 128 + D / 128) ints, both zero on entry and left zero. xd and Zd are this launch's own
+ * hand-off buffers (no other launch may write them): every bit set (0xFF bytes) on entry, and left so. */
 int esp_moe_chain(const void* x, int x_dtype, int64_t x_stride, const void* suh_g, const void* suh_u,
                   const int64_t* TP0, const int64_t* TP1, const int64_t* TP2, const int32_t* B0, const int32_t* B1,
                   const int32_t* B2, const int32_t* C0, const int32_t* C1, const int32_t* C2, const int32_t* uids,

@@ -1,9 +1,9 @@
 """esp_moe_chain, the decode MoE layer after its routing as one launch (the fused gate/up programs, the down programs
-that decode their weights before waiting for their xd slice, and the combine), against the separate launches it
+that decode their weights before reading their xd slice, and the combine), against the separate launches it
 replaces (esp_moe_gateup, esp_grouped, esp_down_combine2: the reference's launch chain, experts.py:231-261), bit for
 bit: given picks (out-of-range ones too), fused routing, graph replays with eager work between them, and the BASELINE
-config-4 layer (256 experts of 1-3 bits plus the 4-bit shared expert). Every hand-off flag and counter is left zero
-and no wait times out (status 0). A table entry without a kernel gives the NaN partials and status bit of the
+config-4 layer (256 experts of 1-3 bits plus the 4-bit shared expert). Every reader count and arrival counter is left
+zero, the launch's own xd and down partials are back to their all-ones sentinel, and no wait times out (status 0). A table entry without a kernel gives the NaN partials and status bit of the
 separate launches.
 """
 import math
@@ -33,10 +33,16 @@ def distinct_picks(R, E, k, gen):
     return torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(R)]).to(torch.int32)
 
 
+def _sentinel(s):
+    """The chained launch's own xd and down partials hold every bit set between launches."""
+    return bool((s.xdc.view(torch.int16) == -1).all()) and bool((s.zd.view(torch.int32) == -1).all())
+
+
 def _clean(ext, s):
     torch.cuda.synchronize()
-    assert int(s.flags.abs().sum()) == 0, "hand-off flags left non-zero"
+    assert int(s.flags.abs().sum()) == 0, "reader counts left non-zero"
     assert int(s.counters.abs().sum()) == 0, "arrival counters left non-zero"
+    assert _sentinel(s), "xd or the down partials not put back to the all-ones sentinel"
     assert int(ext.status(True)) == 0, "a wait timed out or a table entry had no kernel"
 
 
@@ -161,11 +167,11 @@ def test_chain_table_without_kernel_sets_status(dev, ext, layer16):
     osh = torch.empty_like(out)
     (tg, tu, td), (bg, bu, _), (cg, cu, _) = L.ptr, L.k2, L.cb
     ext.moe_chain(x, D, L.suh_g, L.suh_u, tg, tu, td, bg, bu, k2_bad, cg, cu, cb_bad, ids, s.count, members,
-                  s.pick[:P], s.wts[:P], L.svh_g, L.svh_u, L.suh_d, L.svh_d, s.xd, s.z, s.zd, s.y, out, osh,
+                  s.pick[:P], s.wts[:P], L.svh_g, L.svh_u, L.suh_d, L.svh_d, s.xdc, s.z, s.zd, s.y, out, osh,
                   s.counters, s.flags, D, I, s.cfg_gu[2], slots, L.E, k, *L.k2_gu, 2, 8, math.inf, 1)
     torch.cuda.synchronize()
     assert int(ext.status(True)) == 1
-    assert int(s.flags.abs().sum()) == 0 and int(s.counters.abs().sum()) == 0
+    assert int(s.flags.abs().sum()) == 0 and int(s.counters.abs().sum()) == 0 and _sentinel(s)
     o = out.float().cpu().numpy()
     assert not np.isfinite(o[0]).any()                        # row 0 picks expert 2
     assert np.isfinite(o[1]).all() and torch.isfinite(osh.float()).all()

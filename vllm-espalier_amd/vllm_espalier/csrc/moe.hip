@@ -698,8 +698,8 @@ struct GroupedArgs {
     const int* tiles;              // esp_grouped_list: the non-empty (expert slot, member tile) pairs (tile_list_kernel);
                                    // null: grid x is the expert slot and grid z holds the member tile
     int staged;                    // MODE 0: the member rows staged through shared memory (grouped_body_staged)
-    int* xd_ready;                 // MODE 1 in the chained MoE launch: flags of the (expert slot, 128-column block)
-                                   // units whose xd is stored (CNT_STRIDE apart); null otherwise
+    int chain;                     // MODE 1 in the chained MoE launch: xd is stored device-coherently, 8 bytes a lane,
+                                   // over the launch's all-ones sentinel, and read by the down programs of the launch
 };
 
 // Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
@@ -1395,17 +1395,12 @@ __device__ __forceinline__ void grouped_program(const GroupedArgs& a, int bx, in
                 sum_splits4<true>(a.Z + ((size_t)a.SK * a.P + p) * a.N + n, (size_t)a.P * a.N, a.SK, uv, a.Z);
             }
             gateup_unit(gv, uv, sc, a.limit, a.act_mode, l32, v);
-            if (a.xd_ready != nullptr)                      // read in the same launch: device-coherent stores
+            if (a.chain)                                    // read in the same launch: device-coherent stores
                 store4_dev16(a.xd, (size_t)p * a.N + n, v);
             else
                 store4(a.xd, F16, (size_t)p * a.N + n, v);
         }
         if (threadIdx.x == 0) store_dev(cnt_p, 0);          // every program of the block arrived
-        if (a.xd_ready != nullptr) {                        // the chained launch: xd of (u, by) is ready
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (threadIdx.x == 0) store_dev(a.xd_ready + ((size_t)u * ny + by) * CNT_STRIDE, 1);
-        }
     }
 }
 
@@ -1419,20 +1414,24 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5))) void 
 // esp_moe_chain: the decode MoE layer after its routing as ONE launch of three program groups (no counterpart in the
 // reference, whose experts.py:231-261 runs them as separate launches). Workgroups of 4 waves, ids in dependency order:
 //   [0, n_gu)           the fused gate/up programs (esp_moe_gateup's grouped_program<1>); the epilogue of each
-//                       (expert slot, 128-column block) stores xd device-coherently, then raises the unit's flag;
+//                       (expert slot, 128-column block) stores its rows of xd device-coherently, 8 bytes a lane;
 //   [n_gu, + n_dn)      the down programs (expert slot u, output block yb, K split s = gate/up column block s): the
-//                       split's trellis tiles land and are decoded into registers (decode_ahead) before the program
-//                       waits for flag (u, s); then it reads its member rows' xd slice, runs the MFMAs in block_gemm's
-//                       order, stores its partials device-coherently and counts block yb arrived;
-//   [.., + R * D/128)   the combine programs (row r, block yb): they wait for every down program of block yb
-//                       (ucount * SK arrivals), then run down_combine_unit with device-coherent partial loads.
-// Each program's arithmetic is that of the separate launches, in the same order, so the results are bit-identical.
-// Waits are bounded (~20 ms of s_memrealtime, then ESP_STATUS_WAIT_TIMEOUT) and end: producers have lower ids and
-// never wait, so an XCD dispatches every producer before any consumer. A flag or count is reset in the launch by the
-// last of its readers, so the flag buffer is zero between launches.
+//                       split's trellis tiles land and are decoded into registers (decode_ahead); then the program
+//                       reads its member rows' xd slice as soon as the epilogue has stored it, runs the MFMAs in
+//                       block_gemm's order and stores its partials device-coherently;
+//   [.., + R * D/128)   the combine programs (row r, block yb): down_combine_unit's arithmetic on each valid slot's
+//                       partials, read as soon as the down programs have stored them.
+// The hand-offs carry no flags: xd and the down partials are buffers of this launch alone that hold an all-ones
+// sentinel (no fp16 quad and no fp32 value the kernels store has that bit pattern: their NaNs are the canonical quiet
+// ones), and a reader loads each 8- or 16-byte piece device-coherently until no word of it is all-ones. A piece is
+// read, then put back to all-ones in the same launch: xd of (u, s) by the last of its 16 down programs (a count
+// reset with it), a partial by the one combine program that reads it. So both buffers hold the sentinel between
+// launches. Waits are bounded (~20 ms of s_memrealtime, then ESP_STATUS_WAIT_TIMEOUT) and end: producers have lower
+// ids and never wait, so an XCD dispatches every producer before any consumer. Each program's arithmetic is that of
+// the separate launches, in the same order, so the results are bit-identical.
 // ------------------------------------------------------------------------------------------------------------------
 struct ChainArgs {
-    GroupedArgs gu;                // the fused gate/up group (xd_ready set)
+    GroupedArgs gu;                // the fused gate/up group (chain set)
     GroupedArgs dn;                // the down group: X0 = xd, Z = the down partials, K = I, N = D, SK = I / 128
     const int* pick;
     const float* wts;
@@ -1441,40 +1440,58 @@ struct ChainArgs {
     void* out;
     void* out_shared;
     int R, E, n_routed;
-    int* xd_seen;                  // per gate/up unit: down programs past its flag (CNT_STRIDE apart)
-    int* dn_done;                  // per output block: down programs arrived
-    int* dn_seen;                  // per output block: combine programs past the arrivals
+    int* xd_seen;                  // per (expert slot, gate/up column block): down programs that read its xd
     int nexp, n_gu, n_dn;
 };
 
-// Thread 0 waits until *flag >= target (bounded: ~20 ms, then ESP_STATUS_WAIT_TIMEOUT) and counts the workgroup past
-// it on *seen; the last of n_seen resets both to zero. Every thread calls it.
-__device__ __forceinline__ void chain_wait(int* flag, int target, int* seen, int n_seen) {
-    if (threadIdx.x == 0) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();         // 100 MHz
-        while (load_dev(flag) < target) {
+constexpr int CHAIN_ROWS = 4;      // rows the chained launch takes (its member rows: one 16-row MFMA group)
+constexpr int CHAIN_AHEAD = 4;     // steps of a down program (128 k) a wave decodes ahead: 32 VGPRs
+constexpr int CHAIN_MAX_SPLITS = 8;                  // down K splits (I / 128) the combine polls at once
+constexpr unsigned long long CHAIN_EMPTY = ~0ull;    // the sentinel of the launch's xd and down partials
+
+__device__ __forceinline__ bool chain_late(uint64_t t0) {
+    return __builtin_amdgcn_s_memrealtime() - t0 > 2000000ull;       // ~20 ms at 100 MHz
+}
+
+// The member rows' xd slice of (expert slot u, column block s): 128 halves a row, a 32-lane half a row, each lane's
+// 8 bytes loaded device-coherently until the epilogue has stored them, into shared memory (xs, rows xs_stride
+// halves apart) when xs is given. The last of the n_seen readers of the slice puts the sentinel back, and its count.
+__device__ __forceinline__ void chain_take_xd(uint16_t* xd, int K, int k0, const int* rows_sh, int nrows, uint16_t* xs,
+                                              int xs_stride, int* seen, int n_seen) {
+    const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
+    const int NW = (int)(blockDim.x >> 6);
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int m = wave * 2 + half; m < nrows; m += 2 * NW) {
+        const unsigned long long* q =
+            reinterpret_cast<const unsigned long long*>(xd + (size_t)rows_sh[m] * K + k0 + 4 * l32);
+        unsigned long long v = load_dev(q);
+        while (v == CHAIN_EMPTY) {
             __builtin_amdgcn_s_sleep(1);
-            if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
+            if (chain_late(t0)) {
                 raise_status(ESP_STATUS_WAIT_TIMEOUT);
                 break;
             }
+            v = load_dev(q);
         }
-        if (__hip_atomic_fetch_add(seen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_seen - 1) {
-            store_dev(flag, 0);
-            store_dev(seen, 0);
-        }
+        if (xs != nullptr) *reinterpret_cast<unsigned long long*>(xs + m * xs_stride + 4 * l32) = v;
+    }
+    __shared__ int last_reader;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        last_reader = __hip_atomic_fetch_add(seen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_seen - 1;
+        if (last_reader) store_dev(seen, 0);
     }
     __syncthreads();
+    if (last_reader)                                 // every reader has its copy: the slice back to the sentinel
+        for (int m = wave * 2 + half; m < nrows; m += 2 * NW)
+            store_dev(reinterpret_cast<unsigned long long*>(xd + (size_t)rows_sh[m] * K + k0 + 4 * l32), CHAIN_EMPTY);
 }
 
-constexpr int CHAIN_ROWS = 4;      // rows the chained launch takes (its member rows: one 16-row MFMA group)
-constexpr int CHAIN_AHEAD = 4;     // steps of a down program (128 k) a wave decodes ahead: 32 VGPRs
-
-// One down program's GEMM after its prologue: the split's stage (4 steps of 32 k: kr = 128) decoded ahead, the wait
-// for its xd slice, the MFMAs, the scaled partials to Z
+// One down program's GEMM after its prologue: the split's stage (4 steps of 32 k: kr = 128) decoded ahead, its
+// member rows' xd slice, the MFMAs, the scaled partials to Z
 template <int KCB, int K2>
 __device__ __forceinline__ void chain_down_body(const ChainArgs& c, const uint32_t* __restrict__ T, const int* rows_sh,
-                                                int nrows, int yb, int s, float scale, int* flag, int* seen,
+                                                int nrows, int yb, int s, float scale, int* seen,
                                                 unsigned char* smem) {
     const GroupedArgs& a = c.dn;
     uint32_t* stage = reinterpret_cast<uint32_t*>(smem);
@@ -1486,14 +1503,8 @@ __device__ __forceinline__ void chain_down_body(const ChainArgs& c, const uint32
     wait_stage();
     AheadB<CHAIN_AHEAD> pb;
     decode_ahead<KCB, K2, CHAIN_AHEAD>(stage, kr, KW, pb);
-    chain_wait(flag, 1, seen, a.N >> 7);
-    // the member rows' xd slice, a 32-lane half a row (4 halves a lane), into shared memory past the stage
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
-    for (int m = wave * 2 + half; m < nrows; m += 2 * NW)
-        for (int q = 4 * l32; q < kr; q += 128)
-            *reinterpret_cast<unsigned long long*>(xs + m * a.xs_stride + q) =
-                load_dev(reinterpret_cast<const unsigned long long*>(a.X0 + (size_t)rows_sh[m] * a.K + k0 + q));
-    __syncthreads();
+    chain_take_xd(const_cast<uint16_t*>(a.X0), a.K, k0, rows_sh, nrows, xs, a.xs_stride, seen, a.N >> 7);
     RowsA<1, true> al;
     al.set(0, xs + (cl < nrows ? cl : 0) * a.xs_stride + 16 * (G >> 1) + 4 * (G & 1));   // absent rows read row 0
     al.kbase = k0;
@@ -1533,22 +1544,21 @@ __device__ __forceinline__ void chain_down(const ChainArgs& c, int local, unsign
         const uint64_t valid = __ballot(rp >= 0);          // members come first, -1 padded
         if (m == 0) nrows = __builtin_popcountll(valid);
     }
-    if (u >= cnt) return;                                   // no gate/up unit of this slot: nothing waits for it
+    if (u >= cnt) return;                                   // no gate/up unit of this slot: nothing to read
     const uint32_t* T = reinterpret_cast<const uint32_t*>(a.TP0[e]);
     const int k2 = a.B0[e], cb = a.C0[e];
     __syncthreads();
-    int* flag = c.gu.xd_ready + ((size_t)u * nb_gu + s) * CNT_STRIDE;
     int* seen = c.xd_seen + ((size_t)u * nb_gu + s) * CNT_STRIDE;
     const bool runs = supported(cb, k2) && k2 >= a.lo && k2 <= a.hi;
     switch (runs ? cb * 32 + k2 : -1) {
 #define ESP_CHAIN_CASE(CB_, K2_)                                                                              \
     case CB_ * 32 + K2_:                                                                                      \
-        chain_down_body<gemm_cb(CB_), K2_>(c, T, rows_sh, nrows, yb, s, gemm_scale(CB_), flag, seen, smem);   \
+        chain_down_body<gemm_cb(CB_), K2_>(c, T, rows_sh, nrows, yb, s, gemm_scale(CB_), seen, smem);         \
         break;
         ESP_CASES(ESP_CHAIN_CASE)
 #undef ESP_CHAIN_CASE
         default: {                          // no kernel for the expert's table entry: NaN partials, as grouped's
-            chain_wait(flag, 1, seen, nyd);
+            chain_take_xd(const_cast<uint16_t*>(a.X0), a.K, s * 128, rows_sh, nrows, nullptr, 0, seen, nyd);
             if (threadIdx.x == 0) raise_status(supported(cb, k2) ? ESP_STATUS_WIDTH_RANGE : ESP_STATUS_NO_KERNEL);
             const int wave = threadIdx.x >> 6, l32 = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
             const float qn = __builtin_nanf("");
@@ -1558,22 +1568,90 @@ __device__ __forceinline__ void chain_down(const ChainArgs& c, int local, unsign
             break;
         }
     }
-    // every partial of the program stored: count block yb arrived
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(c.dn_done + (size_t)yb * CNT_STRIDE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// down_combine_unit's arithmetic for (row r, block yb) with every valid slot's SK partials loaded device-coherently
+// until the down programs have stored them (no word all-ones), then put back to the sentinel
 template <int OUT_DTYPE>
 __device__ __forceinline__ void chain_combine(const ChainArgs& c, int local, unsigned char* smem) {
-    const int nyd = c.dn.N >> 7;
-    const int r = local / nyd, yb = local % nyd;
-    const int cnt = c.dn.ucount[0];
-    chain_wait(c.dn_done + (size_t)yb * CNT_STRIDE, cnt * c.dn.SK, c.dn_seen + (size_t)yb * CNT_STRIDE, c.R);
-    down_combine_unit<OUT_DTYPE, true>(c.dn.Z, c.pick, c.svh_d, c.y, c.wts, c.out, c.out_shared, c.dn.P, c.dn.N,
-                                       c.dn.SK, c.E, c.dn.slots, c.n_routed, r, yb,
-                                       reinterpret_cast<float (*)[128]>(smem));
+    const GroupedArgs& a = c.dn;
+    const int D = a.N, P = a.P, SK = a.SK, slots = a.slots;
+    const int nyd = D >> 7;
+    const int r = local / nyd, blk = local % nyd;
+    float (*part)[128] = reinterpret_cast<float (*)[128]>(smem);
+    const int l32 = threadIdx.x & 31, hw = threadIdx.x >> 5, nhw = (int)(blockDim.x >> 5);
+    const int n0 = blk * 128;
+    __shared__ float wts_sh[32];
+    if ((int)threadIdx.x < slots) wts_sh[threadIdx.x] = c.wts[r * slots + threadIdx.x];
+    const DevBuf zb(a.Z);
+    const uint32_t empty = 0xFFFFFFFFu;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int k = hw; k < slots; k += nhw) {
+        const int p = r * slots + k;
+        const int n = n0 + 4 * l32;
+        const int e = c.pick[p];
+        float o[4];
+        if (e >= 0 && e < c.E) {
+            float* zp = a.Z + (size_t)p * D + n;
+            float4 u[CHAIN_MAX_SPLITS];
+#pragma unroll
+            for (int q = 0; q < CHAIN_MAX_SPLITS; ++q)
+                if (q < SK) u[q] = zb.load4(zp + (size_t)q * P * D);
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < CHAIN_MAX_SPLITS; ++q)
+                if (q < SK) {
+                    auto pending = [&](const float4& t) {
+                        return __float_as_uint(t.x) == empty || __float_as_uint(t.y) == empty ||
+                               __float_as_uint(t.z) == empty || __float_as_uint(t.w) == empty;
+                    };
+                    while (pending(u[q])) {
+                        __builtin_amdgcn_s_sleep(1);
+                        if (chain_late(t0)) {
+                            raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                            break;
+                        }
+                        u[q] = zb.load4(zp + (size_t)q * P * D);
+                    }
+                    if (q == 0) {                            // split 0 starts the sum, the others follow in order
+                        v[0] = u[0].x; v[1] = u[0].y; v[2] = u[0].z; v[3] = u[0].w;
+                    } else {
+                        v[0] += u[q].x; v[1] += u[q].y; v[2] += u[q].z; v[3] += u[q].w;
+                    }
+                }
+            const float4 e4 = make_float4(__uint_as_float(empty), __uint_as_float(empty), __uint_as_float(empty),
+                                          __uint_as_float(empty));
+#pragma unroll
+            for (int q = 0; q < CHAIN_MAX_SPLITS; ++q)
+                if (q < SK) zb.store4(zp + (size_t)q * P * D, e4);
+            float sv[4];
+            load4_f16(c.svh_d + (size_t)e * D + n, sv);
+            fwht128(v, l32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = v[j] * HAD_SCALE * sv[j];
+            if (c.y != nullptr) *reinterpret_cast<float4*>(c.y + (size_t)p * D + n) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = c.y != nullptr ? c.y[(size_t)p * D + n + j] : 0.f;   // reuses y's row
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[k][4 * l32 + j] = o[j];
+    }
+    __syncthreads();
+    const int col = threadIdx.x & 127;
+    const size_t at = (size_t)r * D + n0 + col;
+    if (threadIdx.x < 128) {
+        float acc = 0.f;
+        for (int q = 0; q < c.n_routed; ++q) acc = fmaf(wts_sh[q], part[q][col], acc);
+        if constexpr (OUT_DTYPE == F32) static_cast<float*>(c.out)[at] = acc;
+        else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(c.out)[at] = f2bf(acc);
+        else static_cast<uint16_t*>(c.out)[at] = f2h(acc);
+    } else if (threadIdx.x < 256 && c.out_shared != nullptr && c.n_routed < slots) {
+        const float v = wts_sh[c.n_routed] * part[c.n_routed][col];
+        if constexpr (OUT_DTYPE == F32) static_cast<float*>(c.out_shared)[at] = v;
+        else if constexpr (OUT_DTYPE == BF16) static_cast<uint16_t*>(c.out_shared)[at] = f2bf(v);
+        else static_cast<uint16_t*>(c.out_shared)[at] = f2h(v);
+    }
 }
 
 template <int OUT_DTYPE>
@@ -2161,6 +2239,7 @@ extern "C" int esp_moe_chain(const void* x, int x_dtype, int64_t x_stride, const
     ESP_REQUIRE((((uintptr_t)Zd | (uintptr_t)y) & 15) == 0 && ((uintptr_t)xd & 7) == 0 && ((uintptr_t)svh_d & 7) == 0,
                 "moe_chain: Zd and y 16-byte aligned, xd and svh_d 8-byte aligned");
     const int64_t SKd = I / 128;                         // a down split a gate/up column block
+    ESP_REQUIRE(SKd <= CHAIN_MAX_SPLITS, "moe_chain: I at most 1024 (8 down splits of 128)");
     ESP_REQUIRE(zd_numel >= SKd * P * D, "moe_chain: Zd needs I / 128 * P * D floats");
     ESP_REQUIRE(SKd * P * D <= (int64_t(1) << 30), "moe_chain: the down partials must fit in 4 GiB");
     const int64_t nb_gu = I / 128, nyd = D / 128;
@@ -2170,10 +2249,8 @@ extern "C" int esp_moe_chain(const void* x, int x_dtype, int64_t x_stride, const
     if (nexp_max <= 0) return esp_host::ok();
     ChainArgs c{};
     c.gu = gu;
-    c.gu.xd_ready = flags;
-    c.xd_seen = flags + nexp_max * nb_gu * CNT_STRIDE;
-    c.dn_done = flags + 2 * nexp_max * nb_gu * CNT_STRIDE;
-    c.dn_seen = c.dn_done + nyd * CNT_STRIDE;
+    c.gu.chain = 1;
+    c.xd_seen = flags;                                   // the first nexp_max * I / 128 lines: xd's reader counts
     GroupedArgs& dn = c.dn;
     dn.mt = 1;
     dn.X0 = dn.X1 = static_cast<const uint16_t*>(xd);

@@ -234,12 +234,15 @@ class Scratch:
             "members": ((maxu * rows,), i32, -1),                     # their member rows, -1 padded
             # esp_moe_gateup's arrival counters, one a (expert, 128 columns) on its own 128-byte line
             "counters": ((maxu * (I // 128) * 32,), i32, 0),
-            # esp_moe_chain: the down partials (apart from the gate/up ones) and its hand-off flags (zero between uses)
-            "zd": ((P * D * (I // 128),), f32, 0),
+            # esp_moe_chain: its reader counts (zero between uses)
             "flags": ((2 * (maxu * (I // 128) + D // 128) * 32,), i32, 0),
         }
         for name, (shape, dtype, fill) in layout.items():
             setattr(self, name, torch.full(shape, fill, dtype=dtype, device=device))
+        # esp_moe_chain's own hand-off buffers, xd and the down partials: every bit set between uses (the launch reads
+        # a piece once no word of it is all-ones, then puts the all-ones back)
+        self.xdc = torch.full((P, I), -1, dtype=torch.int16, device=device).view(f16)
+        self.zd = torch.full((P * D * (I // 128),), -1, dtype=i32, device=device).view(f32)
 
     def window(self, R: int):
         """(ids, members [maxu, R]) views for a window of R tokens."""
@@ -354,10 +357,10 @@ def routed2(x: torch.Tensor, pick: torch.Tensor | None, wts: torch.Tensor | None
         out_shared = torch.empty((R, L.D), dtype=x.dtype, device=x.device)
     shared_out = out_shared if has_shared else None
     sk_gu, sk_d = s.cfg_gu[2], s.cfg_d[2]
-    if CHAIN and FUSED and R <= CHAIN_ROWS and (L.D // sk_gu) % 128 == 0 and sk_d * 128 == L.I:
+    if CHAIN and FUSED and R <= CHAIN_ROWS and (L.D // sk_gu) % 128 == 0 and sk_d * 128 == L.I and L.I <= 1024:
         (tg, tu, td), (bg, bu, bd), (cg, cu, cd) = L.ptr, L.k2, L.cb
         e.moe_chain(x, x.stride(0), L.suh_g, L.suh_u, tg, tu, td, bg, bu, bd, cg, cu, cd, ids, s.count, members,
-                    pick_p, wts_p, L.svh_g, L.svh_u, L.suh_d, L.svh_d, s.xd, s.z, s.zd, s.y, out, shared_out,
+                    pick_p, wts_p, L.svh_g, L.svh_u, L.suh_d, L.svh_d, s.xdc, s.z, s.zd, s.y, out, shared_out,
                     s.counters, s.flags, L.D, L.I, sk_gu, slots, L.E, k, *L.k2_gu, *L.k2_d, math.inf, ACT_F32)
         return out, shared_out
     _gate_up(e, x, L, s, R, P, slots, pick_p, ids, members)
