@@ -235,7 +235,8 @@ def bench_moe(dev, steps: int, layers: int = 8, passes: int = 16, rows=(1, 4, 32
                        "pct_peak": round(100 * gbs / PEAK_GBS, 1), "picked_bytes_per_replay": nbytes}
         log(f"moe T={T}: {us:.2f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak), "
             f"{nbytes / 2**30:.2f} GiB of picked experts a replay")
-    # the router alone (config 3): its 1 MiB bf16 weight a layer stays in the MALL (8 layers), so this is warm
+    # the router alone (config 3): its 1 MiB bf16 weight a layer stays in the MALL (8 layers), so this is warm; then
+    # cold, over 1024 distinct routers
     rt = {}
     for T in (1, 32):
         xg = torch.Generator(device=dev).manual_seed(70 + T)
@@ -248,7 +249,21 @@ def bench_moe(dev, steps: int, layers: int = 8, passes: int = 16, rows=(1, 4, 32
         ms = time_graph(graph_of(fr), steps)
         rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2), "weights": "MALL-warm"}
         log(f"route_group T={T}: {ms * 1000 / len(stack):.2f} us")
-    del stack
+    # and cold: one call on each of 1024 distinct 1 MiB router weights (1 GiB a replay, past the 256 MB MALL)
+    L0 = stack[0][0]
+    routers = [(torch.randn((256, 2048), generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(1024)]
+    for T in (1, 32):
+        xg = torch.Generator(device=dev).manual_seed(90 + T)
+        x = torch.randn((T, 2048), generator=xg, device=dev).to(torch.bfloat16)
+        s = G.scratch(L0, 32, 9, dev)
+
+        def fc():
+            for r in routers:
+                G.route(x, r, 8, L0, s)
+        ms = time_graph(graph_of(fc), max(3, steps // 2))
+        rt[str(T)]["cold_us_per_call"] = round(ms * 1000 / len(routers), 2)
+        log(f"route_group T={T}, cold router weights: {ms * 1000 / len(routers):.2f} us")
+    del stack, routers
     torch.cuda.empty_cache()
     return res, rt
 
