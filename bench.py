@@ -692,7 +692,7 @@ def sweep(dev, force_cb: int = -1) -> dict:
     """Cold sweeps on the BASELINE shapes, each candidate timed as a graph over >= 1 GiB of distinct weights (so
     nothing is served from the 256 MB MALL):
       * dense decode plan (dense.plan): config 2's four launches at 1 and 32 rows, every K split SK (uneven splits
-        allowed) and 4 / 8 / 16 waves a workgroup;
+        allowed) and 4 / 8 / 16 waves a workgroup; the LM head (2048 x 151936, 6-bit mcg) at one row, 1-4 splits;
       * prompt K splits (dense.tile_plan): the same launches as prompt launches over 128, 512 and 2048 rows;
       * grouped tile config (experts.tile_config): the config-4 MoE layer (8 cold 256-expert layers, fused routing)
         at 1, 4 and 32 tokens, gate/up and down each at 4 / 8 waves and every power-of-two K split. force_cb >= 0
@@ -734,6 +734,29 @@ def sweep(dev, force_cb: int = -1) -> dict:
                                                 "best": [list(r) for r in res[:6]]}
             log(f"sweep dense plan {nm} M={M}: rule {rule} {t_rule} us; best " +
                 ", ".join(f"{t}({sk},{w})" for t, sk, w in res[:6]))
+    # the LM head (2048 x 151936, 6-bit mcg) at one row: 4 cold copies (934 MB)
+    from vllm_espalier import workloads as WL
+    hgen = torch.Generator(device=dev).manual_seed(3)
+    heads = [D.Dense([WL.matrix(2048, 151936, 6, "mcg", hgen, dev)]) for _ in range(4)]
+    hx = torch.randn((1, 2048), device=dev).to(torch.bfloat16)
+    hy = torch.empty((1, 151936), dtype=torch.bfloat16, device=dev)
+    keep = heads[0].plans
+    res = []
+    for sk in (1, 2, 3, 4):
+        for w in (4, 8, 16):
+            for h in heads:
+                h.plans = [(sk, w, 2)]
+            D.scratch(dev, sk * D.MAX_ROWS * 151936, 0)
+            g = graph_of(lambda: [h.forward(hx, out=hy) for h in heads])
+            res.append((round(time_graph(g, 5, 1) * 1000 / len(heads), 2), sk, w))
+            del g
+    res.sort()
+    rule = tuple(keep[0][:2])
+    t_rule = next(t for t, sk, w in res if (sk, w) == rule)
+    out["dense_plan"]["LM head, M=1"] = {"rule": list(rule), "rule_us": t_rule, "best": [list(r) for r in res[:6]]}
+    log(f"sweep dense plan LM head M=1: rule {rule} {t_rule} us; best " +
+        ", ".join(f"{t}({sk},{w})" for t, sk, w in res[:6]))
+    del heads
     for T in (128, 512, 2048):
         for i, nm in enumerate(names):
             ds = [blk[i] for blk in stack[:8]]
