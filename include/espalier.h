@@ -33,7 +33,8 @@ extern "C" {
 /* Bits of the device status word (esp_status). */
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
-#define ESP_STATUS_WAIT_TIMEOUT 4 /* a chained launch (dense_multi, moe_chain) gave up waiting for a producer (~20 ms) */
+#define ESP_STATUS_WAIT_TIMEOUT 4 /* a launch gave up waiting (~20 ms): a chained launch (dense_multi, moe_chain) for a
+                                     producer, or a prompt launch (dense_tile) for the other K splits of a tile */
 #define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table),
                                    * or esp_grouped_list's grid (sized from its P and maxm) is shorter than the list */
 
@@ -84,7 +85,9 @@ int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K
  * matrix, in MFMA fragment order), and with SK > 1, Z fp32 (z_numel >= ceil(T / 128) * SK * 128 * sum(n_cols), at most
  * 2^30 floats) and counters int32 (counters_numel >= 32 * ceil(T / 128) * sum(n_cols) / 128; zero on entry and left
  * zero). A row's bits depend on its own input and SK only: the same for any T and any place in the prompt, but not
- * those of esp_dense (another order of the sums). Alignment as esp_dense, xh and Z 16-byte aligned. */
+ * those of esp_dense (another order of the sums). When every workgroup of the launch fits on the device at once, each
+ * K split finishes a share of its tile's rows after all splits have arrived (the same sums in the same order; a wait
+ * past ~20 ms sets ESP_STATUS_WAIT_TIMEOUT). Alignment as esp_dense, xh and Z 16-byte aligned. */
 int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
                    const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
                    const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,

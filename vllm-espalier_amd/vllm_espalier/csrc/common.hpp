@@ -262,7 +262,8 @@ const char* last_error();
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();
 int launch_check(const char* what);
-int dense_status(int clear, hipStream_t st, int* out);     // dense.hip: the dense launches' status word
+int dense_status(int clear, hipStream_t st, int* out);     // dense_multi.hip: the dense launches' status word
+int tile_status(int clear, hipStream_t st, int* out);      // dense_tile.hip: the prompt launches' status word
 }  // namespace esp_host
 
 #define ESP_REQUIRE(cond, ...)                                                                  \

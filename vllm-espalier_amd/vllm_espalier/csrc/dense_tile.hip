@@ -64,6 +64,10 @@ __device__ __forceinline__ void tile_phase_info(int finisher, int nst) {
 #define TILE_NOW() 0ull
 #endif
 
+// Device status of the prompt launches: ESP_STATUS_WAIT_TIMEOUT when a spread finish gave up waiting (read and cleared
+// by esp_status through tile_status)
+__device__ int g_tile_status;
+
 struct TileArgs {
     Shard s[MAX_SHARDS];
     int n;
@@ -73,7 +77,33 @@ struct TileArgs {
     float* Z;                // [row tiles][SK][128][NBT * 128]
     int* counters;           // [row tiles][NBT][CNT_STRIDE]
     int T, K, SK, NBT, SQ, SR, RG;
+    int spread;              // every workgroup of the launch resident at once: each split finishes a share of the rows
 };
+
+// Every split of a (row tile, column block) waits here until all `total` have stored their partials: thread 0 counts
+// its arrival, spins on the count (bounded: ~20 ms of s_memrealtime, then ESP_STATUS_WAIT_TIMEOUT and on), then counts
+// itself past on *seen; the last one past resets both to zero.
+__device__ __forceinline__ void tile_all_arrived(int* counter, int* seen, int total) {
+    __builtin_amdgcn_s_waitcnt(0);          // this wave's device-scope partial stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();          // 100 MHz
+        while (load_dev(counter) < total) {
+            __builtin_amdgcn_s_sleep(1);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
+                __hip_atomic_fetch_or(&g_tile_status, ESP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        if (__hip_atomic_fetch_add(seen, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
+            store_dev(counter, 0);
+            store_dev(seen, 0);
+        }
+    }
+    __syncthreads();
+}
 
 // xh of tile_rot_kernel: a workgroup takes one matrix, one row group of 16 rows and one 128-chunk of K, which fill
 // exactly the 4 (row group, step) A blocks of that chunk: a 32-lane half rotates 2 rows (rows past T are zero) into
@@ -132,6 +162,46 @@ __device__ __forceinline__ void tile_finish_rows(const DevBuf& zb, const float* 
         for (int i = 0; i < RPB; ++i) {
             const int r = rbase + (i0 + i) * RSTEP;
             if (r < Mt) {
+                const float4 mine = *reinterpret_cast<const float4*>(own + r * RED_STRIDE + 4 * l32);
+                float4 s = split == 0 ? mine : u[i][0];
+#pragma unroll
+                for (int q = 1; q <= OM; ++q)
+                    if (q < SK) {
+                        const float4 t = q == split ? mine : q < split ? u[i][q < OM ? q : OM - 1] : u[i][q - 1];
+                        s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+                    }
+                float v[4] = {s.x, s.y, s.z, s.w};
+                finish(v, l32, sv, scale);
+                store4(y, y_dtype, ybase + (size_t)r * y_stride, v);
+            }
+        }
+    }
+}
+
+// A split's share [lo, hi) of the tile's rows after every split arrived: each row's partials added in split order, its
+// own split's from shared memory (own: the block's [128][RED_STRIDE] sums), RPB rows of a half-wave with all their
+// other splits' loads (OM >= SK - 1) in flight; a row past hi reads a row of Z's 128 (not used), so no load branches
+template <int RPB, int OM>
+__device__ __forceinline__ void tile_finish_share(const DevBuf& zb, const float* zp0, size_t zrow, size_t zsplit,
+                                                  const float* own, int lo, int hi, int SK, int split, int rbase,
+                                                  int l32, uint2 sv, float scale, void* y, int y_dtype, size_t ybase,
+                                                  int y_stride) {
+    constexpr int RSTEP = 2 * TILE_WAVES;
+    for (int r0 = lo + rbase; r0 < hi; r0 += RPB * RSTEP) {
+        float4 u[RPB][OM];
+#pragma unroll
+        for (int i = 0; i < RPB; ++i) {
+            const int r = r0 + i * RSTEP < TILE_ROWS ? r0 + i * RSTEP : TILE_ROWS - 1;
+#pragma unroll
+            for (int o = 0; o < OM; ++o) {
+                const int q = o >= SK - 1 ? 0 : o < split ? o : o + 1;    // the o-th split other than its own
+                u[i][o] = zb.load4(zp0 + r * zrow + q * zsplit);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPB; ++i) {
+            const int r = r0 + i * RSTEP;
+            if (r < hi) {
                 const float4 mine = *reinterpret_cast<const float4*>(own + r * RED_STRIDE + 4 * l32);
                 float4 s = split == 0 ? mine : u[i][0];
 #pragma unroll
@@ -316,6 +386,22 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         zb.store4(Zt + split * zsplit + r * zrow + nbg * 128 + 4 * l32,
                   *reinterpret_cast<const float4*>(red + r * RED_STRIDE + 4 * l32));
     int* const cnt_p = a.counters + ((size_t)mt * a.NBT + nbg) * CNT_STRIDE;
+    if (a.spread) {
+        // every split finishes a share of the rows once all have arrived (the sums and order of one finisher)
+        tile_all_arrived(cnt_p, cnt_p + 1, a.SK);
+        const int per = (Mt + a.SK - 1) / a.SK, lo = split * per, hi = lo + per < Mt ? lo + per : Mt;
+        const float* zp0 = Zt + nbg * 128 + 4 * l32;
+        if (a.SK <= 3)
+            tile_finish_share<4, 2>(zb, zp0, zrow, zsplit, red, lo, hi, a.SK, split, wave * 2 + half, l32, sv, scale,
+                                    a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+        else if (a.SK <= 5)
+            tile_finish_share<2, 4>(zb, zp0, zrow, zsplit, red, lo, hi, a.SK, split, wave * 2 + half, l32, sv, scale,
+                                    a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+        else if (a.SK <= 9)
+            tile_finish_share<1, 8>(zb, zp0, zrow, zsplit, red, lo, hi, a.SK, split, wave * 2 + half, l32, sv, scale,
+                                    a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+        return;
+    }
     const bool finisher = arrive_last(cnt_p, a.SK, last);
     TILE_PHASE(5);
     TILE_PHASE_INFO(finisher ? 1 : 0, nst);
@@ -359,11 +445,23 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
 }
 
 template <int KCB, int K2>
-static int launch_tile(const TileArgs& a, dim3 grid, size_t smem, hipStream_t st) {
+static int launch_tile(const TileArgs& a0, dim3 grid, size_t smem, hipStream_t st) {
     auto kern = dense_tile_kernel<KCB, K2>;
     if (smem > 64 * 1024 &&
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "dense_tile: cannot raise the shared memory limit to %zu bytes", smem);
+    TileArgs a = a0;
+    // the finish spread over the splits needs every workgroup resident at once (a split waits for the others of its
+    // tile and block): the CUs times the workgroups a CU holds for this kernel at this shared memory
+    if (a.SK > 1 && a.SK <= 9) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, TILE_WAVES * 64, smem) ==
+                hipSuccess &&
+            (long)grid.x * grid.y * grid.z <= (long)cus * per_cu)
+            a.spread = 1;
+    }
     kern<<<grid, TILE_WAVES * 64, smem, st>>>(a);
     return ESP_OK;
 }
@@ -388,6 +486,26 @@ extern "C" int esp_tile_phase_clear(void) {
     return esp_host::ok();
 }
 #endif
+
+namespace esp_host {
+// the prompt launches' device status word into *out (ORed), cleared if asked (esp_status)
+int tile_status(int clear, hipStream_t st, int* out) {
+    int v = 0;
+    if (hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(g_tile_status), sizeof(int), 0, hipMemcpyDeviceToHost, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(ESP_ERR_HIP, "status: cannot read the prompt launches' status word");
+    *out |= v;
+    if (clear && v) {
+        const int zero = 0;
+        if (hipMemcpyToSymbolAsync(HIP_SYMBOL(g_tile_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice, st) !=
+                hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return fail(ESP_ERR_HIP, "status: cannot clear the prompt launches' status word");
+    }
+    return ESP_OK;
+}
+}  // namespace esp_host
 
 extern "C" int esp_dense_tile(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, int64_t n_shards,
                               const void* const* trellis, const void* const* suh, const void* const* svh,
