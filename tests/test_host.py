@@ -58,21 +58,19 @@ def test_dense_splits_cover_k_and_fit_the_rotation_buffer(K):
 
 @pytest.mark.parametrize("K,N", SHAPES + [(2048, 512), (1024, 1024), (8192, 4096)])
 def test_prompt_plan_is_valid(K, N):
-    """The prompt launches' K splits: whole 4-step stages a split, K of 512 or less unsplit, and at 512 rows (four
-    128-row tiles) a grid past one workgroup a CU filled as far as whole splits go: one more split would pass the
-    two-a-CU 512."""
+    """The prompt launches' K splits: 1 to 8, splits of at least 128 k (one 4-step stage), and at 512 rows (four
+    128-row tiles) a grid within two workgroups a CU that one more split would pass (unless capped)."""
     sk = D.tile_plan(K, N)
-    assert 1 <= sk <= K // 128
-    if K <= 512:
-        assert sk == 1
+    assert 1 <= sk <= min(8, max(1, K // 128))
     per_split = 4 * (N // 128)
-    if per_split * sk > 256 and K > 512:
-        assert per_split * (sk + 1) > 512 or sk == K // 128
+    assert per_split * sk <= 512 or sk == 1
+    assert per_split * (sk + 1) > 512 or sk in (8, K // 128)
 
 
 def test_prompt_plan_config2():
-    """config 2's launches: qkv 3 splits (480 workgroups at 512 rows), o 4, shared gate/up 8, shared down 1."""
-    assert [D.tile_plan(K, N) for K, N in ((2048, 5120), (4096, 2048), (2048, 1024), (512, 2048))] == [3, 4, 8, 1]
+    """config 2's launches: qkv 3 splits (480 workgroups at 512 rows), o 8 (512), shared gate/up 8 (256), shared
+    down 4 (256, its K of 512 in splits of 128)."""
+    assert [D.tile_plan(K, N) for K, N in ((2048, 5120), (4096, 2048), (2048, 1024), (512, 2048))] == [3, 8, 8, 4]
 
 
 def test_dense_plan_depends_on_shape_only(monkeypatch):

@@ -54,22 +54,18 @@ def plan(K: int, N: int, sms: int) -> tuple[int, int, int]:
 
 def tile_plan(K: int, N: int) -> int:
     """K splits of a prompt launch (esp_dense_tile) of a K -> N layer, from its shape alone (so a row's bits never
-    depend on the prompt's length). Enough splits that a 512-row prompt (4 tiles of 128 rows) has ~256 workgroups,
-    SK = ceil(64 / blocks), with at least one 4-step stage a split. Two corrections, both measured on config 2's
-    block: a grid between 256 and 512 workgroups at 512 rows (some CUs running two, the rest one) is raised to fill
-    both of every CU's slots (qkv: 2 -> 3 splits, 53 -> 46 us at 512 rows, 36 -> 31 us at 128); and a K of 512 or
-    less is not split, since its splits' hand-off costs more than they parallelise (down: 22 -> 20 us at 512 rows,
-    43 -> 25 us at 2048). ESPALIER_DENSE_PROMPT_SK forces."""
+    depend on the prompt's length): the most splits that keep a 512-row prompt (4 tiles of 128 rows) within two 8-wave
+    workgroups a CU, 4 * blocks * SK <= 512, so the grid stays resident and the split-K finish is spread over the
+    splits; at most 8 (the spread finish's batch of partial loads) and splits of at least 128 k. From a sweep of every
+    launch's SK at 128 / 512 / 2048 rows with the spread finish (config 2: qkv 3, o 8, shared gate/up 8, shared down 4,
+    the fastest at 512 and 128 rows: o 35.7 -> 31.8 us and shared down 20.9 -> 17.4 us at 512 rows against the earlier
+    4 and 1). At 2048 rows, where the grid is not resident and one split finishes each tile, fewer splits would be
+    faster (o 81 us at 2 against 109 at 8). ESPALIER_DENSE_PROMPT_SK forces."""
     forced = env("ESPALIER_DENSE_PROMPT_SK")
     if forced:
         return int(forced)
-    if K <= 512:
-        return 1
     blocks = N // 128
-    sk = max(1, min(-(-64 // blocks), K // 128))
-    if 256 < 4 * blocks * sk < 512:
-        sk = min(512 // (4 * blocks), K // 128)
-    return sk
+    return max(1, min(128 // blocks, 8, K // 128))
 
 
 TILE_ROWS = 128              # rows a prompt-launch workgroup
