@@ -103,6 +103,27 @@ def test_tile_rows_alone_equal_prompt(dev, name):
         assert torch.equal(y1.view(torch.int16), y[r:r + 1].view(torch.int16)), r
 
 
+@pytest.mark.parametrize("name", ["qkv", "o"])
+def test_tile_long_prompt(dev, ext, name):
+    """A 2049-row prompt (17 row tiles: a grid past what the device holds at once, so the splits of a tile finish it
+    together while later tiles wait to be dispatched): rows alone equal their rows in the prompt, bit for bit, the
+    counters are left zero and no wait timed out."""
+    print(f"dense_tile long prompt {name}", flush=True)
+    assert int(ext.status(True)) == 0
+    mats = _mats(CONFIGS[name], 26, dev)
+    d = D.Dense(mats)
+    T = 2049
+    x = torch.randn((T, d.K), generator=torch.Generator().manual_seed(11)).to(torch.bfloat16).to(dev)
+    y = d.forward_tile(x).clone()
+    torch.cuda.synchronize()
+    assert int(ext.status(True)) == 0, "a split's wait timed out"
+    assert int(D.prompt_scratch(dev, 0, 0, 0)[2].abs().sum()) == 0, "counters left non-zero"
+    assert torch.isfinite(y.float()).all()
+    for r in (0, 127, 128, 1024, 2047, 2048):
+        y1 = d.forward_tile(x[r:r + 1])
+        assert torch.equal(y1.view(torch.int16), y[r:r + 1].view(torch.int16)), r
+
+
 @pytest.mark.parametrize("sk", [1, 2, 5, 16])
 def test_tile_k_splits(dev, ext, sk):
     """Any K split meets the bar (o: K 4096, 128 steps); counters come back zero after each."""

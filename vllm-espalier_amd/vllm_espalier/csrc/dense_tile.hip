@@ -451,15 +451,18 @@ static int launch_tile(const TileArgs& a0, dim3 grid, size_t smem, hipStream_t s
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "dense_tile: cannot raise the shared memory limit to %zu bytes", smem);
     TileArgs a = a0;
-    // the finish spread over the splits needs every workgroup resident at once (a split waits for the others of its
-    // tile and block): the CUs times the workgroups a CU holds for this kernel at this shared memory
+    // The finish spread over the splits: a split waits only for the other splits of its own (row tile, column block),
+    // and a row tile's workgroups are consecutive ids (grid.x * grid.y of them). Workgroups are dispatched in id order,
+    // so the lowest unfinished tile always has every workgroup dispatched (all lower ones are done) and finishes: it
+    // is enough that a tile's workgroups fit on the device with room to spare (half the resident workgroups, the CUs
+    // times what a CU holds of this kernel at this shared memory). The waits are bounded either way.
     if (a.SK > 1 && a.SK <= 9) {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, TILE_WAVES * 64, smem) ==
                 hipSuccess &&
-            (long)grid.x * grid.y * grid.z <= (long)cus * per_cu)
+            2L * grid.x * grid.y <= (long)cus * per_cu)
             a.spread = 1;
     }
     kern<<<grid, TILE_WAVES * 64, smem, st>>>(a);
