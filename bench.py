@@ -263,6 +263,20 @@ def bench_moe(dev, steps: int, layers: int = 8, passes: int = 16, rows=(1, 4, 32
         ms = time_graph(graph_of(fc), max(3, steps // 2))
         rt[str(T)]["cold_us_per_call"] = round(ms * 1000 / len(routers), 2)
         log(f"route_group T={T}, cold router weights: {ms * 1000 / len(routers):.2f} us")
+    # the decoder's routing launch at one token, route_group_rmsnorm: the residual add and RMSNorm inside, the logits
+    # an all-ones hand-off polled by the last workgroup (no arrival count), over the same 1024 cold routers
+    xg = torch.Generator(device=dev).manual_seed(95)
+    h, d1 = (torch.randn((1, 2048), generator=xg, device=dev).to(torch.bfloat16) for _ in range(2))
+    nw = (1 + 0.1 * torch.randn((2048,), generator=xg, device=dev)).to(torch.bfloat16)
+    h_out, a_out = torch.empty_like(h), torch.empty_like(h)
+    s = G.scratch(L0, 32, 9, dev)
+
+    def fn_norm():
+        for r in routers:
+            G.route_rmsnorm(h, d1, nw, 1e-6, h_out, a_out, r, 8, L0, s)
+    ms = time_graph(graph_of(fn_norm), max(3, steps // 2))
+    rt["1"]["rmsnorm_cold_us_per_call"] = round(ms * 1000 / len(routers), 2)
+    log(f"route_group_rmsnorm T=1, cold router weights: {ms * 1000 / len(routers):.2f} us")
     del stack, routers
     torch.cuda.empty_cache()
     return res, rt

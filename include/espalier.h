@@ -34,7 +34,8 @@ extern "C" {
 #define ESP_STATUS_NO_KERNEL 1    /* a grouped launch met an expert whose (codebook, K2) has no kernel */
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
 #define ESP_STATUS_WAIT_TIMEOUT 4 /* a launch gave up waiting (~20 ms): a chained launch (dense_multi, moe_chain) for a
-                                     producer, or a prompt launch (dense_tile) for the other K splits of a tile */
+                                     producer, a prompt launch (dense_tile) for the other K splits of a tile, or
+                                     route_group_rmsnorm at one row for the other workgroups' logits */
 #define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table),
                                    * or esp_grouped_list's grid (sized from its P and maxm) is shorter than the list */
 
@@ -247,7 +248,10 @@ int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, const void*
 
 /* esp_route_group with the router input normalised in the launch: x = RMSNorm(h + d1) * norm_w, bit-identical to
  * esp_add_rmsnorm followed by esp_route_group; x is stored to a_out and the residual h + d1 to h_out. No counterpart in
- * the reference. R <= 4, H <= 8192, rows x_stride apart, 16-byte aligned. */
+ * the reference. R <= 4, H <= 8192, rows x_stride apart, 16-byte aligned. Unlike esp_route_group's, logits is this
+ * launch's own hand-off buffer (no other launch may write it): every bit set (0xFF bytes) on entry, and left so. At one
+ * row the last workgroup reads the others' logits once none is all-ones (no arrival count; counter stays zero), with
+ * a bounded wait (~20 ms, then ESP_STATUS_WAIT_TIMEOUT). */
 int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, double eps, void* h_out, void* a_out,
                             int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
                             const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,

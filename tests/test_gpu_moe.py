@@ -210,6 +210,72 @@ def test_route_group_rows_alone_and_graph(dev, ext):
         assert torch.equal(bufs[2].view(R, 9), pick) and torch.equal(bufs[3].view(R, 9), wts), f"replay {i}"
 
 
+@pytest.mark.parametrize("R,E,shared", [(1, 256, True), (1, 256, False), (1, 100, True), (2, 256, True),
+                                         (4, 256, True)])
+def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared):
+    """route_group_rmsnorm (the norm inside the routing launch; its logits an all-ones hand-off buffer, which at one
+    row the last workgroup polls instead of counting arrivals) against add_rmsnorm then route_group: the normalised
+    rows, the residual, picks, weights and grouping bit for bit; the logits left all-ones and the counter zero, over
+    two launches in a row and graph replays (each reading the all-ones the previous one left)."""
+    print(f"route_group_rmsnorm R={R} E={E} shared={shared}", flush=True)
+    H, k, eps = 2048, 8, 1e-6
+    x, gate, sgate = router_inputs(R, 700 + R + E, E=E, near_ties=R >= 3)
+    gen = torch.Generator().manual_seed(710 + R + E)
+    h = x.to(dev)
+    d1 = (torch.randn((R, H), generator=gen) * 0.5).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=gen)).to(torch.bfloat16).to(dev)
+    sid = E if shared else -1
+    h_ref, a_ref = h.clone(), torch.empty_like(h)
+    ext.add_rmsnorm(h_ref, d1, None, w, a_ref, eps)
+    _, pick_r, wts_r, uids_r, count_r, members_r = run_route(ext, dev, a_ref, gate, sgate, k, sid)
+    cnt = int(count_r.item())
+    slots = k + shared
+    maxu = min(R * slots, E + shared)
+    logits = torch.full((R * (E + shared),), -1, dtype=torch.int32, device=dev).view(torch.float32)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    pick = torch.zeros(R * slots, dtype=torch.int32, device=dev)
+    wts = torch.zeros(R * slots, dtype=torch.float32, device=dev)
+    uids = torch.zeros(maxu, dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    members = torch.full((maxu, R), -7, dtype=torch.int32, device=dev)
+    h_out, a_out = torch.empty_like(h), torch.empty_like(h)
+    gd, sd = gate.to(dev), sgate.to(dev) if shared else None
+
+    def launch():
+        ext.route_group_rmsnorm(h, d1, w, eps, h_out, a_out, gd, sd, k, sid, logits, counter, pick, wts, uids, count,
+                                members)
+
+    def check(tag):
+        torch.cuda.synchronize()
+        assert torch.equal(a_out.view(torch.int16), a_ref.view(torch.int16)), tag
+        assert torch.equal(h_out.view(torch.int16), h_ref.view(torch.int16)), tag
+        assert torch.equal(pick.view(R, slots), pick_r) and torch.equal(wts.view(R, slots), wts_r), tag
+        assert int(count.item()) == cnt, tag
+        assert torch.equal(uids[:cnt], uids_r[:cnt]) and torch.equal(members[:cnt], members_r[:cnt]), tag
+        assert bool((logits.view(torch.int32) == -1).all()), f"{tag}: the logits must be left all-ones"
+        assert int(counter.item()) == 0, f"{tag}: the counter must be left zero"
+
+    def clear():
+        for t in (pick, wts, uids, count, h_out, a_out):
+            t.zero_()
+        members.fill_(-7)
+
+    ext.status(clear=True)
+    for i in range(2):
+        clear()
+        launch()
+        check(f"launch {i}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for i in range(3):
+        clear()
+        g.replay()
+        check(f"replay {i}")
+        torch.randn((64, 64), device=dev).sum()           # eager work between replays
+    assert ext.status() == 0
+
+
 def test_route_group_limits_raise(dev, ext):
     x, gate, sgate = router_inputs(2, 1, near_ties=False)
     with pytest.raises(RuntimeError, match="shape limits"):

@@ -5,6 +5,8 @@
 // Grouping: distinct picks in id order, each with its member rows (code row * 32 + slot) in pick order, -1 padded.
 // When every expert appears at most once a row (top-k picks are distinct) and R <= 32, a row bitmask per expert gives
 // each member's rank as a popcount; otherwise each expert scans the picks in order.
+#include <type_traits>
+
 #include "common.hpp"
 #include "trellis.hpp"
 #include "gemm.hpp"
@@ -199,6 +201,14 @@ __device__ __forceinline__ uint16_t f64_to_bf16(double d) {
 // then 0xFFFF - id, so the wave maximum is the largest logit with the lowest id on ties), takes k maxima, the
 // softmax over the picks and the shared gate's sigmoid, and groups the picks.
 // ------------------------------------------------------------------------------------------------------------------
+// Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
+// they cannot run, which the host cannot check without reading the tables back. Read and cleared by esp_status.
+__device__ int g_status;
+
+__device__ __forceinline__ void raise_status(int bits) {
+    __hip_atomic_fetch_or(&g_status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct RouteArgs {
     const uint16_t* x;
     const uint16_t* gate;
@@ -221,6 +231,9 @@ struct RouteArgs {
     uint16_t* na_out;
     float neps;
     int norm;
+    // logits hold all-ones between launches (esp_route_group_rmsnorm): at one row the last workgroup (dispatched after
+    // the others) polls them until no logit is all-ones, with no arrival count; every launch puts the all-ones back
+    int sentinel;
 };
 
 constexpr int RT = 1024;             // threads of a route workgroup
@@ -248,13 +261,33 @@ __device__ __forceinline__ float bf16_unorder(uint32_t k) {
 // plain loads; 1: device-coherent loads (the logits were stored by other workgroups of the same launch), a lane
 // holding experts lane + 64 q; 2: as 1, with one 16-byte load a lane of experts 4 lane + q (E == 256, lr 16-byte
 // aligned). Every load, the shared logit's too, is issued before any is used (one round trip).
-template <int LOAD>
+constexpr uint32_t ROUTE_EMPTY = 0xFFFFFFFFu;     // the all-ones sentinel of esp_route_group_rmsnorm's logits
+
+__device__ __forceinline__ bool route_late(uint64_t t0) {
+    return __builtin_amdgcn_s_memrealtime() - t0 > 2000000ull;       // ~20 ms at 100 MHz
+}
+
+template <int LOAD, bool POLL = false>
 __device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has, int lane, int& e_out, float& w_out,
                                          float& w_shared) {
     auto expert = [lane](int q) __attribute__((always_inline)) { return LOAD == 2 ? 4 * lane + q : lane + 64 * q; };
     float l4[4];
     if constexpr (LOAD == 2) {
-        const float4 v = DevBuf(lr).load4(lr + 4 * lane);
+        const DevBuf lb(lr);
+        float4 v = lb.load4(lr + 4 * lane);
+        if constexpr (POLL) {
+            // until the other workgroups' logits have landed: no word all-ones (bounded)
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            while (__float_as_uint(v.x) == ROUTE_EMPTY || __float_as_uint(v.y) == ROUTE_EMPTY ||
+                   __float_as_uint(v.z) == ROUTE_EMPTY || __float_as_uint(v.w) == ROUTE_EMPTY) {
+                __builtin_amdgcn_s_sleep(1);
+                if (route_late(t0)) {
+                    raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                    break;
+                }
+                v = lb.load4(lr + 4 * lane);
+            }
+        }
         l4[0] = v.x; l4[1] = v.y; l4[2] = v.z; l4[3] = v.w;
     } else {
 #pragma unroll
@@ -262,8 +295,32 @@ __device__ __forceinline__ void topk_row(const float* lr, int E, int k, bool has
             const int e = expert(q);
             l4[q] = e < E ? (LOAD ? load_dev(lr + e) : lr[e]) : 0.f;
         }
+        if constexpr (POLL) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                while (expert(q) < E && __float_as_uint(l4[q]) == ROUTE_EMPTY) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (route_late(t0)) {
+                        raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                        break;
+                    }
+                    l4[q] = load_dev(lr + expert(q));
+                }
+        }
     }
-    const float ls = has ? (LOAD ? load_dev(lr + E) : lr[E]) : 0.f;
+    float ls = has ? (LOAD ? load_dev(lr + E) : lr[E]) : 0.f;
+    if constexpr (POLL) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (has && __float_as_uint(ls) == ROUTE_EMPTY) {
+            __builtin_amdgcn_s_sleep(1);
+            if (route_late(t0)) {
+                raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                break;
+            }
+            ls = load_dev(lr + E);
+        }
+    }
     uint32_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -417,44 +474,62 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
             }
         }
     }
-    if (!arrive_last(counter, (int)gridDim.x, &last)) return;
-
     // one row (a decode step): wave 0 takes the top-k and groups its picks itself -- the ids are distinct (top-k picks and
     // the shared id), so a pick's place is the number of smaller ids and its member rank 0 -- with no shared-memory
     // round trip or barrier; the tables are group_wave's
-    if (R == 1 && a.uids != nullptr && slots <= 64) {
-        if (wave == 0) {
-            int e_mine;
-            float w_mine, w_shared;
-            if (a.E == 256 && ((uintptr_t)logits & 15) == 0)
-                topk_row<2>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
-            else
-                topk_row<1>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
-            int id = -1;
-            if (lane < a.k) {
-                pick_out[lane] = e_mine;
-                wts_out[lane] = w_mine;
-                id = e_mine;
+    const bool one_row = R == 1 && a.uids != nullptr && slots <= 64;
+    auto route_one = [&](auto poll) __attribute__((always_inline)) {
+        constexpr bool POLL = decltype(poll)::value;
+        int e_mine;
+        float w_mine, w_shared;
+        const bool wide = a.E == 256 && ((uintptr_t)logits & 15) == 0;
+        if (wide)
+            topk_row<2, POLL>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+        else
+            topk_row<1, POLL>(logits, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+        if constexpr (POLL) {
+            // the logits are read: the sentinel back for the next launch
+            const float e1 = __uint_as_float(ROUTE_EMPTY);
+            if (wide) {
+                DevBuf(logits).store4(logits + 4 * lane, make_float4(e1, e1, e1, e1));
+            } else {
+                for (int e = lane; e < a.E; e += 64) store_dev(logits + e, e1);
             }
-            if (has && lane == a.k) {
-                pick_out[a.k] = a.shared_id;
-                wts_out[a.k] = w_shared;
-                id = a.shared_id;
-            }
-            const bool valid = lane < slots && id >= 0 && id < C;
-            int place = 0;
-            for (int j = 0; j < slots; ++j) {
-                const int ej = __builtin_amdgcn_readlane(id, j);
-                place += ej >= 0 && ej < C && ej < id;
-            }
-            const uint64_t vm = __ballot(valid);
-            if (lane == 0) *a.ucount = __builtin_popcountll(vm);
-            if (valid) {
-                a.uids[place] = id;
-                a.members[(size_t)place * a.maxm] = lane;                        // row 0, slot lane
-                for (int m = 1; m < a.maxm; ++m) a.members[(size_t)place * a.maxm + m] = -1;
-            }
+            if (has && lane == 0) store_dev(logits + a.E, e1);
         }
+        int id = -1;
+        if (lane < a.k) {
+            pick_out[lane] = e_mine;
+            wts_out[lane] = w_mine;
+            id = e_mine;
+        }
+        if (has && lane == a.k) {
+            pick_out[a.k] = a.shared_id;
+            wts_out[a.k] = w_shared;
+            id = a.shared_id;
+        }
+        const bool valid = lane < slots && id >= 0 && id < C;
+        int place = 0;
+        for (int j = 0; j < slots; ++j) {
+            const int ej = __builtin_amdgcn_readlane(id, j);
+            place += ej >= 0 && ej < C && ej < id;
+        }
+        const uint64_t vm = __ballot(valid);
+        if (lane == 0) *a.ucount = __builtin_popcountll(vm);
+        if (valid) {
+            a.uids[place] = id;
+            a.members[(size_t)place * a.maxm] = lane;                        // row 0, slot lane
+            for (int m = 1; m < a.maxm; ++m) a.members[(size_t)place * a.maxm + m] = -1;
+        }
+    };
+    if (a.sentinel && one_row) {
+        // no arrival count: the last workgroup, dispatched after every other, polls the logits themselves
+        if (blockIdx.x == gridDim.x - 1 && wave == 0) route_one(std::true_type{});
+        return;
+    }
+    if (!arrive_last(counter, (int)gridDim.x, &last)) return;
+    if (one_row) {
+        if (wave == 0) route_one(std::false_type{});
         if (tid == 0) store_dev(counter, 0);
         return;
     }
@@ -465,6 +540,8 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         int e_mine;
         float w_mine, w_shared;
         topk_row<1>(logits + (size_t)r * C, a.E, a.k, has, lane, e_mine, w_mine, w_shared);
+        if (a.sentinel)                                  // the row's logits read: the sentinel back
+            for (int e = lane; e < C; e += 64) store_dev(logits + (size_t)r * C + e, __uint_as_float(ROUTE_EMPTY));
         if (lane < a.k) {
             pick_out[r * slots + lane] = e_mine;
             wts_out[r * slots + lane] = w_mine;
@@ -701,14 +778,6 @@ struct GroupedArgs {
     int chain;                     // MODE 1 in the chained MoE launch: xd is stored device-coherently, 8 bytes a lane,
                                    // over the launch's all-ones sentinel, and read by the down programs of the launch
 };
-
-// Device status word of the library (one per GPU): bits the kernels set when a device-resident table names something
-// they cannot run, which the host cannot check without reading the tables back. Read and cleared by esp_status.
-__device__ int g_status;
-
-__device__ __forceinline__ void raise_status(int bits) {
-    __hip_atomic_fetch_or(&g_status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // The GEMM of one program. A rows: member m's row is abase + (by_member ? m : its slot row) * astride, holding k from
 // kbase, in shared memory (LDS) or global memory. dev: the partials go to Z with device-scope stores (another
@@ -1837,7 +1906,8 @@ struct RouteNorm {
 static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate, int64_t E,
                       const void* sgate, int64_t k, int64_t shared_id, float* logits, int64_t logits_numel,
                       int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu,
-                      int32_t* ucount, int32_t* members, int64_t maxm, const RouteNorm* nrm, void* stream) {
+                      int32_t* ucount, int32_t* members, int64_t maxm, const RouteNorm* nrm, void* stream,
+                      int sentinel = 0) {
     const int has = shared_id >= 0;
     ESP_REQUIRE(x && gate && logits && counter && pick_out && wts_out && uids && ucount && members,
                 "route_group: null pointer");
@@ -1873,6 +1943,7 @@ static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, i
     a.shared_id = (int)shared_id;
     a.maxm = (int)maxm;
     a.win = (int)R;
+    a.sentinel = sentinel;
     size_t smem = 0;
     if (nrm) {
         ESP_REQUIRE(nrm->h && nrm->w && nrm->h_out && nrm->a_out, "route_group_rmsnorm: null pointer");
@@ -1952,7 +2023,7 @@ extern "C" int esp_route_group_rmsnorm(const void* h, const void* d1, const void
                                        int32_t* members, int64_t maxm, void* stream) {
     const RouteNorm nrm{h, d1, norm_w, h_out, a_out, eps};
     return route_impl(h, x_dtype, x_stride, R, H, gate, E, sgate, k, shared_id, logits, logits_numel, counter,
-                      pick_out, wts_out, uids, maxu, ucount, members, maxm, &nrm, stream);
+                      pick_out, wts_out, uids, maxu, ucount, members, maxm, &nrm, stream, 1);
 }
 
 extern "C" int esp_group_shared(const int32_t* pick_in, const float* wts_in, const void* x, int x_dtype,

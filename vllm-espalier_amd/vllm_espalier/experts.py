@@ -243,6 +243,8 @@ class Scratch:
         # a piece once no word of it is all-ones, then puts the all-ones back)
         self.xdc = torch.full((P, I), -1, dtype=torch.int16, device=device).view(f16)
         self.zd = torch.full((P * D * (I // 128),), -1, dtype=i32, device=device).view(f32)
+        # esp_route_group_rmsnorm's logits (the shared gate's after each row's E): all-ones between uses
+        self.logits_n = torch.full((rows * (E + 1),), -1, dtype=i32, device=device).view(f32)
 
     def window(self, R: int):
         """(ids, members [maxu, R]) views for a window of R tokens."""
@@ -327,11 +329,12 @@ def route(x: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
 def route_rmsnorm(h: torch.Tensor, d1: torch.Tensor | None, norm_w: torch.Tensor, eps: float, h_out: torch.Tensor,
                   a_out: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
     """route() of a_out = RMSNorm(h + d1) * norm_w, the norm made inside the routing launch (bit-identical to
-    add_rmsnorm then route); stores a_out and the residual h + d1 to h_out. At most 4 rows."""
+    add_rmsnorm then route); stores a_out and the residual h + d1 to h_out. At most 4 rows. Its logits go through the
+    scratch's all-ones buffer (logits_n), which the launch leaves all-ones."""
     R = h.shape[0]
     ids, members = s.window(R)
     P = R * s.slots
-    ext().route_group_rmsnorm(h, d1, norm_w, eps, h_out, a_out, gate, L.gate_w, k, L.shared_id, s.logits,
+    ext().route_group_rmsnorm(h, d1, norm_w, eps, h_out, a_out, gate, L.gate_w, k, L.shared_id, s.logits_n,
                               s.route_counter, s.pick[:P], s.wts[:P], ids, s.count, members)
 
 
