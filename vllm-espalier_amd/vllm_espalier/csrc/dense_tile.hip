@@ -258,8 +258,10 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
     const int m0 = mt * TILE_ROWS, Mt = a.T - m0 < TILE_ROWS ? a.T - m0 : TILE_ROWS, rgt = (Mt + 15) >> 4;
     const int ksteps = a.K >> 5;
     const uint16_t* X = a.xh + (((size_t)si * a.RG + mt * TILE_RG) * ksteps + s0) * TILE_FRAG;
-    uint16_t* sa = reinterpret_cast<uint16_t*>(smem);
-    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + 2 * A_BUF * 2);
+    // the trellis stages first: their words are read at per-lane addresses plus constants, which fit the LDS reads'
+    // 16-bit immediate offsets only below 64 KiB (past it every read needs an address add)
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem);
+    uint16_t* sa = reinterpret_cast<uint16_t*>(smem + 2 * B_BUF * 4);
 
     // stage st of the split into buffer buf: the block's trellis tiles, then the tile's A blocks (rgt row groups x n
     // steps of 64 16-byte units; a wave's 64 units are one block, so its LDS destination is one contiguous KiB)
