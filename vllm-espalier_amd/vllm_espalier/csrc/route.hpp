@@ -87,7 +87,9 @@ __device__ __forceinline__ float bf16_unorder(uint32_t k) {
 // shared slot's sigmoid weight. Lane t < k returns pick t; every lane returns the shared weight (when has). LOAD 0:
 // plain loads; 1: device-coherent loads (the logits were stored by other workgroups of the same launch), a lane
 // holding experts lane + 64 q; 2: as 1, with one 16-byte load a lane of experts 4 lane + q (E == 256, lr 16-byte
-// aligned). Every load, the shared logit's too, is issued before any is used (one round trip).
+// aligned). Every load, the shared logit's too, is issued before any is used (one round trip). POLL: the logits
+// were stored over the all-ones sentinel; each is reloaded (bounded, ~20 ms) until it is not all-ones, and `late` is
+// set where a wait gave up (the caller raises its status bit).
 constexpr uint32_t ROUTE_EMPTY = 0xFFFFFFFFu;     // the all-ones sentinel of esp_route_group_rmsnorm's logits
 
 __device__ __forceinline__ bool route_late(uint64_t t0) {
