@@ -17,6 +17,12 @@ launches, with HIP events on the launch stream); and
 then fp32 Hadamards and torch.matmul), on a bounded sample of the same layer.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-moe] [--no-decoder]
+
+Comparing two builds (how changes are judged): `python bench.py --compare` times the workloads a change is decided
+on (the dense block at 1 and 32 rows, the MoE layer at 1 / 4 / 32 tokens, the decode step, the config-2 prompt block
+at 512 rows and the tile prefill) and prints one JSON line; `--package DIR` runs it (or any mode) on the package in
+DIR (a directory holding `vllm_espalier`, e.g. another checkout's `vllm-espalier_amd`, built there) instead of this
+repository's. Alternate the two builds in one session on one GPU: runs of one build agree to ~0.2 %, boxes ~1.5 %.
 """
 from __future__ import annotations
 
@@ -29,7 +35,10 @@ import time
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
-sys.path.insert(0, str(REPO / "vllm-espalier_amd"))
+PACKAGE_ROOT = REPO / "vllm-espalier_amd"
+if "--package" in sys.argv[:-1]:              # before any import of vllm_espalier (see --package)
+    PACKAGE_ROOT = Path(sys.argv[sys.argv.index("--package") + 1]).resolve()
+sys.path.insert(0, str(PACKAGE_ROOT))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E, public spec
 COLD_BYTES = 1 << 30         # distinct weight bytes a cold graph streams
@@ -923,6 +932,50 @@ def phase_table(res: dict) -> str:
     return "\n".join(lines)
 
 
+def compare(dev) -> dict:
+    """The workloads a change is decided on, timed as graphs of cold weights (the bench's own helpers): us a layer for
+    the dense block at 1 and 32 rows, the MoE layer at 1 / 4 / 32 tokens and the config-2 prompt block at 512 rows; us a
+    decode step; ms and tok/s of the 512-token tile prefill."""
+    import torch
+    from vllm_espalier import step as S
+    res = {}
+    stack = dense_stack(98, 11, dev)
+    for M in (1, 32):
+        g = run_dense(stack, M, dev)
+        res[f"dense_block_{M}_us"] = round(min(time_graph(g, 10, 2) for _ in range(2)) * 1000 / len(stack), 2)
+        del g
+    del stack
+    moe = bench_moe(dev, 10, rows=(1, 4, 32))[0]
+    for T, v in moe.items():
+        res[f"moe_layer_{T}_us"] = v["us_per_layer"]
+    stack = dense_stack(8, 11, dev)
+    g = run_dense_prompt(stack, 512, dev)
+    res["prompt_block_512_us"] = round(min(time_graph(g, 5, 1) for _ in range(2)) * 1000 / len(stack), 2)
+    del g, stack
+    dec = S.SyntheticDecoder(n_layers=40, seed=5, device=dev)
+    b = dec.buffers(1)
+    b.ids_in.fill_(1)
+    dec.forward(1)
+
+    def decode_step():
+        dec.forward(1)
+        b.ids_in.copy_(b.ids_out)
+    g = graph_of(decode_step)
+    res["decode_step_us"] = round(min(time_graph(g, 10, 3) for _ in range(3)) * 1000, 1)
+    del g
+    bp = dec.prefill_buffers(512)
+    bp.ids_in.copy_(torch.arange(512, dtype=torch.int32, device=dev))
+    dec.prefill(512)
+    torch.cuda.synchronize()
+    g = graph_of(lambda: dec.prefill(512))
+    ms = min(time_graph(g, 3, 1) for _ in range(2))
+    res["tile_prefill_512_ms"] = round(ms, 3)
+    res["tile_prefill_512_tok_per_s"] = round(512 / ms * 1000, 1)
+    for k, v in res.items():
+        log(f"compare {k}: {v}")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -948,6 +1001,9 @@ def main() -> int:
                     "experts.tile_config (one JSON line), and exit")
     ap.add_argument("--force-cb", type=int, default=-1, help="with --sweep: decode every expert with this kernel "
                     "codebook (same bytes, wrong values) to see the decode arithmetic's share")
+    ap.add_argument("--compare", action="store_true", help="time the workloads two builds are compared on (one "
+                    "JSON line), and exit")
+    ap.add_argument("--package", metavar="DIR", help="import vllm_espalier from DIR instead of this repository")
     a = ap.parse_args()
     if a.rocprof_summary:
         print(rocprof_summary(a.rocprof_summary))
@@ -973,6 +1029,12 @@ def main() -> int:
     G.ext()                                   # the HIP extension must be there: no fallback
     name = torch.cuda.get_device_name(dev)
     log(f"device {name}")
+    if a.compare:
+        import vllm_espalier
+        res = compare(dev)
+        print(json.dumps({"compare": res, "package": str(Path(vllm_espalier.__file__).parent), "device": name}),
+              flush=True)
+        return 0
     if a.traffic_probe:
         traffic_probe(dev)
         return 0
