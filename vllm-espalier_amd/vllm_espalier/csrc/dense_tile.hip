@@ -391,6 +391,7 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
     if (a.spread) {
         // every split finishes a share of the rows once all have arrived (the sums and order of one finisher)
         tile_all_arrived(cnt_p, cnt_p + 1, a.SK);
+        TILE_PHASE(5);
         const int per = (Mt + a.SK - 1) / a.SK, lo = split * per, hi = lo + per < Mt ? lo + per : Mt;
         const float* zp0 = Zt + nbg * 128 + 4 * l32;
         if (a.SK <= 3)
@@ -402,6 +403,9 @@ __global__ __launch_bounds__(TILE_WAVES * 64) void dense_tile_kernel(TileArgs a)
         else if (a.SK <= 9)
             tile_finish_share<1, 8>(zb, zp0, zrow, zsplit, red, lo, hi, a.SK, split, wave * 2 + half, l32, sv, scale,
                                     a.y, a.y_dtype, yrow0 + ycol, a.y_stride);
+        TILE_PHASE_DRAIN();
+        TILE_PHASE(6);
+        TILE_PHASE_INFO(1, nst);                          // every split finishes its share
         return;
     }
     const bool finisher = arrive_last(cnt_p, a.SK, last);
