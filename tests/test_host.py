@@ -203,3 +203,12 @@ def test_shared_scratch_keeps_outgrown_buffers_only_when_captured():
     assert len(s.retired) == 1 and s.retired[0] is b and c[0].numel() == 40
     assert dev not in s.captured                 # the new pair has not been captured yet
     del a
+
+
+def test_status_bits_match_the_header():
+    """experts.check_status names every ESP_STATUS_* bit of include/espalier.h, with the header's values."""
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parent.parent / "include" / "espalier.h").read_text()
+    bits = {int(v) for v in re.findall(r"^#define ESP_STATUS_\w+ (\d+)", text, re.M)}
+    assert bits == {b for b, _ in X.STATUS_BITS}

@@ -203,6 +203,23 @@ class Layer:
         return self.tables[2].k2_lo, self.tables[2].k2_hi
 
 
+# The bits of the device status word (include/espalier.h, ESP_STATUS_*)
+STATUS_BITS = ((1, "a grouped launch met an expert whose (codebook, K2) has no kernel"),
+               (2, "a grouped launch met an expert whose K2 lies outside the launch's range"),
+               (4, "a launch gave up waiting (~20 ms) for another part of the launch"),
+               (8, "a tile list held more member tiles than its bound, or a list launch's grid was shorter than it"))
+
+
+def check_status(clear: bool = True) -> None:
+    """Raise RuntimeError naming every bit set in the device status word (esp_status: what the kernels met in
+    device-resident tables or in-launch hand-offs, which the host cannot see without reading it back), clearing the
+    word first if asked. The read synchronises the current stream, so call it outside graph capture: after a prefill,
+    between decode steps, in tests."""
+    v = int(ext().status(clear))
+    if v:
+        raise RuntimeError(f"espalier device status {v:#x}: " + "; ".join(t for b, t in STATUS_BITS if v & b))
+
+
 def prepare(experts, shared=None, gate_w=None) -> Layer:
     """experts: [(gate, up, down) EspMatrix] in expert order; shared: the shared expert's (gate, up, down), appended as
     the last table entry, with gate_w its sigmoid-gate weight [D]. Each matrix's suh / svh become rows of the layer's
