@@ -210,20 +210,23 @@ def test_route_group_rows_alone_and_graph(dev, ext):
         assert torch.equal(bufs[2].view(R, 9), pick) and torch.equal(bufs[3].view(R, 9), wts), f"replay {i}"
 
 
-@pytest.mark.parametrize("R,E,shared", [(1, 256, True), (1, 256, False), (1, 100, True), (2, 256, True),
-                                         (4, 256, True)])
-def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared):
+@pytest.mark.parametrize("R,E,shared,dtype", [(1, 256, True, "bf16"), (1, 256, False, "bf16"), (1, 100, True, "bf16"),
+                                               (2, 256, True, "bf16"), (4, 256, True, "bf16"), (1, 256, True, "fp16"),
+                                               (3, 256, True, "fp16")])
+def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared, dtype):
     """route_group_rmsnorm (the norm inside the routing launch; its logits an all-ones hand-off buffer, which at one
     row the last workgroup polls instead of counting arrivals) against add_rmsnorm then route_group: the normalised
     rows, the residual, picks, weights and grouping bit for bit; the logits left all-ones and the counter zero, over
     two launches in a row and graph replays (each reading the all-ones the previous one left)."""
-    print(f"route_group_rmsnorm R={R} E={E} shared={shared}", flush=True)
+    print(f"route_group_rmsnorm R={R} E={E} shared={shared} {dtype}", flush=True)
     H, k, eps = 2048, 8, 1e-6
+    t = torch.bfloat16 if dtype == "bf16" else torch.float16
     x, gate, sgate = router_inputs(R, 700 + R + E, E=E, near_ties=R >= 3)
+    x, gate, sgate = x.to(t), gate.to(t), sgate.to(t)
     gen = torch.Generator().manual_seed(710 + R + E)
     h = x.to(dev)
-    d1 = (torch.randn((R, H), generator=gen) * 0.5).to(torch.bfloat16).to(dev)
-    w = (1 + 0.1 * torch.randn(H, generator=gen)).to(torch.bfloat16).to(dev)
+    d1 = (torch.randn((R, H), generator=gen) * 0.5).to(t).to(dev)
+    w = (1 + 0.1 * torch.randn(H, generator=gen)).to(t).to(dev)
     sid = E if shared else -1
     h_ref, a_ref = h.clone(), torch.empty_like(h)
     ext.add_rmsnorm(h_ref, d1, None, w, a_ref, eps)
