@@ -256,8 +256,20 @@ def bench_moe(dev, steps: int, layers: int = 8, passes: int = 16, rows=(1, 4, 32
             for (L, experts, shared, router), x in zip(stack, xs):
                 G.route(x, router, 8, L, s)
         ms = time_graph(graph_of(fr), steps)
-        rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2), "weights": "MALL-warm"}
+        rt[str(T)] = {"us_per_call": round(ms * 1000 / len(stack), 2), "weights": "MALL-warm",
+                      "entry": "esp_route_group_own (logits an all-ones hand-off buffer)"}
         log(f"route_group T={T}: {ms * 1000 / len(stack):.2f} us")
+        # the reference's contract (esp_route_group: logits plain scratch, arrivals counted)
+        plain = torch.zeros((T * 257,), dtype=torch.float32, device=dev)
+        ids, members = s.window(T)
+
+        def fp():
+            for (L, experts, shared, router), x in zip(stack, xs):
+                G.ext().route_group(x, router, L.gate_w, 8, L.shared_id, plain, s.route_counter, s.pick[:T * 9],
+                                    s.wts[:T * 9], ids, s.count, members)
+        ms = time_graph(graph_of(fp), steps)
+        rt[str(T)]["plain_logits_us_per_call"] = round(ms * 1000 / len(stack), 2)
+        log(f"route_group T={T}, plain logits (esp_route_group): {ms * 1000 / len(stack):.2f} us")
     # and cold: one call on each of 1024 distinct 1 MiB router weights (1 GiB a replay, past the 256 MB MALL)
     L0 = stack[0][0]
     routers = [(torch.randn((256, 2048), generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(1024)]

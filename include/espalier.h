@@ -106,6 +106,16 @@ int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int64_t R, int
                     int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount,
                     int32_t* members, int64_t maxm, void* stream);
 
+/* esp_route_group with its logits as the launch's own hand-off buffer, as esp_route_group_rmsnorm's: every bit of
+ * logits set (0xFF bytes) on entry, and left so; at one row the last workgroup reads the others' logits once none is
+ * all-ones instead of counting arrivals (the counter stays zero), with a bounded wait (~20 ms, then
+ * ESP_STATUS_WAIT_TIMEOUT). Bit-identical to esp_route_group. No counterpart in the reference (whose logits are plain
+ * scratch): for callers that own a logits buffer across calls. */
+int esp_route_group_own(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H, const void* gate,
+                        int64_t E, const void* sgate, int64_t k, int64_t shared_id, float* logits,
+                        int64_t logits_numel, int32_t* counter, int32_t* pick_out, float* wts_out, int32_t* uids,
+                        int64_t maxu, int32_t* ucount, int32_t* members, int64_t maxm, void* stream);
+
 /* esp_route_group's routing for any number of rows, without the grouping: the same logits, picks and weights (a row's
  * routing depends on that row alone; bf16 x bf16 products and their sums are exact in fp64 for ordinary data, so the
  * order of the sums does not show after the rounding), for a whole prompt in two launches: the logits on the fp64

@@ -279,6 +279,60 @@ def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared, dtype):
     assert ext.status() == 0
 
 
+@pytest.mark.parametrize("R,shared", [(1, True), (1, False), (3, True), (32, True)])
+def test_route_group_own_equals_route_group(dev, ext, R, shared):
+    """esp_route_group_own (route_group over its own all-ones logits buffer: polled by the last workgroup at one row,
+    restored by the top-k waves at more) against esp_route_group: picks, weights and grouping bit for bit, near-ties
+    included, over launches in a row and graph replays; the logits left all-ones and the counter zero."""
+    print(f"route_group_own R={R} shared={shared}", flush=True)
+    x, gate, sgate = router_inputs(R, 800 + R, near_ties=R >= 3)
+    k, E = 8, 256
+    sid = E if shared else -1
+    _, pick_r, wts_r, uids_r, count_r, members_r = run_route(ext, dev, x, gate, sgate, k, sid)
+    cnt = int(count_r.item())
+    slots, C = k + shared, E + shared
+    maxu = min(R * slots, C)
+    logits = torch.full((R * C,), -1, dtype=torch.int32, device=dev).view(torch.float32)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    pick = torch.zeros(R * slots, dtype=torch.int32, device=dev)
+    wts = torch.zeros(R * slots, dtype=torch.float32, device=dev)
+    uids = torch.zeros(maxu, dtype=torch.int32, device=dev)
+    count = torch.zeros(1, dtype=torch.int32, device=dev)
+    members = torch.full((maxu, R), -7, dtype=torch.int32, device=dev)
+    xd, gd, sd = x.to(dev), gate.to(dev), sgate.to(dev) if shared else None
+
+    def launch():
+        ext.route_group_own(xd, gd, sd, k, sid, logits, counter, pick, wts, uids, count, members)
+
+    def check(tag):
+        torch.cuda.synchronize()
+        assert torch.equal(pick.view(R, slots), pick_r) and torch.equal(wts.view(R, slots), wts_r), tag
+        assert int(count.item()) == cnt, tag
+        assert torch.equal(uids[:cnt], uids_r[:cnt]) and torch.equal(members[:cnt], members_r[:cnt]), tag
+        assert bool((logits.view(torch.int32) == -1).all()), f"{tag}: the logits must be left all-ones"
+        assert int(counter.item()) == 0, f"{tag}: the counter must be left zero"
+
+    def clear():
+        for t in (pick, wts, uids, count):
+            t.zero_()
+        members.fill_(-7)
+
+    ext.status(clear=True)
+    for i in range(2):
+        clear()
+        launch()
+        check(f"launch {i}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for i in range(3):
+        clear()
+        g.replay()
+        check(f"replay {i}")
+        torch.randn((64, 64), device=dev).sum()           # eager work between replays
+    assert ext.status() == 0
+
+
 def test_route_group_limits_raise(dev, ext):
     x, gate, sgate = router_inputs(2, 1, near_ties=False)
     with pytest.raises(RuntimeError, match="shape limits"):

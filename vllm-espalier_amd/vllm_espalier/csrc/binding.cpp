@@ -316,9 +316,10 @@ void dense_tile(const at::Tensor& x, const std::vector<at::Tensor>& T, const std
                         counters.numel(), k2, cb, SK, cur_stream()));
 }
 
-void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
-                 int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out, at::Tensor wts_out,
-                 at::Tensor uids, at::Tensor ucount, at::Tensor members) {
+// route_group's checks and call; own: over the caller's all-ones logits buffer (esp_route_group_own)
+static void route_group_impl(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate,
+                             int64_t k, int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out,
+                             at::Tensor wts_out, at::Tensor uids, at::Tensor ucount, at::Tensor members, bool own) {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1 && gate.is_contiguous(), "x / gate layout");
     TORCH_CHECK(gate.scalar_type() == x.scalar_type(), "gate and x must share a dtype");
     TORCH_CHECK(x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kHalf, "x: bf16/fp16");
@@ -338,11 +339,24 @@ void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optiona
     const int64_t slots = k + (shared_id >= 0);
     TORCH_CHECK(pick_out.numel() >= R * slots && wts_out.numel() >= R * slots, "pick / wts too small");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-    call(esp_route_group(x.data_ptr(), dtype_code(x), x.stride(0), R, H, gate.data_ptr(), E,
-                         sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits),
-                         logits.numel(), mptr<int32_t>(counter), mptr<int32_t>(pick_out), mptr<float>(wts_out),
-                         mptr<int32_t>(uids), uids.numel(), mptr<int32_t>(ucount), mptr<int32_t>(members),
-                         members.size(1), cur_stream()));
+    auto fn = own ? esp_route_group_own : esp_route_group;
+    call(fn(x.data_ptr(), dtype_code(x), x.stride(0), R, H, gate.data_ptr(), E,
+            sgate.has_value() ? sgate->data_ptr() : nullptr, k, shared_id, mptr<float>(logits), logits.numel(),
+            mptr<int32_t>(counter), mptr<int32_t>(pick_out), mptr<float>(wts_out), mptr<int32_t>(uids), uids.numel(),
+            mptr<int32_t>(ucount), mptr<int32_t>(members), members.size(1), cur_stream()));
+}
+
+void route_group(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
+                 int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out, at::Tensor wts_out,
+                 at::Tensor uids, at::Tensor ucount, at::Tensor members) {
+    route_group_impl(x, gate, sgate, k, shared_id, logits, counter, pick_out, wts_out, uids, ucount, members, false);
+}
+
+// route_group over its own all-ones logits buffer (esp_route_group_own; no reference counterpart)
+void route_group_own(const at::Tensor& x, const at::Tensor& gate, const c10::optional<at::Tensor>& sgate, int64_t k,
+                     int64_t shared_id, at::Tensor logits, at::Tensor counter, at::Tensor pick_out,
+                     at::Tensor wts_out, at::Tensor uids, at::Tensor ucount, at::Tensor members) {
+    route_group_impl(x, gate, sgate, k, shared_id, logits, counter, pick_out, wts_out, uids, ucount, members, true);
 }
 
 // route_group's routing over any number of rows, without the grouping (no reference counterpart)
@@ -697,6 +711,7 @@ PYBIND11_MODULE(espalier_ext, m) {
           py::arg("norm_d1") = py::none(), py::arg("norm_d2") = py::none(), py::arg("norm_w") = py::none(),
           py::arg("norm_h_out") = py::none(), py::arg("eps") = 0.0);
     m.def("route_group_rmsnorm", &route_group_rmsnorm);
+    m.def("route_group_own", &route_group_own);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);
     m.def("argmax", &argmax, py::arg("logits"), py::arg("ids"), py::arg("part") = py::none(),

@@ -1784,6 +1784,15 @@ extern "C" int esp_route_group(const void* x, int x_dtype, int64_t x_stride, int
                       pick_out, wts_out, uids, maxu, ucount, members, maxm, nullptr, stream);
 }
 
+extern "C" int esp_route_group_own(const void* x, int x_dtype, int64_t x_stride, int64_t R, int64_t H,
+                                   const void* gate, int64_t E, const void* sgate, int64_t k, int64_t shared_id,
+                                   float* logits, int64_t logits_numel, int32_t* counter, int32_t* pick_out,
+                                   float* wts_out, int32_t* uids, int64_t maxu, int32_t* ucount, int32_t* members,
+                                   int64_t maxm, void* stream) {
+    return route_impl(x, x_dtype, x_stride, R, H, gate, E, sgate, k, shared_id, logits, logits_numel, counter,
+                      pick_out, wts_out, uids, maxu, ucount, members, maxm, nullptr, stream, 1);
+}
+
 extern "C" int esp_route_group_rmsnorm(const void* h, const void* d1, const void* norm_w, double eps, void* h_out,
                                        void* a_out, int x_dtype, int64_t x_stride, int64_t R, int64_t H,
                                        const void* gate, int64_t E, const void* sgate, int64_t k, int64_t shared_id,

@@ -245,7 +245,6 @@ class Scratch:
             "z": ((partials,), f32, 0),                               # K-split partial sums of either projection
             "y": ((P, D), f32, 0),                                    # per-slot down outputs
             "route_counter": ((1,), i32, 0),                          # route_group's arrival count
-            "logits": ((rows * E,), f32, 0),                          # route_group's logits
             "pick": ((P,), i32, 0), "wts": ((P,), f32, 0),            # with the shared slot
             "ids": ((maxu,), i32, 0), "count": ((1,), i32, 0),        # distinct experts, in id order
             "members": ((maxu * rows,), i32, -1),                     # their member rows, -1 padded
@@ -260,7 +259,8 @@ class Scratch:
         # a piece once no word of it is all-ones, then puts the all-ones back)
         self.xdc = torch.full((P, I), -1, dtype=torch.int16, device=device).view(f16)
         self.zd = torch.full((P * D * (I // 128),), -1, dtype=i32, device=device).view(f32)
-        # esp_route_group_rmsnorm's logits (the shared gate's after each row's E): all-ones between uses
+        # the logits of esp_route_group_own and esp_route_group_rmsnorm (the shared gate's after each row's E): all-ones
+        # between uses
         self.logits_n = torch.full((rows * (E + 1),), -1, dtype=i32, device=device).view(f32)
 
     def window(self, R: int):
@@ -335,12 +335,13 @@ def routed(x: torch.Tensor, pick: torch.Tensor, wts: torch.Tensor, L: Layer, s: 
 
 def route(x: torch.Tensor, gate: torch.Tensor, k: int, L: Layer, s: Scratch):
     """The router GEMV (plus the shared gate), softmax / top-k / renormalisation and the grouping in one launch
-    (route_group) into the scratch's tables; routed2(..., pick=None) then runs the experts."""
+    (route_group, over the scratch's all-ones logits buffer: esp_route_group_own, the same bits) into the scratch's
+    tables; routed2(..., pick=None) then runs the experts."""
     R = x.shape[0]
     ids, members = s.window(R)
     P = R * s.slots
-    ext().route_group(x, gate, L.gate_w, k, L.shared_id, s.logits, s.route_counter, s.pick[:P], s.wts[:P], ids,
-                      s.count, members)
+    ext().route_group_own(x, gate, L.gate_w, k, L.shared_id, s.logits_n, s.route_counter, s.pick[:P], s.wts[:P], ids,
+                          s.count, members)
 
 
 def route_rmsnorm(h: torch.Tensor, d1: torch.Tensor | None, norm_w: torch.Tensor, eps: float, h_out: torch.Tensor,
