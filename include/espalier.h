@@ -35,7 +35,8 @@ extern "C" {
 #define ESP_STATUS_WIDTH_RANGE 2  /* a grouped launch met an expert whose K2 lies outside the launch's [lo, hi] */
 #define ESP_STATUS_WAIT_TIMEOUT 4 /* a launch gave up waiting (~20 ms): a chained launch (dense_multi, moe_chain) for a
                                      producer, a prompt launch (dense_tile) for the other K splits of a tile, or
-                                     route_group_rmsnorm at one row for the other workgroups' logits */
+                                     route_group_own / route_group_rmsnorm at one row for the other workgroups'
+                                     logits, or dense_own for the other K splits' partials */
 #define ESP_STATUS_TILE_LIST 8    /* esp_tile_list met more non-empty member tiles than its bound (a malformed table),
                                    * or esp_grouped_list's grid (sized from its P and maxm) is shorter than the list */
 
@@ -78,6 +79,18 @@ int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K
               const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh, int64_t xh_numel,
               float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK,
               int64_t W, int64_t PF, int64_t rot_smem, void* stream);
+
+/* esp_dense with Z as the launch's own hand-off buffer: every bit of Z set (0xFF bytes) on entry, and left so. Where the
+ * last K split's workgroup can hold one (row, split) partial a 32-lane half (M * (SK - 1) <= 2 W, in its shared
+ * memory), it reads the other splits' partials once none is all-ones, with no arrival count (a bounded wait: ~20 ms,
+ * then ESP_STATUS_WAIT_TIMEOUT); otherwise the arrivals are counted as in esp_dense and the finisher puts the all-ones
+ * back. Bit-identical to esp_dense; counters zero on entry and left zero. No counterpart in the reference (whose Z is
+ * plain scratch): for callers that keep a partials buffer across calls. */
+int esp_dense_own(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                  const void* const* trellis, const void* const* suh, const void* const* svh, const int64_t* n_cols,
+                  const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,
+                  int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel, int64_t k2,
+                  int64_t cb, int64_t SK, int64_t W, int64_t PF, int64_t rot_smem, void* stream);
 
 /* esp_dense over any number of rows (a whole prompt), for prefill: the same layer, with each weight decoded once for
  * every 128 rows instead of once a 32-row window. No counterpart in the reference (its prefill re-decodes the weights

@@ -187,6 +187,51 @@ def test_dense_split_finish_rows(dev, ext, name, M):
         assert torch.equal(d.forward(x[r:r + 1]).view(torch.int16), y[r:r + 1].view(torch.int16)), r
 
 
+@pytest.mark.parametrize("name", ["qkv", "o", "shared_gate_up", "shared_down"])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 32])
+def test_dense_own_equals_dense(dev, ext, name, M):
+    """esp_dense_own (Z an all-ones buffer of the caller's: the last split polls the others' partials where it can
+    hold one a 32-lane half, else arrivals are counted and the finisher restores the all-ones) against esp_dense:
+    y bit for bit over launches in a row and graph replays; Z left all-ones, counters zero, no wait timed out."""
+    print(f"dense_own {name} M={M}", flush=True)
+    mats = _mats(CONFIGS[name], 31, dev)
+    d = D.Dense(mats)
+    x = torch.randn((M, d.K), generator=torch.Generator().manual_seed(40 + M)).to(torch.bfloat16).to(dev)
+    want = _dense_call(d, x, torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev)).clone()
+    _, xh = D.scratch(dev, 0, 0)
+    zo = torch.full((max(sk * M * l.n for l, (sk, _, _) in zip(d.launches, d.plans)),), -1, dtype=torch.int32,
+                    device=dev).view(torch.float32)
+    y = torch.empty((M, d.n_out), dtype=torch.bfloat16, device=dev)
+
+    def launch():
+        for (idx, k2, cb), (sk, w, pf) in zip(d.groups, d.plans):
+            ext.dense_own(x, [d.mats[i].trellis for i in idx], [d.mats[i].suh for i in idx],
+                          [d.mats[i].svh for i in idx], [d.col0[i] for i in idx], y, xh, zo, d.counters, k2, cb, sk,
+                          w, pf, D.ROT_SMEM)
+
+    def check(tag):
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16)), tag
+        assert bool((zo.view(torch.int32) == -1).all()), f"{tag}: Z must be left all-ones"
+        assert int(d.counters.abs().sum()) == 0, f"{tag}: counters must be left zero"
+
+    ext.status(True)
+    assert D.polls(M, d.plans[0][0], d.plans[0][1]) == (M * (d.plans[0][0] - 1) <= 2 * d.plans[0][1])
+    for i in range(2):
+        y.zero_()
+        launch()
+        check(f"launch {i}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    for i in range(3):
+        y.zero_()
+        g.replay()
+        check(f"replay {i}")
+        torch.randn((64, 64), device=dev).sum()           # eager work between replays
+    assert int(ext.status(True)) == 0, "a wait timed out"
+
+
 @pytest.mark.parametrize("M", [1, 8, 32])
 def test_dense_graph_replay_equals_eager(dev, M):
     mats = _mats(CONFIGS["qkv"], 14, dev)

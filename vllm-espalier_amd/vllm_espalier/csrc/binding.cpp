@@ -246,10 +246,11 @@ void down_combine2(const at::Tensor& Z, const at::Tensor& pick, const at::Tensor
                            rows, P, D, SK, slots, E, n_routed, cur_stream()));
 }
 
-void dense(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
-           const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y, at::Tensor xh,
-           at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
-           int64_t rot_smem) {
+// dense's checks and call; own: Z is the caller's all-ones partials buffer (esp_dense_own)
+static void dense_call(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
+                       const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y,
+                       at::Tensor xh, at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK, int64_t W,
+                       int64_t PF, int64_t rot_smem, bool own) {
     TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.stride(1) == 1, "x: CUDA [M, K], unit column stride");
     TORCH_CHECK(y.is_cuda() && y.dim() == 2 && y.stride(1) == 1, "y: CUDA [M, N], unit column stride");
     TORCH_CHECK(T.size() == suh.size() && T.size() == svh.size() && T.size() == col0.size(), "one entry a matrix");
@@ -275,10 +276,26 @@ void dense(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vec
     check(counters, at::kInt, "counters");
     TORCH_CHECK(xh.scalar_type() == at::kHalf, "xh: fp16 scratch");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-    call(esp_dense(x.data_ptr(), dtype_code(x), x.stride(0), M, K, (int64_t)T.size(), tp.data(), sp.data(), vp.data(),
-                   ncols.data(), col0.data(), y.data_ptr(), dtype_code(y), y.stride(0), y.size(1), xh.data_ptr(),
-                   xh.numel(), mptr<float>(Z), Z.numel(), mptr<int32_t>(counters), counters.numel(), k2, cb, SK, W, PF,
-                   rot_smem, cur_stream()));
+    auto fn = own ? esp_dense_own : esp_dense;
+    call(fn(x.data_ptr(), dtype_code(x), x.stride(0), M, K, (int64_t)T.size(), tp.data(), sp.data(), vp.data(),
+            ncols.data(), col0.data(), y.data_ptr(), dtype_code(y), y.stride(0), y.size(1), xh.data_ptr(), xh.numel(),
+            mptr<float>(Z), Z.numel(), mptr<int32_t>(counters), counters.numel(), k2, cb, SK, W, PF, rot_smem,
+            cur_stream()));
+}
+
+void dense(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
+           const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y, at::Tensor xh,
+           at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+           int64_t rot_smem) {
+    dense_call(x, T, suh, svh, col0, y, xh, Z, counters, k2, cb, SK, W, PF, rot_smem, false);
+}
+
+// dense over the caller's all-ones partials buffer (esp_dense_own; no reference counterpart)
+void dense_own(const at::Tensor& x, const std::vector<at::Tensor>& T, const std::vector<at::Tensor>& suh,
+               const std::vector<at::Tensor>& svh, const std::vector<int64_t>& col0, at::Tensor y, at::Tensor xh,
+               at::Tensor Z, at::Tensor counters, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+               int64_t rot_smem) {
+    dense_call(x, T, suh, svh, col0, y, xh, Z, counters, k2, cb, SK, W, PF, rot_smem, true);
 }
 
 // dense over a whole prompt (no reference counterpart): x [T, K], any T
@@ -712,6 +729,7 @@ PYBIND11_MODULE(espalier_ext, m) {
           py::arg("norm_h_out") = py::none(), py::arg("eps") = 0.0);
     m.def("route_group_rmsnorm", &route_group_rmsnorm);
     m.def("route_group_own", &route_group_own);
+    m.def("dense_own", &dense_own);
     m.def("embed", &embed);
     m.def("add_rmsnorm", &add_rmsnorm);
     m.def("argmax", &argmax, py::arg("logits"), py::arg("ids"), py::arg("part") = py::none(),

@@ -264,6 +264,7 @@ int ok();
 int launch_check(const char* what);
 int dense_status(int clear, hipStream_t st, int* out);     // dense_multi.hip: the dense launches' status word
 int tile_status(int clear, hipStream_t st, int* out);      // dense_tile.hip: the prompt launches' status word
+int dense_own_status(int clear, hipStream_t st, int* out); // dense.hip: esp_dense_own's status word
 }  // namespace esp_host
 
 #define ESP_REQUIRE(cond, ...)                                                                  \

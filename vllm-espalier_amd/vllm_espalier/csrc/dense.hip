@@ -19,6 +19,13 @@
 
 namespace esp {
 
+// Device status of esp_dense_own's bounded waits (read and cleared by esp_status through dense_own_status)
+__device__ int g_dense_own_status;
+
+__device__ void dense_raise_status(int bits) {
+    __hip_atomic_fetch_or(&g_dense_own_status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // dequant: out fp16 [K][N]. A wave decodes one 32k x 16n block (two k tiles of one n tile) with the MFMA lane decode
 // (the same code the GEMMs run) and scatters its 8 values a lane.
@@ -315,12 +322,18 @@ static int dense_impl(const void* x, int x_dtype, int64_t x_stride, int64_t M, i
                       const int64_t* col0, void* y, int y_dtype, int64_t y_stride, int64_t y_cols, void* xh,
                       int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters, int64_t counters_numel,
                       int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t rot_smem, const DenseNorm* nrm,
-                      void* stream) {
+                      void* stream, bool own = false) {
     DenseLaunch L{};
     const int rc = prepare_dense(x, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype,
                                  y_stride, y_cols, xh, xh_numel, Z, z_numel, counters, counters_numel, k2, cb, SK, W,
                                  rot_smem, nrm, L);
     if (rc) return rc;
+    if (own && SK > 1) {
+        // the polled hand-off when the finisher holds one (row, split) partial a 32-lane half and they fit its shared
+        // memory past the block's sums; else the arrivals are counted and the finisher restores the all-ones
+        const bool poll = M * (SK - 1) <= 2 * L.W && (size_t)(L.W / 4 + SK - 1) * M * 512 <= L.smem;
+        L.a.own = poll ? 2 : 1;
+    }
     return launch_prepared(L, (hipStream_t)stream);
 }
 
@@ -335,6 +348,19 @@ extern "C" int esp_dense(const void* x, int x_dtype, int64_t x_stride, int64_t M
     return dense_impl(x, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
                       y_cols, xh, xh_numel, Z, z_numel, counters, counters_numel, k2, cb, SK, W, rot_smem, nullptr,
                       stream);
+}
+
+extern "C" int esp_dense_own(const void* x, int x_dtype, int64_t x_stride, int64_t M, int64_t K, int64_t n_shards,
+                             const void* const* trellis, const void* const* suh, const void* const* svh,
+                             const int64_t* n_cols, const int64_t* col0, void* y, int y_dtype, int64_t y_stride,
+                             int64_t y_cols, void* xh, int64_t xh_numel, float* Z, int64_t z_numel, int32_t* counters,
+                             int64_t counters_numel, int64_t k2, int64_t cb, int64_t SK, int64_t W, int64_t PF,
+                             int64_t rot_smem, void* stream) {
+    (void)PF;
+    ESP_REQUIRE(x, "dense_own: null x");
+    return dense_impl(x, x_dtype, x_stride, M, K, n_shards, trellis, suh, svh, n_cols, col0, y, y_dtype, y_stride,
+                      y_cols, xh, xh_numel, Z, z_numel, counters, counters_numel, k2, cb, SK, W, rot_smem, nullptr,
+                      stream, true);
 }
 
 extern "C" int esp_dense_rmsnorm(const void* h, const void* d1, const void* d2, const void* norm_w, double eps,
@@ -447,3 +473,23 @@ extern "C" int esp_phase_clear(void) {
     return esp_host::ok();
 }
 #endif
+
+namespace esp_host {
+// esp_dense_own's device status word into *out (ORed), cleared if asked (esp_status)
+int dense_own_status(int clear, hipStream_t st, int* out) {
+    int v = 0;
+    if (hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(esp::g_dense_own_status), sizeof(int), 0, hipMemcpyDeviceToHost, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(ESP_ERR_HIP, "status: cannot read the dense launches' status word");
+    *out |= v;
+    if (clear && v) {
+        const int zero = 0;
+        if (hipMemcpyToSymbolAsync(HIP_SYMBOL(esp::g_dense_own_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice,
+                                   st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return fail(ESP_ERR_HIP, "status: cannot clear the dense launches' status word");
+    }
+    return ESP_OK;
+}
+}  // namespace esp_host

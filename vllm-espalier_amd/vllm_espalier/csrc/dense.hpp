@@ -67,6 +67,9 @@ struct DenseArgs {
     int SQ, SR;              // K / 32 steps = SQ * SK + SR: split s has SQ + (s < SR) steps
     int cnt_stride;          // ints between two column blocks' arrival counters (32: a 128-byte line each)
     int gather;              // the last workgroup loads the M * SK partials one a 32-lane half (shared memory holds them)
+    // esp_dense_own: Z holds all-ones between launches. 2: split SK - 1 (dispatched after the others) polls the other
+    // splits' partials, no arrival count; 1: arrivals counted, and the finisher puts the all-ones back
+    int own;
     // esp_dense_rmsnorm: the input rows are RMSNorm(h + d1 + d2) * nw (norm.hpp), made in the launch; workgroup (0, 0)
     // stores the residual h + d1 + d2 to nh_out. Rows of h, d1, d2 and nh_out are x_stride apart.
     const uint16_t* nh;
@@ -161,6 +164,9 @@ __device__ __forceinline__ void finish(float (&v)[4], int l32, uint2 sv, float s
         v[j] *= HAD_SCALE * s[j];
     }
 }
+
+// ORs bits into esp_dense_own's status word (dense.hip; only its launches call it)
+__device__ void dense_raise_status(int bits);
 
 // The work of one workgroup: column block nbg of the launch, K split `split`. smem: the dynamic shared memory;
 // last, npart, ninv: small shared scratch of the calling kernel.
@@ -381,6 +387,54 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     // 4. K splits: partials to Z, the last split of the block to arrive adds them in split order and finishes
     const size_t zrow = (size_t)a.NBT * 128;
     const DevBuf zb(a.Z);
+    constexpr uint32_t empty = 0xFFFFFFFFu;
+    const float4 e4 = make_float4(__uint_as_float(empty), __uint_as_float(empty), __uint_as_float(empty),
+                                  __uint_as_float(empty));
+    if constexpr (!MULTI) {
+        if (a.own == 2) {
+            // the splits below SK - 1 store their partials and leave; split SK - 1 loads each of theirs, one (row,
+            // split) a 32-lane half, until no word is all-ones (bounded: ~20 ms, then ESP_STATUS_WAIT_TIMEOUT), puts
+            // the all-ones back, and adds each row's splits in split order, its own (from shared memory) last
+            if (split != a.SK - 1) {
+                for (int r = wave * 2 + half; r < M; r += 2 * NW)
+                    zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
+                return;
+            }
+            const int others = a.SK - 1, idx = wave * 2 + half;
+            float4* zs = reinterpret_cast<float4*>(smem + (size_t)KW * M * 128 * 4);   // past the block's sums
+            if (idx < M * others) {
+                const int r = idx / others, q = idx - r * others;
+                float* zp = a.Z + ((size_t)q * M + r) * zrow + nbg * 128 + 4 * l32;
+                float4 u = zb.load4(zp);
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                while (__float_as_uint(u.x) == empty || __float_as_uint(u.y) == empty ||
+                       __float_as_uint(u.z) == empty || __float_as_uint(u.w) == empty) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (__builtin_amdgcn_s_memrealtime() - t0 > 2000000ull) {
+                        if (l32 == 0) dense_raise_status(ESP_STATUS_WAIT_TIMEOUT);
+                        break;
+                    }
+                    u = zb.load4(zp);
+                }
+                zs[idx * 32 + l32] = u;
+                zb.store4(zp, e4);
+            }
+            __syncthreads();
+            for (int r = idx; r < M; r += 2 * NW) {
+                float4 s = zs[(r * others) * 32 + l32];
+                for (int q = 1; q < others; ++q) {
+                    const float4 u = zs[(r * others + q) * 32 + l32];
+                    s.x += u.x; s.y += u.y; s.z += u.z; s.w += u.w;
+                }
+                const float4 own = row_sum(r);
+                s.x += own.x; s.y += own.y; s.z += own.z; s.w += own.w;
+                float v[4] = {s.x, s.y, s.z, s.w};
+                finish(v, l32, sv, S.scale);
+                store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
+            }
+            return;
+        }
+    }
     for (int r = wave * 2 + half; r < M; r += 2 * NW)
         zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
     int* const cnt_p = a.counters + (size_t)nbg * a.cnt_stride;
@@ -399,6 +453,10 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             zs[idx * 32 + l32] = zb.load4(a.Z + (size_t)q * zsplit + (size_t)r * zrow + nbg * 128 + 4 * l32);
         }
         __syncthreads();
+        if (a.own && idx < M * a.SK) {                      // the partials are read: the all-ones back
+            const int r = idx / a.SK, q = idx - r * a.SK;
+            zb.store4(a.Z + (size_t)q * zsplit + (size_t)r * zrow + nbg * 128 + 4 * l32, e4);
+        }
         for (int r = wave * 2 + half; r < M; r += 2 * NW) {
             float4 s = zs[(r * a.SK) * 32 + l32];
             for (int q = 1; q < a.SK; ++q) {
@@ -430,6 +488,11 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
                 } else if (q0 + i < a.SK) {
                     s.x += u[i].x; s.y += u[i].y; s.z += u[i].z; s.w += u[i].w;
                 }
+            }
+            if (a.own) {                                        // the partials are read: the all-ones back
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (q0 + i < a.SK) zb.store4(const_cast<float*>(zp) + (q0 + i) * zsplit, e4);
             }
         }
         float v[4] = {s.x, s.y, s.z, s.w};

@@ -2258,6 +2258,7 @@ extern "C" int esp_status(int32_t* status, int clear, void* stream) {
         return esp_host::fail(ESP_ERR_HIP, "status: cannot read the device status word");
     if (esp_host::dense_status(clear, st, status)) return ESP_ERR_HIP;
     if (esp_host::tile_status(clear, st, status)) return ESP_ERR_HIP;
+    if (esp_host::dense_own_status(clear, st, status)) return ESP_ERR_HIP;
     *status |= v;
     if (clear && v) {
         const int zero = 0;

@@ -69,6 +69,9 @@ def tile_plan(K: int, N: int) -> int:
 
 
 TILE_ROWS = 128              # rows a prompt-launch workgroup
+# launches whose last K split can poll the others' partials run as esp_dense_own over an all-ones partials buffer (the
+# same bits, no arrival count); ESPALIER_DENSE_OWN=0 runs every launch as esp_dense
+OWN = env("ESPALIER_DENSE_OWN", "1") != "0"
 
 
 class _SharedScratch:
@@ -77,7 +80,8 @@ class _SharedScratch:
     graph may write to it (it was handed out during a stream capture); otherwise it is dropped, and the caching
     allocator reuses its memory, so a series of growing prompts outside capture keeps only the current pair."""
 
-    def __init__(self):
+    def __init__(self, ones: bool = False):
+        self.ones = ones                     # Z every bit set (the all-ones partials of esp_dense_own)
         self.current: dict = {}
         self.captured: set = set()          # devices whose current pair was handed out during a capture
         self.retired: list = []
@@ -94,7 +98,9 @@ class _SharedScratch:
                 self.retired.append(have)
             z_floats, xh_halves = max(z_floats, have[0].numel()), max(xh_halves, have[1].numel())
         self.captured.discard(device)
-        pair = (torch.empty(max(z_floats, 1), dtype=torch.float32, device=device),
+        z = (torch.full((max(z_floats, 1),), -1, dtype=torch.int32, device=device).view(torch.float32) if self.ones
+             else torch.empty(max(z_floats, 1), dtype=torch.float32, device=device))
+        pair = (z,
                 torch.empty(max(xh_halves, 1), dtype=torch.float16, device=device))
         self.current[device] = pair
         if capturing:
@@ -103,11 +109,24 @@ class _SharedScratch:
 
 
 _SHARED = _SharedScratch()
+_OWN = _SharedScratch(ones=True)
 
 
 def scratch(device, z_floats: int, xh_halves: int):
     """(Z, xh) of the device, grown to at least the given sizes."""
     return _SHARED.reserve(device, z_floats, xh_halves)
+
+
+def own_partials(device, z_floats: int):
+    """The device's all-ones partials buffer of esp_dense_own (left all-ones by every launch), grown to at least
+    z_floats."""
+    return _OWN.reserve(device, z_floats, 0)[0]
+
+
+def polls(M: int, sk: int, w: int) -> bool:
+    """Whether a launch of M rows, sk K splits and w waves takes esp_dense_own's polled hand-off: its last split holds
+    one (row, split) partial a 32-lane half."""
+    return sk > 1 and M * (sk - 1) <= 2 * w
 
 
 _PROMPT = _SharedScratch()
@@ -170,6 +189,7 @@ class Dense:
         blocks = max(l.n // 128 for l in self.launches)
         self.counters = torch.zeros(COUNTER_STRIDE * blocks, dtype=torch.int32, device=device)
         scratch(device, max(l.sk * MAX_ROWS * l.n for l in self.launches), 4 * MAX_ROWS * self.K)
+        own_partials(device, max(l.sk * 2 * l.w // max(l.sk - 1, 1) * l.n for l in self.launches))
 
     def _code(self, i: int) -> tuple[int, int]:
         m = self.mats[i]
@@ -205,10 +225,16 @@ class Dense:
             x = x.contiguous()
         z, xh = scratch(x.device, 0, 0)
         e = ext()
+        M = x.shape[0]
         for l in self.launches:
             pick = l.members
-            e.dense(x, [codes[i] for i in pick], [pre[i] for i in pick], [post[i] for i in pick],
-                    [self.col0[i] for i in pick], y, xh, z, self.counters, l.k2, l.cb, l.sk, l.w, l.pf, ROT_SMEM)
+            # a launch whose last split can poll the others' partials runs over the all-ones buffer (the same bits)
+            if OWN and polls(M, l.sk, l.w):
+                run, zl = e.dense_own, own_partials(x.device, l.sk * M * l.n)
+            else:
+                run, zl = e.dense, z
+            run(x, [codes[i] for i in pick], [pre[i] for i in pick], [post[i] for i in pick],
+                [self.col0[i] for i in pick], y, xh, zl, self.counters, l.k2, l.cb, l.sk, l.w, l.pf, ROT_SMEM)
         return y
 
     def reserve_prompt(self, T: int) -> None:
