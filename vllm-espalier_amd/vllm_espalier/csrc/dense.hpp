@@ -398,8 +398,10 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
             if (split != a.SK - 1) {
                 for (int r = wave * 2 + half; r < M; r += 2 * NW)
                     zb.store4(a.Z + ((size_t)split * M + r) * zrow + nbg * 128 + 4 * l32, row_sum(r));
+                ESP_PHASE(4);
                 return;
             }
+            ESP_PHASE(4);
             const int others = a.SK - 1, idx = wave * 2 + half;
             float4* zs = reinterpret_cast<float4*>(smem + (size_t)KW * M * 128 * 4);   // past the block's sums
             if (idx < M * others) {
@@ -420,6 +422,8 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
                 zb.store4(zp, e4);
             }
             __syncthreads();
+            ESP_PHASE(5);
+            ESP_PHASE_XCD(1);
             for (int r = idx; r < M; r += 2 * NW) {
                 float4 s = zs[(r * others) * 32 + l32];
                 for (int q = 1; q < others; ++q) {
@@ -432,6 +436,8 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
                 finish(v, l32, sv, S.scale);
                 store4_y(a.y, a.y_dtype, (size_t)r * a.y_stride + ycol, v, coherent);
             }
+            ESP_PHASE_DRAIN();
+            ESP_PHASE(6);
             return;
         }
     }
