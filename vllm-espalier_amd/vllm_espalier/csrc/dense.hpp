@@ -244,11 +244,22 @@ __device__ __forceinline__ void dense_program(const DenseArgs& a, const int nbg,
     // in flight. The scales are loaded after the copies are issued: they need the shard's other fields, a later
     // round of argument loads.
     const bool norm_apart = a.norm && 4 * M < NW;
+    // Without the norm, the waves that rotate the input rows (a (row, 128-block) a 32-lane half) issue no copies when
+    // the others suffice, so their row loads are not queued behind the stage (vmcnt returns in order): the rows are
+    // rotated while the stage lands, not after it
+    bool rows_apart = false;
+    int rot_waves = 0;
+    if constexpr (MG == 1) {
+        rot_waves = (M * (((k0 + kr + 127) >> 7) - (k0 >> 7)) + 1) >> 1;
+        rows_apart = a.fused && !a.norm && !(MULTI && a.wait_done) && rot_waves + 4 <= NW;
+    }
     {
         const int steps = kr >> 5;
         const int sst = steps < StagePlan<K2>::MAX_STEPS ? steps : StagePlan<K2>::MAX_STEPS;
         if (norm_apart)
             issue_stage_waves<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage, 4 * M, NW - 4 * M);
+        else if (rows_apart)
+            issue_stage_waves<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage, rot_waves, NW - rot_waves);
         else
             issue_stage<K2>(S.T, NTILES, k0 >> 4, 2 * sst, cb_local * 8, stage);
     }
