@@ -69,13 +69,14 @@ __device__ __forceinline__ void issue_stage(const uint32_t* __restrict__ T, int 
 }
 
 // issue_stage for a K2 known only at run time (a launch whose experts differ in width): the same units in the same
-// LDS places as issue_stage<K2>
+// LDS places as issue_stage<K2>, issued by waves w0 .. of the workgroup (the ones below issue nothing)
 __device__ __forceinline__ void issue_stage_rt(const uint32_t* __restrict__ T, int k2, int NTILES, int kt0, int rows,
-                                               int nt0, uint32_t* lds) {
+                                               int nt0, uint32_t* lds, int w0 = 0) {
     const int TW = 4 * k2, UPR = 2 * TW;
     const int units = rows * UPR;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int u0 = wave * 64; u0 < units; u0 += (int)blockDim.x) {
+    const int wave = (int)(threadIdx.x >> 6) - w0, lane = threadIdx.x & 63;
+    if (wave < 0) return;
+    for (int u0 = wave * 64; u0 < units; u0 += (int)blockDim.x - 64 * w0) {
         const int u = u0 + lane;
         if (u < units) {
             const int r = u / UPR, w = (u - r * UPR) * 4;

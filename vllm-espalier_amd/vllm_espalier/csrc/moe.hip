@@ -1172,12 +1172,16 @@ __device__ __forceinline__ void grouped_program(const GroupedArgs& a, int bx, in
     GateupScales sc{};
     if (MODE == 1 && runs) {
         // the first stage's copies in flight, then the member rows' K range, rotated, into shared memory; the
-        // epilogue's scales (the expert's, for this lane's 4 columns) ride along, for the workgroup that runs it
-        issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), by * 8, stage);
+        // epilogue's scales (the expert's, for this lane's 4 columns) ride along, for the workgroup that runs it.
+        // The waves that rotate (a (row, 128-block) a 32-lane half) issue no copies when others are left for them:
+        // vector loads return in order, so rows loaded after the copies would wait for the whole stage.
+        const int chunks = kr >> 7;
+        const int rot_waves = (nrows * chunks + 1) >> 1;
+        issue_stage_rt(T, k2, a.N >> 4, k0 >> 4, 2 * first_stage_steps(k2, kr >> 5), by * 8, stage,
+                       rot_waves < NW ? rot_waves : 0);
         sc = gateup_scales(a.svh0, a.svh1, a.suh_d, (size_t)e * a.N + by * 128 + 4 * l32);
         uint16_t* xs = reinterpret_cast<uint16_t*>(smem + a.stage_bytes);
         const uint16_t* suh = (mat ? a.suh1 : a.suh0) + (size_t)e * a.K;
-        const int chunks = kr >> 7;
         for (int idx = wave * 2 + half; idx < nrows * chunks; idx += 2 * NW) {
             const int m = idx / chunks, ch = idx - m * chunks;
             const int row = rows_sh[m] / a.slots;
