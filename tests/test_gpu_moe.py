@@ -210,22 +210,31 @@ def test_route_group_rows_alone_and_graph(dev, ext):
         assert torch.equal(bufs[2].view(R, 9), pick) and torch.equal(bufs[3].view(R, 9), wts), f"replay {i}"
 
 
-@pytest.mark.parametrize("R,E,shared,dtype", [(1, 256, True, "bf16"), (1, 256, False, "bf16"), (1, 100, True, "bf16"),
-                                               (2, 256, True, "bf16"), (4, 256, True, "bf16"), (1, 256, True, "fp16"),
-                                               (3, 256, True, "fp16")])
-def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared, dtype):
+@pytest.mark.parametrize("R,E,shared,dtype,delta", [(1, 256, True, "bf16", True), (1, 256, False, "bf16", True),
+                                                     (1, 100, True, "bf16", True), (2, 256, True, "bf16", True),
+                                                     (4, 256, True, "bf16", True), (1, 256, True, "fp16", True),
+                                                     (3, 256, True, "fp16", True), (1, 256, True, "bf16", False),
+                                                     (2, 256, True, "fp16", False), (1, 256, True, "bf16", 4096),
+                                                     (2, 100, True, "bf16", 1024)])
+def test_route_group_rmsnorm_sentinel(dev, ext, R, E, shared, dtype, delta):
     """route_group_rmsnorm (the norm inside the routing launch; its logits an all-ones hand-off buffer, which at one
     row the last workgroup polls instead of counting arrivals) against add_rmsnorm then route_group: the normalised
     rows, the residual, picks, weights and grouping bit for bit; the logits left all-ones and the counter zero, over
-    two launches in a row and graph replays (each reading the all-ones the previous one left)."""
-    print(f"route_group_rmsnorm R={R} E={E} shared={shared} {dtype}", flush=True)
-    H, k, eps = 2048, 8, 1e-6
+    two launches in a row and graph replays (each reading the all-ones the previous one left). Without the delta, h
+    holds planted -0 and +0 elements, which the residual must keep bit for bit."""
+    # delta: True / False, or a width other than 2048 (with the delta: the launch's general norm path)
+    H = 2048 if isinstance(delta, bool) else delta
+    print(f"route_group_rmsnorm R={R} E={E} shared={shared} {dtype} delta={delta} H={H}", flush=True)
+    k, eps = 8, 1e-6
     t = torch.bfloat16 if dtype == "bf16" else torch.float16
-    x, gate, sgate = router_inputs(R, 700 + R + E, E=E, near_ties=R >= 3)
+    x, gate, sgate = router_inputs(R, 700 + R + E, H=H, E=E, near_ties=R >= 3)
     x, gate, sgate = x.to(t), gate.to(t), sgate.to(t)
     gen = torch.Generator().manual_seed(710 + R + E)
+    if not delta:
+        x[:, 5::97] = -0.0
+        x[:, 7::101] = 0.0
     h = x.to(dev)
-    d1 = (torch.randn((R, H), generator=gen) * 0.5).to(t).to(dev)
+    d1 = (torch.randn((R, H), generator=gen) * 0.5).to(t).to(dev) if delta else None
     w = (1 + 0.1 * torch.randn(H, generator=gen)).to(t).to(dev)
     sid = E if shared else -1
     h_ref, a_ref = h.clone(), torch.empty_like(h)

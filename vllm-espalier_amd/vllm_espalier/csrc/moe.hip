@@ -178,7 +178,9 @@ __device__ __forceinline__ void raise_status(int bits) {
     __hip_atomic_fetch_or(&g_status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int BF16>
+// NORM: the launch normalises its input rows (esp_route_group_rmsnorm; a.norm set), an instance of its own so that the
+// plain routing's code does not carry the norm's
+template <int BF16, bool NORM>
 __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
     extern __shared__ __align__(16) unsigned char rsmem[];     // norm: the normalised rows [R][H]
     __shared__ int last;
@@ -204,24 +206,48 @@ __global__ __launch_bounds__(RT) void route_group_kernel(RouteArgs a) {
         route_load8(p, h, a.H, v);
     };
     uint2 gv[4][2];
-    if (active && a.H <= 2048) {
+    auto gate_loads = [&]() __attribute__((always_inline)) {
+        if (active && a.H <= 2048) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) load8(w, 512 * q + 8 * lane, gv[q]);   // in flight while the rows are normalised
-    }
-    if (a.norm) {
-        // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them. The norm
-        // weights of a thread's chunks are in flight with the rows.
+            for (int q = 0; q < 4; ++q) load8(w, 512 * q + 8 * lane, gv[q]);
+        }
+    };
+    if constexpr (!NORM) gate_loads();
+    if constexpr (NORM) {
+        // every workgroup normalises the rows itself (four waves a row); workgroup 0 also stores them. The rows'
+        // loads go first, then the norm weights and the gate's chunks, which stay in flight while the rows are
+        // normalised (vector loads return in order; the norm's barriers wait only for shared memory).
         __shared__ float npart[16], ninv[4];
         const int r = tid >> 8, t = tid & 255;
         uint4 wq[NORM_CHUNKS];
+        auto after_rows = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < NORM_CHUNKS; ++c) {
-            const int i = (c * 256 + t) * 8;
-            wq[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (r < R && i < a.H) wq[c] = *reinterpret_cast<const uint4*>(a.nw + i);
-        }
+            for (int c = 0; c < NORM_CHUNKS; ++c) {
+                const int i = (c * 256 + t) * 8;
+                wq[c] = make_uint4(0u, 0u, 0u, 0u);
+                if (r < R && i < a.H) wq[c] = *reinterpret_cast<const uint4*>(a.nw + i);
+            }
+            gate_loads();
+        };
         uint4 zq[NORM_CHUNKS];
-        norm_rows_inv(a.nh, a.nd1, nullptr, a.x_stride, R, a.H, a.neps, BF16, npart, ninv, zq);
+        if (a.H == 2048) {
+            // the same loads without conditions inside the rows' waves (the only active ones: rg = r < R), so that
+            // the rows' use waits for the rows alone; a column past the router's loads row 0 of the gate, unused
+            auto after_rows_2048 = [&]() __attribute__((always_inline)) {
+                wq[0] = *reinterpret_cast<const uint4*>(a.nw + t * 8);
+#pragma unroll
+                for (int k = 1; k < NORM_CHUNKS; ++k) wq[k] = make_uint4(0u, 0u, 0u, 0u);
+                const uint16_t* wl = c < C ? w : a.gate;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    gv[q][0] = *reinterpret_cast<const uint2*>(wl + 512 * q + 8 * lane);
+                    gv[q][1] = *reinterpret_cast<const uint2*>(wl + 512 * q + 8 * lane + 4);
+                }
+            };
+            norm_rows_inv_2048(a.nh, a.nd1, a.x_stride, R, a.neps, BF16, npart, ninv, zq, after_rows_2048);
+        } else {
+            norm_rows_inv_then(a.nh, a.nd1, nullptr, a.x_stride, R, a.H, a.neps, BF16, npart, ninv, zq, after_rows);
+        }
         uint16_t* xs = reinterpret_cast<uint16_t*>(rsmem);
         if (r < R) {
             const size_t o = (size_t)r * a.x_stride;
@@ -1735,13 +1761,18 @@ static int route_impl(const void* x, int x_dtype, int64_t x_stride, int64_t R, i
         smem = (size_t)R * H * 2;
     }
     const unsigned grid = (unsigned)((E + has + RT_COLS - 1) / RT_COLS);
-    const void* fn = a.bf16 ? (const void*)route_group_kernel<1> : (const void*)route_group_kernel<0>;
+    const void* fn = a.norm ? (a.bf16 ? (const void*)route_group_kernel<1, true> : (const void*)route_group_kernel<0, true>)
+                            : (a.bf16 ? (const void*)route_group_kernel<1, false> : (const void*)route_group_kernel<0, false>);
     if (smem > 64 * 1024 && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess)
         return esp_host::fail(ESP_ERR_HIP, "route_group: cannot raise the shared memory limit to %zu bytes", smem);
-    if (a.bf16)
-        route_group_kernel<1><<<grid, RT, smem, (hipStream_t)stream>>>(a);
+    if (a.norm && a.bf16)
+        route_group_kernel<1, true><<<grid, RT, smem, (hipStream_t)stream>>>(a);
+    else if (a.norm)
+        route_group_kernel<0, true><<<grid, RT, smem, (hipStream_t)stream>>>(a);
+    else if (a.bf16)
+        route_group_kernel<1, false><<<grid, RT, smem, (hipStream_t)stream>>>(a);
     else
-        route_group_kernel<0><<<grid, RT, smem, (hipStream_t)stream>>>(a);
+        route_group_kernel<0, false><<<grid, RT, smem, (hipStream_t)stream>>>(a);
     return esp_host::launch_check("route_group");
 }
 

@@ -74,9 +74,14 @@ __device__ __forceinline__ uint4 norm_z8_of(uint4 uh, uint4 u1, uint4 u2, bool h
 
 // Thread t's chunks of row (h, d1, d2) (elements (c * 256 + t) * 8 .. + 8, c < NORM_CHUNKS, those below D): z packed
 // in the model dtype (the stored residual, exact; h itself when no delta is added) and its share of the sum of squares.
-// Every load is issued before any is used, so the three operands cost one memory round trip.
+// Every load is issued before any is used, so the three operands cost one memory round trip. `after` runs between the
+// loads and their first use: loads it issues are queued behind the rows' (vector loads return in order).
+struct NoLoads {
+    __device__ __forceinline__ void operator()() const {}
+};
+template <typename F = NoLoads>
 __device__ __forceinline__ float norm_z_rows(const uint16_t* h, const uint16_t* d1, const uint16_t* d2, int D, bool bf,
-                                             int t, uint4 (&zq)[NORM_CHUNKS]) {
+                                             int t, uint4 (&zq)[NORM_CHUNKS], const F& after = F{}) {
     const uint16_t* p1 = d1 ? d1 : h;             // a stand-in row keeps the loads free of the delta branches
     const uint16_t* p2 = d2 ? d2 : h;
     uint4 uh[NORM_CHUNKS], u1[NORM_CHUNKS], u2[NORM_CHUNKS];
@@ -90,6 +95,7 @@ __device__ __forceinline__ float norm_z_rows(const uint16_t* h, const uint16_t* 
             u2[c] = *reinterpret_cast<const uint4*>(p2 + i);
         }
     }
+    after();
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NORM_CHUNKS; ++c) {
@@ -142,6 +148,60 @@ __device__ __forceinline__ void norm_rows_inv(const uint16_t* h, const uint16_t*
     if constexpr (LDS_ONLY) lds_barrier(); else __syncthreads();
     if ((int)threadIdx.x < R) inv_sh[threadIdx.x] = norm_inv(part_sh + 4 * threadIdx.x, D, eps);
     if constexpr (LDS_ONLY) lds_barrier(); else __syncthreads();
+}
+
+// norm_rows_inv's scales for D = 2048 (one chunk a thread) and no second delta, with the caller's own loads issued
+// behind the rows' (after, run by the rows' waves once). Inside the rows' waves every load is unconditional, so the
+// compiler can wait for the rows alone (vmcnt counts what after issued): after's loads stay in flight while the rows
+// are summed, and the two barriers wait only for shared-memory work. Same sums in the same order as norm_rows_inv.
+template <typename F>
+__device__ __forceinline__ void norm_rows_inv_2048(const uint16_t* h, const uint16_t* d1, int stride, int R, float eps,
+                                                   bool bf, float* part_sh, float* inv_sh, uint4 (&zq)[NORM_CHUNKS],
+                                                   const F& after) {
+    const int wave = threadIdx.x >> 6, r = wave >> 2, t = threadIdx.x & 255;
+#pragma unroll
+    for (int c = 1; c < NORM_CHUNKS; ++c) zq[c] = make_uint4(0u, 0u, 0u, 0u);
+    if (r < R) {
+        const size_t o = (size_t)r * stride + (size_t)t * 8;
+        // A missing delta is -0 in every element (h + -0 = h exactly, -0 included), so the sum is always formed and
+        // the delta's load always issued before `after`'s (h stands in for its address); a load used only under
+        // the delta's condition would be sunk behind them
+        const uint16_t* p1 = d1 ? d1 : h;
+        const uint4 uh = *reinterpret_cast<const uint4*>(h + o);
+        const uint4 l1 = *reinterpret_cast<const uint4*>(p1 + o);
+        const uint4 u1 = d1 ? l1 : make_uint4(0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u);
+        after();
+        float z[8];
+        zq[0] = norm_z8_of(uh, u1, u1, true, false, bf, z);
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += z[j] * z[j];
+        ss = wave_sum_f32(ss);
+        if ((threadIdx.x & 63) == 0) part_sh[wave] = ss;
+    }
+    lds_barrier();
+    if ((int)threadIdx.x < R) inv_sh[threadIdx.x] = norm_inv(part_sh + 4 * threadIdx.x, 2048, eps);
+    lds_barrier();
+}
+
+// norm_rows_inv's scales (no zs) with the caller's own loads issued behind the rows' (after, run by every thread once):
+// they stay in flight through the two barriers, which wait only for shared-memory work
+template <typename F>
+__device__ __forceinline__ void norm_rows_inv_then(const uint16_t* h, const uint16_t* d1, const uint16_t* d2,
+                                                   int stride, int R, int D, float eps, bool bf, float* part_sh,
+                                                   float* inv_sh, uint4 (&zq)[NORM_CHUNKS], const F& after) {
+    const int wave = threadIdx.x >> 6, r = wave >> 2, t = threadIdx.x & 255;
+    if (r < R) {
+        const size_t o = (size_t)r * stride;
+        const float ss =
+            wave_sum_f32(norm_z_rows(h + o, d1 ? d1 + o : nullptr, d2 ? d2 + o : nullptr, D, bf, t, zq, after));
+        if ((threadIdx.x & 63) == 0) part_sh[wave] = ss;
+    } else {
+        after();
+    }
+    lds_barrier();
+    if ((int)threadIdx.x < R) inv_sh[threadIdx.x] = norm_inv(part_sh + 4 * threadIdx.x, D, eps);
+    lds_barrier();
 }
 
 // thread t's chunks of its row (norm_rows_inv's zq) stored at row (o = r * stride) of out
