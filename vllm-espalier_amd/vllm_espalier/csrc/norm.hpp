@@ -173,6 +173,7 @@ __device__ __forceinline__ void norm_rows_inv_2048(const uint16_t* h, const uint
         after();
         float z[8];
         zq[0] = norm_z8_of(uh, u1, u1, true, false, bf, z);
+        if (!d1) zq[0] = uh;                                  // the residual is h itself, bit for bit (NaNs too)
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) ss += z[j] * z[j];
