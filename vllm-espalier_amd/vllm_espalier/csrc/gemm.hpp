@@ -32,6 +32,11 @@ struct StagePlan {
     static constexpr int MAX_STEPS = stage_max_steps(K2);
 };
 
+// Cache policy of the trellis copies: non-temporal (the nt bit of gfx950's global_load_lds). A decode step streams
+// ~1 GB of trellis words, each read once, through the 256 MB MALL; marked non-temporal they do not push out what the
+// step reads again soon and waits on (activations, routing tables, scales, norm weights, router weights).
+constexpr int CPOL_NT = 2;
+
 // Copy k tiles [kt0, kt0 + rows) of the block (n tiles nt0..nt0+7) into lds: 16-byte units, 64 a wave instruction,
 // issued by waves w0 .. w0 + nw - 1 of the workgroup (the others issue nothing).
 template <int K2>
@@ -46,7 +51,7 @@ __device__ __forceinline__ void issue_stage_waves(const uint32_t* __restrict__ T
         if (u < units) {
             const int r = u / UPR, w = (u - r * UPR) * 4;
             const uint32_t* src = T + ((size_t)(kt0 + r) * NTILES + nt0) * TW + w;
-            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, CPOL_NT);
         }
     }
 }
@@ -63,7 +68,7 @@ __device__ __forceinline__ void issue_stage(const uint32_t* __restrict__ T, int 
         if (u < units) {
             const int r = u / UPR, w = (u - r * UPR) * 4;
             const uint32_t* src = T + ((size_t)(kt0 + r) * NTILES + nt0) * TW + w;
-            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, CPOL_NT);
         }
     }
 }
@@ -81,7 +86,7 @@ __device__ __forceinline__ void issue_stage_rt(const uint32_t* __restrict__ T, i
         if (u < units) {
             const int r = u / UPR, w = (u - r * UPR) * 4;
             const uint32_t* src = T + ((size_t)(kt0 + r) * NTILES + nt0) * TW + w;
-            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void_ptr)src, (lds_void_ptr)(lds + u0 * 4), 16, 0, CPOL_NT);
         }
     }
 }
