@@ -678,7 +678,7 @@ __device__ __forceinline__ void grouped_body_staged(const GroupedArgs& a, const 
             const int u0 = wave * 64 + i * nthr;
             if (u0 < 2 * n * UPR && u0 + lane < 2 * n * UPR)
                 __builtin_amdgcn_global_load_lds((global_void_ptr)(Ts + t_off[i]), (lds_void_ptr)(tb + u0 * 4), 16, 0,
-                                                 0);
+                                                 CPOL_NT);
         }
         uint16_t* abuf = reinterpret_cast<uint16_t*>(buf + B_WORDS * 4);
 #pragma unroll
